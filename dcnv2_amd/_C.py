@@ -1,0 +1,216 @@
+"""Native operator module: the drop-in for the reference's ``Conv2d._C``.
+
+The reference builds ``Conv2d._C`` as a pybind11 extension exporting
+``dcn_v2_forward`` and ``dcn_v2_backward`` (reference ``ext.cpp:15-18``,
+``name.h:15-36``).  Here the same two functions, with the same positional
+arguments and result order, bind the C ABI of ``lib/libdcnv2_amd.so``
+(``include/dcnv2_amd.h``) through ctypes.  Torch supplies only device memory
+(outputs and the scratch workspace come from its caching allocator, as the
+reference's ``at::zeros``/``at::empty`` do, ``com.cu:232-235, 766-774``) and
+the current stream; all arithmetic runs in the gfx950 kernels of the library.
+
+Extensions over the reference, all trailing and optional: ``dilation_h``,
+``dilation_w`` and ``deformable_groups`` (the reference's Python module accepts
+them but never forwards them, ``dcn_v2_mm.py:67-68, 94-102``); fp16/bf16 as
+well as fp32 tensors; ``mask`` and ``bias`` may be ``None``.
+
+Errors: any invalid device, dtype, shape or launch failure raises
+``RuntimeError``, as the reference's ``AT_ASSERTM`` checks do
+(``com.cu:209-213, 743-747, 760-761``).  There is no CPU fallback: without the
+built library every call raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch
+
+_LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libdcnv2_amd.so")
+_DTYPES = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
+_lib = None
+_lib_lock = threading.Lock()
+
+
+class Desc(ctypes.Structure):
+    """``dcn2_desc`` of ``include/dcnv2_amd.h``."""
+    _fields_ = [(name, ctypes.c_int32) for name in (
+        "batch", "in_channels", "height", "width", "out_channels", "kernel_h", "kernel_w",
+        "stride_h", "stride_w", "pad_h", "pad_w", "dilation_h", "dilation_w",
+        "deformable_groups", "dtype")]
+
+
+def library_path() -> str:
+    return _LIB_PATH
+
+
+def lib() -> ctypes.CDLL:
+    """Loads libdcnv2_amd.so once; raises RuntimeError if it was never built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lib_lock:
+        if _lib is None:
+            if not os.path.exists(_LIB_PATH):
+                raise RuntimeError(
+                    f"dcnv2_amd: native library {_LIB_PATH} is not built; "
+                    "run `python -m dcnv2_amd.build` (or __graft_entry__.build())")
+            L = ctypes.CDLL(_LIB_PATH)
+            vp, sz, dp = ctypes.c_void_p, ctypes.c_size_t, ctypes.POINTER(Desc)
+            L.dcn2_output_shape.argtypes = [dp, ctypes.POINTER(ctypes.c_int32),
+                                            ctypes.POINTER(ctypes.c_int32)]
+            L.dcn2_output_shape.restype = ctypes.c_int
+            L.dcn2_forward_workspace_bytes.argtypes = [dp]
+            L.dcn2_forward_workspace_bytes.restype = sz
+            L.dcn2_backward_workspace_bytes.argtypes = [dp]
+            L.dcn2_backward_workspace_bytes.restype = sz
+            L.dcn2_forward.argtypes = [dp] + [vp] * 7 + [sz, vp]
+            L.dcn2_forward.restype = ctypes.c_int
+            L.dcn2_backward.argtypes = [dp] + [vp] * 11 + [sz, vp]
+            L.dcn2_backward.restype = ctypes.c_int
+            L.dcn2_last_error.argtypes = []
+            L.dcn2_last_error.restype = ctypes.c_char_p
+            L.dcn2_version.argtypes = []
+            L.dcn2_version.restype = ctypes.c_char_p
+            _lib = L
+    return _lib
+
+
+def _err(prefix: str) -> RuntimeError:
+    return RuntimeError(f"{prefix}: {lib().dcn2_last_error().decode()}")
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def make_desc(input, weight, stride_h, stride_w, pad_h, pad_w, dilation_h, dilation_w,
+              deformable_groups) -> Desc:
+    B, C, H, W = (int(v) for v in input.shape)
+    Cout, _, kh, kw = (int(v) for v in weight.shape)
+    return Desc(B, C, H, W, Cout, kh, kw, int(stride_h), int(stride_w), int(pad_h), int(pad_w),
+                int(dilation_h), int(dilation_w), int(deformable_groups), _DTYPES[input.dtype])
+
+
+def _validate(name, input, weight, mask, offset, bias, extra=()):
+    tensors = {"input": input, "weight": weight, "offset": offset}
+    if mask is not None:
+        tensors["mask"] = mask
+    if bias is not None:
+        tensors["bias"] = bias
+    tensors.update(dict(extra))
+    for k, t in tensors.items():
+        if not isinstance(t, torch.Tensor):
+            raise RuntimeError(f"{name}: {k} must be a tensor")
+        if not t.is_cuda:  # reference com.cu:209-213
+            raise RuntimeError(f"{name}: {k} must be a GPU (HIP) tensor")
+    dev = input.device
+    for k, t in tensors.items():
+        if t.device != dev:
+            raise RuntimeError(f"{name}: {k} is on {t.device}, input on {dev}")
+        if t.dtype != input.dtype:
+            raise RuntimeError(f"{name}: {k} has dtype {t.dtype}, input has {input.dtype}")
+    if input.dtype not in _DTYPES:
+        raise RuntimeError(f"{name}: unsupported dtype {input.dtype} "
+                           "(float32, float16 and bfloat16 are supported)")
+    if input.dim() != 4 or weight.dim() != 4 or offset.dim() != 4:
+        raise RuntimeError(f"{name}: input, weight and offset must be 4-D")
+    if weight.shape[1] != input.shape[1]:  # reference com.cu:760-761
+        raise RuntimeError(f"{name}: input has {input.shape[1]} channels, "
+                           f"weight expects {weight.shape[1]}")
+    if bias is not None and tuple(bias.shape) != (weight.shape[0],):
+        raise RuntimeError(f"{name}: bias shape {tuple(bias.shape)} != ({weight.shape[0]},)")
+
+
+def _geometry(name, desc, input, mask, offset):
+    ho, wo = ctypes.c_int32(), ctypes.c_int32()
+    if lib().dcn2_output_shape(ctypes.byref(desc), ctypes.byref(ho), ctypes.byref(wo)) != 0:
+        raise _err(name)
+    B, G, KK = desc.batch, desc.deformable_groups, desc.kernel_h * desc.kernel_w
+    want_off = (B, 2 * G * KK, ho.value, wo.value)
+    if tuple(offset.shape) != want_off:
+        raise RuntimeError(f"{name}: offset shape {tuple(offset.shape)} != {want_off}")
+    if mask is not None and tuple(mask.shape) != (B, G * KK, ho.value, wo.value):
+        raise RuntimeError(f"{name}: mask shape {tuple(mask.shape)} != "
+                           f"{(B, G * KK, ho.value, wo.value)}")
+    return ho.value, wo.value
+
+
+def _workspace(nbytes, device):
+    # 256 extra bytes so the start can be aligned to 256 whatever the allocator returns
+    buf = torch.empty(int(nbytes) + 256, dtype=torch.uint8, device=device)
+    addr = buf.data_ptr()
+    aligned = (addr + 255) & ~255
+    return buf, aligned, int(nbytes)
+
+
+def dcn_v2_forward(input, weight, mask, offset, bias, stride_h, stride_w, pad_h, pad_w,
+                   dilation_h=1, dilation_w=1, deformable_groups=1):
+    """Reference ``MyDCN_forward`` (``com.cu:198-272``): returns the output
+    ``[B, Cout, Ho, Wo]`` in the input dtype."""
+    name = "dcn_v2_forward"
+    _validate(name, input, weight, mask, offset, bias)
+    input, weight, offset = input.contiguous(), weight.contiguous(), offset.contiguous()
+    mask = mask.contiguous() if mask is not None else None
+    bias = bias.contiguous() if bias is not None else None
+    desc = make_desc(input, weight, stride_h, stride_w, pad_h, pad_w, dilation_h, dilation_w,
+                     deformable_groups)
+    ho, wo = _geometry(name, desc, input, mask, offset)
+    L = lib()
+    out = torch.empty((desc.batch, desc.out_channels, ho, wo), dtype=input.dtype,
+                      device=input.device)
+    with torch.cuda.device(input.device):
+        ws_buf, ws, ws_bytes = _workspace(L.dcn2_forward_workspace_bytes(ctypes.byref(desc)),
+                                          input.device)
+        stream = torch.cuda.current_stream(input.device).cuda_stream
+        rc = L.dcn2_forward(ctypes.byref(desc), _ptr(input), _ptr(weight), _ptr(mask),
+                            _ptr(offset), _ptr(bias), _ptr(out), ctypes.c_void_p(ws), ws_bytes,
+                            ctypes.c_void_p(stream))
+    if rc != 0:
+        raise _err(name)
+    del ws_buf  # returned to torch's caching allocator in stream order
+    return out
+
+
+def dcn_v2_backward(input, weight, mask, offset, bias, grad_output, stride_h, stride_w, pad_h,
+                    pad_w, dilation_h=1, dilation_w=1, deformable_groups=1):
+    """Reference ``MyDCN_backward`` (``com.cu:733-848``): returns
+    ``[grad_input, grad_offset, grad_mask, grad_weight, grad_bias]`` (the order
+    of ``com.cu:845-847``); ``grad_mask``/``grad_bias`` are ``None`` when
+    ``mask``/``bias`` is."""
+    name = "dcn_v2_backward"
+    _validate(name, input, weight, mask, offset, bias, extra=[("grad_output", grad_output)])
+    input, weight, offset = input.contiguous(), weight.contiguous(), offset.contiguous()
+    mask = mask.contiguous() if mask is not None else None
+    grad_output = grad_output.contiguous()
+    desc = make_desc(input, weight, stride_h, stride_w, pad_h, pad_w, dilation_h, dilation_w,
+                     deformable_groups)
+    ho, wo = _geometry(name, desc, input, mask, offset)
+    if tuple(grad_output.shape) != (desc.batch, desc.out_channels, ho, wo):
+        raise RuntimeError(f"{name}: grad_output shape {tuple(grad_output.shape)} != "
+                           f"{(desc.batch, desc.out_channels, ho, wo)}")
+    L = lib()
+    grad_input = torch.empty_like(input)
+    grad_offset = torch.empty_like(offset)
+    grad_mask = torch.empty_like(mask) if mask is not None else None
+    grad_weight = torch.empty_like(weight)
+    grad_bias = torch.empty((desc.out_channels,), dtype=input.dtype, device=input.device) \
+        if bias is not None else None
+    with torch.cuda.device(input.device):
+        ws_buf, ws, ws_bytes = _workspace(L.dcn2_backward_workspace_bytes(ctypes.byref(desc)),
+                                          input.device)
+        stream = torch.cuda.current_stream(input.device).cuda_stream
+        rc = L.dcn2_backward(ctypes.byref(desc), _ptr(input), _ptr(weight), _ptr(mask),
+                             _ptr(offset), _ptr(grad_output), _ptr(grad_input),
+                             _ptr(grad_offset), _ptr(grad_mask), _ptr(grad_weight),
+                             _ptr(grad_bias), ctypes.c_void_p(ws), ws_bytes,
+                             ctypes.c_void_p(stream))
+    if rc != 0:
+        raise _err(name)
+    del ws_buf
+    return [grad_input, grad_offset, grad_mask, grad_weight, grad_bias]
+
+
+def version() -> str:
+    return lib().dcn2_version().decode()

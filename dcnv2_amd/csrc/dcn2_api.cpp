@@ -1,0 +1,213 @@
+// extern "C" entry points of libdcnv2_amd.so (declared in include/dcnv2_amd.h).
+//
+// Host-side work of the reference's MyDCN_forward / MyDCN_backward
+// (com.cu:198-272, 733-848): argument validation, output-shape math, scratch
+// carving and the launch sequence.  Scratch comes from the caller's workspace
+// (the Python layer allocates it from torch's caching allocator), never from
+// hipMalloc, and every launch goes to the caller's stream.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "../../include/dcnv2_amd.h"
+#include "dcn2_common.h"
+#include "dcn2_kernels.h"
+
+namespace dcn2 {
+
+static thread_local std::string g_last_error;
+
+static int fail(int code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+// Validates `d` and derives the packing geometry.  Returns DCN2_OK or an error.
+static int make_geo(const dcn2_desc *d, Geo &g) {
+    if (!d) return fail(DCN2_EINVAL, "dcn2: null descriptor");
+    g.B = d->batch;
+    g.C = d->in_channels;
+    g.H = d->height;
+    g.W = d->width;
+    g.Cout = d->out_channels;
+    g.kh = d->kernel_h;
+    g.kw = d->kernel_w;
+    g.sh = d->stride_h;
+    g.sw = d->stride_w;
+    g.ph = d->pad_h;
+    g.pw = d->pad_w;
+    g.dh = d->dilation_h;
+    g.dw = d->dilation_w;
+    g.G = d->deformable_groups;
+    g.dtype = d->dtype;
+    if (g.dtype != DCN2_F32 && g.dtype != DCN2_F16 && g.dtype != DCN2_BF16)
+        return fail(DCN2_EINVAL, "dcn2: unsupported dtype code %d", g.dtype);
+    if (g.B < 0 || g.C <= 0 || g.H <= 0 || g.W <= 0 || g.Cout <= 0)
+        return fail(DCN2_EINVAL, "dcn2: invalid shape B=%d C=%d H=%d W=%d Cout=%d", g.B, g.C,
+                    g.H, g.W, g.Cout);
+    if (g.kh <= 0 || g.kw <= 0 || g.sh <= 0 || g.sw <= 0 || g.dh <= 0 || g.dw <= 0 ||
+        g.ph < 0 || g.pw < 0)
+        return fail(DCN2_EINVAL,
+                    "dcn2: invalid kernel/stride/padding/dilation (%d,%d)/(%d,%d)/(%d,%d)/(%d,%d)",
+                    g.kh, g.kw, g.sh, g.sw, g.ph, g.pw, g.dh, g.dw);
+    if (g.G <= 0 || g.C % g.G != 0)
+        return fail(DCN2_EINVAL, "dcn2: in_channels %d not divisible by deformable_groups %d",
+                    g.C, g.G);
+    g.Ho = (g.H + 2 * g.ph - (g.dh * (g.kh - 1) + 1)) / g.sh + 1;
+    g.Wo = (g.W + 2 * g.pw - (g.dw * (g.kw - 1) + 1)) / g.sw + 1;
+    if (g.H + 2 * g.ph < g.dh * (g.kh - 1) + 1 || g.W + 2 * g.pw < g.dw * (g.kw - 1) + 1 ||
+        g.Ho <= 0 || g.Wo <= 0)
+        return fail(DCN2_EINVAL, "dcn2: empty output (%d x %d)", g.Ho, g.Wo);
+    g.esz = g.dtype == DCN2_F32 ? 4 : 2;
+    g.KC = g.dtype == DCN2_F32 ? 32 : 64;
+    g.Cg = g.C / g.G;
+    g.Cgp = round_up(g.Cg, g.KC);
+    g.cs = g.G * g.Cgp;
+    g.N = g.Ho * g.Wo;
+    g.KK = g.kh * g.kw;
+    g.BM = g.Cout > 128 ? 256 : 128;
+    g.Mp = round_up(g.Cout, g.BM);
+    // All in-kernel offsets within one image (and of the packed weights) are
+    // 32-bit; the per-image base is 64-bit.
+    const long long lim = 0x7fffffffLL;
+    const long long Kp = (long long)g.KK * g.cs;
+    if ((long long)g.H * g.W * g.cs >= lim || (long long)g.C * g.H * g.W >= lim ||
+        (long long)g.Ho * g.Wo * g.Cout >= lim || (long long)g.Ho * g.Wo * 2 * g.G * g.KK >= lim ||
+        Kp * g.Mp >= lim || (long long)g.Ho * g.Wo >= lim || g.B > 65535)
+        return fail(DCN2_ERANGE, "dcn2: problem exceeds the 32-bit per-image index range");
+    g.Kp = (int)Kp;
+    return DCN2_OK;
+}
+
+FwdWorkspace fwd_workspace(const Geo &g) {
+    FwdWorkspace w;
+    size_t o = 0;
+    w.xt = o;
+    o += align256((size_t)g.B * g.H * g.W * g.cs * g.esz);
+    w.wp = o;
+    o += align256((size_t)g.Mp * g.Kp * g.esz);
+    w.total = o;
+    return w;
+}
+
+BwdWorkspace bwd_workspace(const Geo &g) {
+    BwdWorkspace w;
+    size_t o = 0;
+    w.xt = o;
+    o += align256((size_t)g.B * g.H * g.W * g.cs * g.esz);
+    w.wt = o;
+    o += align256((size_t)g.Mp * g.Kp * g.esz);
+    w.gi_acc = o;
+    o += align256((size_t)g.B * g.H * g.W * g.cs * sizeof(float));
+    w.gw_acc = o;
+    o += align256((size_t)g.Mp * g.Kp * sizeof(float));
+    w.gb_acc = o;
+    o += align256((size_t)g.Mp * sizeof(float));
+    w.total = o;
+    return w;
+}
+
+static int check_launch(hipError_t e, const char *what) {
+    if (e != hipSuccess)
+        return fail(DCN2_ELAUNCH, "dcn2: %s launch failed: %s", what, hipGetErrorString(e));
+    return DCN2_OK;
+}
+
+}  // namespace dcn2
+
+using namespace dcn2;
+
+extern "C" {
+
+int dcn2_output_shape(const dcn2_desc *d, int32_t *out_h, int32_t *out_w) {
+    Geo g;
+    const int rc = make_geo(d, g);
+    if (rc) return rc;
+    if (out_h) *out_h = g.Ho;
+    if (out_w) *out_w = g.Wo;
+    return DCN2_OK;
+}
+
+size_t dcn2_forward_workspace_bytes(const dcn2_desc *d) {
+    Geo g;
+    if (make_geo(d, g)) return 0;
+    return fwd_workspace(g).total;
+}
+
+size_t dcn2_backward_workspace_bytes(const dcn2_desc *d) {
+    Geo g;
+    if (make_geo(d, g)) return 0;
+    return bwd_workspace(g).total;
+}
+
+int dcn2_forward(const dcn2_desc *d, const void *input, const void *weight, const void *mask,
+                 const void *offset, const void *bias, void *output, void *workspace,
+                 size_t workspace_bytes, void *stream) {
+    Geo g;
+    int rc = make_geo(d, g);
+    if (rc) return rc;
+    if (g.B > 0 && (!input || !offset || !output))
+        return fail(DCN2_EINVAL, "dcn2_forward: null input/offset/output pointer");
+    if (!weight) return fail(DCN2_EINVAL, "dcn2_forward: null weight pointer");
+    const FwdWorkspace ws = fwd_workspace(g);
+    if (!workspace || workspace_bytes < ws.total || ((uintptr_t)workspace & 255))
+        return fail(DCN2_EWORKSPACE,
+                    "dcn2_forward: workspace needs %zu bytes at 256-byte alignment (got %zu)",
+                    ws.total, workspace_bytes);
+    if (g.B == 0) return DCN2_OK;
+    hipStream_t s = (hipStream_t)stream;
+    char *base = (char *)workspace;
+    void *xt = base + ws.xt, *wp = base + ws.wp;
+    if ((rc = check_launch(launch_pack_input(g, input, xt, s), "pack_input"))) return rc;
+    if ((rc = check_launch(launch_pack_weight(g, weight, wp, false, s), "pack_weight"))) return rc;
+    return check_launch(launch_forward(g, xt, wp, offset, mask, bias, output, s), "forward");
+}
+
+int dcn2_backward(const dcn2_desc *d, const void *input, const void *weight, const void *mask,
+                  const void *offset, const void *grad_output, void *grad_input,
+                  void *grad_offset, void *grad_mask, void *grad_weight, void *grad_bias,
+                  void *workspace, size_t workspace_bytes, void *stream) {
+    Geo g;
+    int rc = make_geo(d, g);
+    if (rc) return rc;
+    if (!weight || !grad_weight)
+        return fail(DCN2_EINVAL, "dcn2_backward: null weight/grad_weight pointer");
+    if (g.B > 0 && (!input || !offset || !grad_output || !grad_input || !grad_offset))
+        return fail(DCN2_EINVAL, "dcn2_backward: null input/offset/grad pointer");
+    if ((mask == nullptr) != (grad_mask == nullptr))
+        return fail(DCN2_EINVAL, "dcn2_backward: grad_mask must be given exactly when mask is");
+    const BwdWorkspace ws = bwd_workspace(g);
+    if (!workspace || workspace_bytes < ws.total || ((uintptr_t)workspace & 255))
+        return fail(DCN2_EWORKSPACE,
+                    "dcn2_backward: workspace needs %zu bytes at 256-byte alignment (got %zu)",
+                    ws.total, workspace_bytes);
+    hipStream_t s = (hipStream_t)stream;
+    char *base = (char *)workspace;
+    void *xt = base + ws.xt, *wt = base + ws.wt;
+    if (g.B > 0) {
+        if ((rc = check_launch(launch_pack_input(g, input, xt, s), "pack_input"))) return rc;
+    }
+    if ((rc = check_launch(launch_pack_weight(g, weight, wt, true, s), "pack_weight_t")))
+        return rc;
+    return check_launch(launch_backward(g, xt, wt, offset, mask, grad_output,
+                                        grad_input, grad_offset, grad_mask, grad_weight,
+                                        grad_bias, (float *)(base + ws.gi_acc),
+                                        (float *)(base + ws.gw_acc), (float *)(base + ws.gb_acc),
+                                        s),
+                        "backward");
+}
+
+const char *dcn2_last_error(void) { return g_last_error.c_str(); }
+
+const char *dcn2_version(void) { return "dcnv2_amd 1 gfx950"; }
+
+}  // extern "C"

@@ -1,0 +1,593 @@
+// DCNv2 backward for gfx950.
+//
+// Reference (com.cu:733-848) loops over the batch on the host and, per image,
+// runs a cuBLAS GEMM for the column gradient (com.cu:789-793), the coordinate
+// kernel (com.cu:431-501), the col2im atomic scatter (com.cu:553-609), a
+// second im2col (com.cu:637-706) and two more cuBLAS calls for grad_weight and
+// grad_bias (com.cu:829-835).  Here the whole batch is one launch per stage:
+//
+//  colgrad kernel  (grid: pixel tiles x batch)
+//     cg[k][n] = sum_m Wt[k][m] * gO[m][n]            MFMA, kept on chip (LDS)
+//     grad_mask / grad_offset  via the corner sums    S_q = sum_c cg_c * x_c(corner q)
+//         grad_mask = sum_q w_q S_q,  grad_off_y = mask * sum_q dw_q/dy S_q, ...
+//       (4 FMAs per channel instead of re-evaluating bilinear and both
+//        coordinate weights per channel as com.cu:486-492 does)
+//     grad_input  scatter with fp32 atomics, lanes = channels so one wave
+//       instruction updates a contiguous channel run of one corner.
+//  gradw kernel    (grid: pixel-tile splits x K chunks x M chunks)
+//     gW[m][k] += sum_n gO[m][n] * col[k][n]           MFMA over re-sampled
+//       columns in LDS; partial tiles are added to an fp32 accumulator.
+//     grad_bias from the same gO fragments.
+//  finalize kernels: fp32 accumulators -> caller dtype and layout.
+#include <algorithm>
+
+#include "dcn2_common.h"
+#include "dcn2_sampler.h"
+#include "dcn2_kernels.h"
+#include "../../include/dcnv2_amd.h"
+
+namespace dcn2 {
+
+struct BwdParams {
+    const void *xt, *wt, *offset, *mask, *gout;
+    void *goff, *gmask;
+    float *gi_acc, *gw_acc, *gb_acc;
+    int B, H, W, Cout, kh, kw, sh, sw, ph, pw, dh, dw, G, Cg, Cgp, Ho, Wo, Kp, Mp;
+    int tiles_per_img, splits;
+    int go_vec;  // grad_output rows can be read with 16-byte loads (N % 8 == 0, aligned base)
+};
+
+// Per-pixel sampling record written by the reduction phase for the scatter.
+struct Desc {
+    int off[4];
+    float w[4];  // masked bilinear weight of each corner, 0 outside the image
+};
+
+template <typename T, int KPL> struct FragSet;
+template <typename T> struct FragSet<T, 1> {
+    template <typename F> static __device__ __forceinline__ void set(F &f, int, T v) { f = v; }
+};
+template <typename T> struct FragSet<T, 8> {
+    template <typename F> static __device__ __forceinline__ void set(F &f, int e, T v) { f[e] = v; }
+};
+
+__device__ __forceinline__ float shfl_xor_f(float v, int mask) {
+    return __shfl_xor(v, mask, 64);
+}
+
+// ---------------------------------------------------------------------------
+// Column-gradient kernel: grad_offset, grad_mask and grad_input.
+// 512 threads; BN = 128 output pixels of one image per block.
+template <typename T, int MCH>
+__global__ __launch_bounds__(512) void dcn2_colgrad_kernel(const BwdParams p) {
+    using M = Mma<T>;
+    using frag = typename M::frag;
+    constexpr int KC = M::KC, KPL = M::KPL, KSTEP = M::KSTEP;
+    constexpr int BN = 128;
+    constexpr int NB = (KC / 32) * (BN / 32);  // 32x32 blocks of one chunk (8 or 4)
+    constexpr int WPB = 8 / NB;                // waves sharing one block's M reduction
+    constexpr int MPW = MCH / WPB;             // M range of one wave per M chunk
+    constexpr int NMS = MPW / KSTEP;           // MFMA steps per wave per M chunk
+    constexpr int LDC = KC + 4;                // pitch (floats) of the column gradient
+    constexpr int QPP = 512 / BN;              // lanes per pixel in the reduction phase
+    constexpr int CPL = KC / QPP;              // channels per lane there
+    constexpr int PPW = 64 / KC;               // pixels per wave step in the scatter
+    constexpr int E = Unpack<T>::E;
+    static_assert(CPL * sizeof(T) == 32, "reduction lane covers 32 bytes per corner");
+
+    __shared__ __attribute__((aligned(16))) float sCG[WPB][BN][LDC];
+    __shared__ Desc sD[BN];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int blk = wave % NB, wr = wave / NB;
+    const int kb = blk / (BN / 32), nb = blk - kb * (BN / 32);
+    const int b = blockIdx.y, n0 = blockIdx.x * BN;
+    const int N = p.Ho * p.Wo, KK = p.kh * p.kw, cs = p.G * p.Cgp;
+    const int cpg = p.Cgp / KC, nch = KK * p.G * cpg, nmc = p.Mp / MCH;
+
+    const T *__restrict__ xt = (const T *)p.xt + (size_t)b * p.H * p.W * cs;
+    const T *__restrict__ offs = (const T *)p.offset + (size_t)b * p.G * KK * 2 * N;
+    const T *__restrict__ msk = p.mask ? (const T *)p.mask + (size_t)b * p.G * KK * N : nullptr;
+    const T *__restrict__ go = (const T *)p.gout + (size_t)b * p.Cout * N;
+    const T *__restrict__ wt = (const T *)p.wt;
+    T *__restrict__ goff = (T *)p.goff + (size_t)b * p.G * KK * 2 * N;
+    T *__restrict__ gmask = p.gmask ? (T *)p.gmask + (size_t)b * p.G * KK * N : nullptr;
+    float *__restrict__ gi = p.gi_acc + (size_t)b * p.H * p.W * cs;
+
+    // gO fragments (MFMA B operand, [m][n]): n = this wave's 32-pixel block.
+    frag gfr[NMS];
+    auto load_go = [&](int mc) {
+        const int n = n0 + nb * 32 + (lane & 31);
+#pragma unroll
+        for (int s = 0; s < NMS; ++s) {
+#pragma unroll
+            for (int e = 0; e < KPL; ++e) {
+                const int m = mc * MCH + wr * MPW + s * KSTEP + (lane >> 5) * KPL + e;
+                const T v = (n < N && m < p.Cout) ? go[(size_t)m * N + n] : (T)0.0f;
+                FragSet<T, KPL>::set(gfr[s], e, v);
+            }
+        }
+    };
+    if (nmc == 1) load_go(0);
+
+    // Reduction-phase identity: pixel pr, channel quarter lq.
+    const int pr = tid / QPP, lq = tid - pr * QPP;
+    const int nr = n0 + pr;
+    int oyr = 0, oxr = 0;
+    if (nr < N) {
+        oyr = nr / p.Wo;
+        oxr = nr - oyr * p.Wo;
+    }
+    float racc[3] = {0.0f, 0.0f, 0.0f};  // grad_mask, grad_off_y, grad_off_x (lq == 0)
+
+    for (int ch = 0; ch < nch; ++ch) {
+        const int tg = ch / cpg, cc = ch - tg * cpg;
+        const int tap = tg / p.G, g = tg - tap * p.G;
+        const int ki = tap / p.kw, kj = tap - ki * p.kw;
+
+        // Sampling position of (pr, tap, g) and the corner gathers of this
+        // lane's channels; issued before the MFMA so their latency overlaps it.
+        SamplePos sp;
+        float mv = 0.0f;
+        bool live = nr < N;
+        if (live) {
+            const size_t ob = ((size_t)g * KK + tap) * 2 * N + nr;
+            const float y = (float)(oyr * p.sh - p.ph + ki * p.dh) + to_f32(offs[ob]);
+            const float x = (float)(oxr * p.sw - p.pw + kj * p.dw) + to_f32(offs[ob + N]);
+            mv = msk ? to_f32(msk[((size_t)g * KK + tap) * N + nr]) : 1.0f;
+            sp = sample_pos(y, x, p.H, p.W);
+        } else {
+            sp = sample_pos(-2.0f, -2.0f, p.H, p.W);
+        }
+        const Corners cr = make_corners(sp, mv, p.W, cs);
+        uint4 raw[4][2];
+        {
+            const int cbase = g * p.Cgp + cc * KC + lq * CPL;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const uint4 *src = reinterpret_cast<const uint4 *>(xt + cr.off[q] + cbase);
+                raw[q][0] = src[0];
+                raw[q][1] = src[1];
+            }
+        }
+
+        // Column gradient of this chunk: block (kb, nb), M share wr.
+        f32x16 acc;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+        const T *wrow = wt + (size_t)(ch * KC + kb * 32 + (lane & 31)) * p.Mp + wr * MPW +
+                        (lane >> 5) * KPL;
+        for (int mc = 0; mc < nmc; ++mc) {
+            if (nmc > 1) load_go(mc);
+#pragma unroll
+            for (int s = 0; s < NMS; ++s) {
+                const frag a = *reinterpret_cast<const frag *>(wrow + mc * MCH + s * KSTEP);
+                acc = M::mma(a, gfr[s], acc);
+            }
+        }
+        {
+            const int nl = nb * 32 + (lane & 31);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int kl = kb * 32 + 8 * j + 4 * (lane >> 5);
+                *reinterpret_cast<f32x4 *>(&sCG[wr][nl][kl]) =
+                    f32x4{acc[4 * j], acc[4 * j + 1], acc[4 * j + 2], acc[4 * j + 3]};
+            }
+        }
+        if (lq == 0) {
+            Desc d;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                d.off[q] = cr.off[q];
+                d.w[q] = cr.w[q];
+            }
+            sD[pr] = d;
+        }
+        __syncthreads();
+
+        // grad_mask / grad_offset: corner sums over this lane's channels.
+        {
+            float cgv[CPL];
+#pragma unroll
+            for (int c4 = 0; c4 < CPL / 4; ++c4) {
+                f32x4 v = *reinterpret_cast<const f32x4 *>(&sCG[0][pr][lq * CPL + 4 * c4]);
+#pragma unroll
+                for (int w2 = 1; w2 < WPB; ++w2)
+                    v += *reinterpret_cast<const f32x4 *>(&sCG[w2][pr][lq * CPL + 4 * c4]);
+                cgv[4 * c4] = v[0];
+                cgv[4 * c4 + 1] = v[1];
+                cgv[4 * c4 + 2] = v[2];
+                cgv[4 * c4 + 3] = v[3];
+            }
+            float S[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                float s = 0.0f;
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    float v[E];
+                    Unpack<T>::run(raw[q][u], v);
+#pragma unroll
+                    for (int e = 0; e < E; ++e) s = fmaf(cgv[u * E + e], v[e], s);
+                }
+                S[q] = s;
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+#pragma unroll
+                for (int x = 1; x < QPP; x <<= 1) S[q] += shfl_xor_f(S[q], x);
+            }
+            if (lq == 0) {
+                const bool v00 = sp.vy0 && sp.vx0, v01 = sp.vy0 && sp.vx1;
+                const bool v10 = sp.vy1 && sp.vx0, v11 = sp.vy1 && sp.vx1;
+                const float S0 = v00 ? S[0] : 0.0f, S1 = v01 ? S[1] : 0.0f;
+                const float S2 = v10 ? S[2] : 0.0f, S3 = v11 ? S[3] : 0.0f;
+                const float ly = sp.ly, lx = sp.lx, hy = 1.0f - ly, hx = 1.0f - lx;
+                racc[0] += hy * hx * S0 + hy * lx * S1 + ly * hx * S2 + ly * lx * S3;
+                racc[1] += mv * (hx * (S2 - S0) + lx * (S3 - S1));
+                racc[2] += mv * (hy * (S1 - S0) + ly * (S3 - S2));
+                if (cc == cpg - 1) {
+                    if (live) {
+                        const size_t ob = ((size_t)g * KK + tap) * 2 * N + nr;
+                        goff[ob] = from_f32<T>(racc[1]);
+                        goff[ob + N] = from_f32<T>(racc[2]);
+                        if (gmask) gmask[((size_t)g * KK + tap) * N + nr] = from_f32<T>(racc[0]);
+                    }
+                    racc[0] = racc[1] = racc[2] = 0.0f;
+                }
+            }
+        }
+
+        // grad_input scatter: lane = channel, one corner run per instruction.
+        {
+            const int c = lane % KC, sub = lane / KC;
+            const bool cvalid = cc * KC + c < p.Cg;
+            float *gib = gi + g * p.Cgp + cc * KC + c;
+            for (int it = 0; it < BN / (8 * PPW); ++it) {
+                const int pl = (it * 8 + wave) * PPW + sub;
+                if (n0 + pl >= N || !cvalid) continue;
+                float v = sCG[0][pl][c];
+#pragma unroll
+                for (int w2 = 1; w2 < WPB; ++w2) v += sCG[w2][pl][c];
+                const Desc d = sD[pl];
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    if (d.w[q] != 0.0f) unsafeAtomicAdd(gib + d.off[q], v * d.w[q]);
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// ---------------------------------------------------------------------------
+// grad_weight kernel.  Block = one K chunk (blockIdx.y) x 32*MB output
+// channels (blockIdx.z) x a strided subset of the pixel tiles (blockIdx.x).
+// D[m][k] = sum_n gO[m][n] * col[k][n]; A = gO straight from global memory
+// (rows are pixel-contiguous), B = re-sampled columns in LDS.
+// 2-byte types keep the LDS stage as [k][n] with the 16-byte blocks of each
+// row XOR-swizzled by h(k) = ((k & 15) ^ (k >> 3)) & 15 so that both the
+// sampler's 2-byte stores and the MFMA's 16-byte reads are bank-conflict free.
+template <typename T> struct GwLayout;
+template <> struct GwLayout<float> {
+    static constexpr bool kMajor = false;
+};
+template <> struct GwLayout<f16> {
+    static constexpr bool kMajor = true;
+};
+template <> struct GwLayout<bf16> {
+    static constexpr bool kMajor = true;
+};
+
+__device__ __forceinline__ int gw_swz(int k) { return ((k & 15) ^ (k >> 3)) & 15; }
+
+template <typename T, int MB>
+__global__ __launch_bounds__(512) void dcn2_gradw_kernel(const BwdParams p) {
+    using M = Mma<T>;
+    using frag = typename M::frag;
+    constexpr int KC = M::KC, KPL = M::KPL, KSTEP = M::KSTEP;
+    constexpr int BN = 128, NKS = BN / KSTEP;
+    constexpr int KB = KC / 32;
+    constexpr int NBLK = MB * KB;
+    constexpr int BPW = NBLK >= 16 ? 2 : 1;  // blocks per wave
+    constexpr bool KMAJ = GwLayout<T>::kMajor;
+    constexpr int LDN = KMAJ ? BN : KC + 4;  // pitch of the LDS stage (elements)
+    constexpr int ROWS = KMAJ ? KC : BN;
+    constexpr int CPS = KC / 4;
+    static_assert(!KMAJ || BN == 128, "swizzle assumes 16 blocks of 8 per row");
+
+    __shared__ __attribute__((aligned(16))) T sC[2][ROWS][LDN];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    int mblk, kblk0;
+    bool active;
+    if constexpr (BPW == 2) {
+        mblk = wave;
+        kblk0 = 0;
+        active = true;
+    } else {
+        mblk = wave / KB;
+        kblk0 = wave - mblk * KB;
+        active = wave < NBLK;
+    }
+    const bool do_bias = p.gb_acc != nullptr && blockIdx.y == 0 && kblk0 == 0 && active;
+    const int ch = blockIdx.y, sp = blockIdx.x, S = p.splits;
+    const int mrow = blockIdx.z * 32 * MB + mblk * 32 + (lane & 31);
+    const int N = p.Ho * p.Wo, KK = p.kh * p.kw, cs = p.G * p.Cgp;
+    const int T_total = p.B * p.tiles_per_img;
+
+    SampleGeo sg;
+    sg.H = p.H; sg.W = p.W; sg.kh = p.kh; sg.kw = p.kw; sg.sh = p.sh; sg.sw = p.sw;
+    sg.ph = p.ph; sg.pw = p.pw; sg.dh = p.dh; sg.dw = p.dw; sg.G = p.G; sg.Cgp = p.Cgp;
+    sg.Wo = p.Wo; sg.N = N; sg.cs = cs; sg.KK = KK;
+    Sampler<T, 1> smp;
+
+    auto issue_tile = [&](int t) {
+        const int b = t / p.tiles_per_img, n0 = (t - b * p.tiles_per_img) * BN;
+        smp.bind(n0, sg, tid);
+        smp.issue(ch, sg, (const T *)p.xt + (size_t)b * p.H * p.W * cs,
+                  (const T *)p.offset + (size_t)b * p.G * KK * 2 * N,
+                  p.mask ? (const T *)p.mask + (size_t)b * p.G * KK * N : nullptr);
+    };
+    auto store_stage = [&](int buf) {
+        const int pl = tid >> 2;
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            float v[16 / sizeof(T)];
+            smp.blend(0, u, v);
+            if constexpr (KMAJ) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int k = smp.q[0] * CPS + u * 8 + e;
+                    sC[buf][k][((pl >> 3) ^ gw_swz(k)) * 8 + (pl & 7)] = (T)v[e];
+                }
+            } else {
+                *reinterpret_cast<uint4 *>(&sC[buf][pl][smp.q[0] * CPS + u * 4]) = pack16<T>(v);
+            }
+        }
+    };
+
+    f32x16 acc[BPW];
+#pragma unroll
+    for (int i = 0; i < BPW; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][r] = 0.0f;
+    float bsum = 0.0f;
+
+    const bool aligned = p.go_vec != 0;
+    auto load_a = [&](frag &a, int t, int ks) {
+        const int b = t / p.tiles_per_img, n0 = (t - b * p.tiles_per_img) * BN;
+        const int n = n0 + ks * KSTEP + (lane >> 5) * KPL;
+        const T *row = (const T *)p.gout + ((size_t)b * p.Cout + mrow) * N;
+        if (mrow < p.Cout && aligned && n + KPL <= N && KPL == 8) {
+            a = *reinterpret_cast<const frag *>(row + n);
+        } else {
+#pragma unroll
+            for (int e = 0; e < KPL; ++e) {
+                const T v = (mrow < p.Cout && n + e < N) ? row[n + e] : (T)0.0f;
+                FragSet<T, KPL>::set(a, e, v);
+            }
+        }
+    };
+
+    if (sp < T_total) {
+        issue_tile(sp);
+        store_stage(0);
+    }
+    __syncthreads();
+    int it = 0;
+    for (int t = sp; t < T_total; t += S, ++it) {
+        const int buf = it & 1;
+        const bool more = t + S < T_total;
+        if (more) issue_tile(t + S);
+        if (active) {
+#pragma unroll
+            for (int ks = 0; ks < NKS; ++ks) {
+                frag a;
+                load_a(a, t, ks);
+                if (do_bias) {
+                    if constexpr (KPL == 1) {
+                        bsum += to_f32(a);
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < KPL; ++e) bsum += to_f32(a[e]);
+                    }
+                }
+#pragma unroll
+                for (int i = 0; i < BPW; ++i) {
+                    const int k = (kblk0 + i) * 32 + (lane & 31);
+                    frag bf;
+                    if constexpr (KMAJ) {
+                        const int nblk = ks * 2 + (lane >> 5);
+                        bf = *reinterpret_cast<const frag *>(
+                            &sC[buf][k][(nblk ^ gw_swz(k)) * 8]);
+                    } else {
+                        bf = sC[buf][ks * KSTEP + (lane >> 5)][k];
+                    }
+                    acc[i] = M::mma(a, bf, acc[i]);
+                }
+            }
+        }
+        if (more) store_stage(buf ^ 1);
+        __syncthreads();
+    }
+
+    if (!active) return;
+#pragma unroll
+    for (int i = 0; i < BPW; ++i) {
+        const int k = ch * KC + (kblk0 + i) * 32 + (lane & 31);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int m = blockIdx.z * 32 * MB + mblk * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            if (m < p.Cout) unsafeAtomicAdd(p.gw_acc + (size_t)m * p.Kp + k, acc[i][r]);
+        }
+    }
+    if (do_bias) {
+        bsum += shfl_xor_f(bsum, 32);
+        if (lane < 32 && mrow < p.Cout) unsafeAtomicAdd(p.gb_acc + mrow, bsum);
+    }
+}
+
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void fill_zero_kernel(float4 *__restrict__ p, size_t n4) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (size_t)gridDim.x * 256)
+        p[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+}
+
+// gi_acc [B][HW][cs] fp32 -> grad_input [B][C][HW] T; 64 pixels x 32 padded
+// channels per block, transposed through LDS.
+template <typename T>
+__global__ __launch_bounds__(256) void finalize_gi_kernel(const float *__restrict__ acc,
+                                                          T *__restrict__ gi, int C, int HW,
+                                                          int Cg, int Cgp, int cs) {
+    __shared__ float tile[64][33];
+    const int px0 = blockIdx.x * 64, cp0 = blockIdx.y * 32, b = blockIdx.z;
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int pl = (tid >> 5) + 8 * i, cl = tid & 31;
+        const int px = px0 + pl;
+        tile[pl][cl] = px < HW ? acc[((size_t)b * HW + px) * cs + cp0 + cl] : 0.0f;
+    }
+    __syncthreads();
+    const int pl = tid & 63;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int cl = (tid >> 6) + 4 * i;
+        const int cp = cp0 + cl, g = cp / Cgp, ci = cp - g * Cgp;
+        const int px = px0 + pl;
+        if (ci < Cg && px < HW) gi[((size_t)b * C + g * Cg + ci) * HW + px] = (T)tile[pl][cl];
+    }
+}
+
+// gw_acc [Mp][Kp] (K order tap, group, channel) -> grad_weight [Cout][C][kh][kw];
+// gb_acc -> grad_bias.
+template <typename T>
+__global__ __launch_bounds__(256) void finalize_gw_kernel(const float *__restrict__ gwa,
+                                                          const float *__restrict__ gba,
+                                                          T *__restrict__ gw, T *__restrict__ gb,
+                                                          int Cout, int C, int KK, int Cg,
+                                                          int Cgp, int G, int Kp) {
+    const long idx = (long)blockIdx.x * 256 + threadIdx.x;
+    const long total = (long)Cout * C * KK;
+    if (idx < total) {
+        const int m = (int)(idx / ((long)C * KK));
+        const int r = (int)(idx - (long)m * C * KK);
+        const int c = r / KK, tap = r - c * KK;
+        const int g = c / Cg, ci = c - g * Cg;
+        gw[idx] = (T)gwa[(size_t)m * Kp + ((size_t)tap * G + g) * Cgp + ci];
+    }
+    if (gb && idx < Cout) gb[idx] = (T)gba[idx];
+}
+
+// ---------------------------------------------------------------------------
+template <typename T>
+static hipError_t backward_t(const Geo &g, const BwdParams &p0, void *grad_input,
+                             void *grad_weight, void *grad_bias, hipStream_t s) {
+    BwdParams p = p0;
+    hipError_t e;
+    // 1. zero the fp32 accumulators
+    {
+        const size_t n_gi = (size_t)g.B * g.H * g.W * g.cs;
+        const size_t n_gw = (size_t)g.Mp * g.Kp;
+        float *bufs[3] = {p.gi_acc, p.gw_acc, p.gb_acc};
+        const size_t counts[3] = {n_gi, n_gw, (size_t)g.Mp};
+        for (int i = 0; i < 3; ++i) {
+            const size_t n4 = (counts[i] + 3) / 4;
+            if (n4 == 0) continue;
+            const unsigned blocks = (unsigned)std::min<size_t>((n4 + 255) / 256, 4096);
+            fill_zero_kernel<<<blocks, 256, 0, s>>>((float4 *)bufs[i], n4);
+            if ((e = hipGetLastError()) != hipSuccess) return e;
+        }
+    }
+    if (g.B > 0) {
+        // 2. column gradient: grad_offset, grad_mask, grad_input accumulation
+        {
+            dim3 grid(p.tiles_per_img, g.B);
+            // fp32 keeps the 128-wide M chunk: 256 would hold 128 gO registers.
+            if (sizeof(T) == 2 && g.Mp % 256 == 0)
+                dcn2_colgrad_kernel<T, 256><<<grid, 512, 0, s>>>(p);
+            else
+                dcn2_colgrad_kernel<T, 128><<<grid, 512, 0, s>>>(p);
+            if ((e = hipGetLastError()) != hipSuccess) return e;
+        }
+        // 3. grad_weight / grad_bias
+        {
+            const int nch = g.Kp / g.KC;
+            const int mb = (g.Mp % 256 == 0) ? 8 : 4;
+            const int nmc = g.Mp / (32 * mb);
+            const int T_total = g.B * p.tiles_per_img;
+            int S = 1024 / (nch * nmc);
+            S = std::max(1, std::min(S, T_total));
+            p.splits = S;
+            dim3 grid(S, nch, nmc);
+            if (mb == 8)
+                dcn2_gradw_kernel<T, 8><<<grid, 512, 0, s>>>(p);
+            else
+                dcn2_gradw_kernel<T, 4><<<grid, 512, 0, s>>>(p);
+            if ((e = hipGetLastError()) != hipSuccess) return e;
+        }
+        // 4. grad_input to the caller's layout
+        {
+            const int HW = g.H * g.W;
+            dim3 grid(ceil_div(HW, 64), g.cs / 32, g.B);
+            finalize_gi_kernel<T><<<grid, 256, 0, s>>>(p.gi_acc, (T *)grad_input, g.C, HW, g.Cg,
+                                                       g.Cgp, g.cs);
+            if ((e = hipGetLastError()) != hipSuccess) return e;
+        }
+    }
+    // 5. grad_weight / grad_bias to the caller's layout
+    {
+        const long total = std::max<long>((long)g.Cout * g.C * g.KK, g.Cout);
+        finalize_gw_kernel<T><<<(unsigned)((total + 255) / 256), 256, 0, s>>>(
+            p.gw_acc, p.gb_acc, (T *)grad_weight, (T *)grad_bias, g.Cout, g.C, g.KK, g.Cg, g.Cgp,
+            g.G, g.Kp);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+hipError_t launch_backward(const Geo &g, const void *xt, const void *wt, const void *offset,
+                           const void *mask, const void *grad_out, void *grad_input,
+                           void *grad_offset, void *grad_mask, void *grad_weight, void *grad_bias,
+                           float *gi_acc, float *gw_acc, float *gb_acc, hipStream_t s) {
+    BwdParams p;
+    p.xt = xt;
+    p.wt = wt;
+    p.offset = offset;
+    p.mask = mask;
+    p.gout = grad_out;
+    p.goff = grad_offset;
+    p.gmask = grad_mask;
+    p.gi_acc = gi_acc;
+    p.gw_acc = gw_acc;
+    p.gb_acc = grad_bias ? gb_acc : nullptr;
+    p.B = g.B;
+    p.H = g.H;
+    p.W = g.W;
+    p.Cout = g.Cout;
+    p.kh = g.kh;
+    p.kw = g.kw;
+    p.sh = g.sh;
+    p.sw = g.sw;
+    p.ph = g.ph;
+    p.pw = g.pw;
+    p.dh = g.dh;
+    p.dw = g.dw;
+    p.G = g.G;
+    p.Cg = g.Cg;
+    p.Cgp = g.Cgp;
+    p.Ho = g.Ho;
+    p.Wo = g.Wo;
+    p.Kp = g.Kp;
+    p.Mp = g.Mp;
+    p.tiles_per_img = ceil_div(g.N, 128);
+    p.splits = 1;
+    p.go_vec = (g.N % 8 == 0) && (((uintptr_t)grad_out & 15) == 0);
+    switch (g.dtype) {
+    case DCN2_F16: return backward_t<f16>(g, p, grad_input, grad_weight, grad_bias, s);
+    case DCN2_BF16: return backward_t<bf16>(g, p, grad_input, grad_weight, grad_bias, s);
+    default: return backward_t<float>(g, p, grad_input, grad_weight, grad_bias, s);
+    }
+}
+
+}  // namespace dcn2

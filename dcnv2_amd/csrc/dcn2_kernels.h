@@ -1,0 +1,53 @@
+// Host-side launchers of the gfx950 kernels.  Each returns hipSuccess or the
+// launch error; none synchronises.  Geometry is validated by dcn2_api.cpp
+// before any launcher runs.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+
+namespace dcn2 {
+
+// Validated problem geometry plus the derived packing sizes.
+struct Geo {
+    int B, C, H, W, Cout, kh, kw, sh, sw, ph, pw, dh, dw, G;
+    int dtype;      // enum dcn2_dtype
+    int esz;        // element size in bytes
+    int Cg;         // channels per deformable group
+    int KC;         // channel chunk of one LDS stage (64 for f16/bf16, 32 for f32)
+    int Cgp;        // Cg rounded up to KC
+    int cs;         // channels-last pixel stride of xt: G*Cgp
+    int Ho, Wo, N;  // output spatial size, N = Ho*Wo
+    int KK;         // kh*kw
+    int Kp;         // packed GEMM K = KK*G*Cgp
+    int BM;         // forward block tile in M (128 or 256)
+    int Mp;         // Cout rounded up to BM
+};
+
+// Workspace carving shared by forward and backward (byte offsets).
+struct FwdWorkspace {
+    size_t xt, wp, total;
+};
+FwdWorkspace fwd_workspace(const Geo &g);
+
+struct BwdWorkspace {
+    size_t xt, wt, gi_acc, gw_acc, gb_acc, total;
+};
+BwdWorkspace bwd_workspace(const Geo &g);
+
+// dcn2_pack.hip
+hipError_t launch_pack_input(const Geo &g, const void *input, void *xt, hipStream_t s);
+hipError_t launch_pack_weight(const Geo &g, const void *weight, void *wp, bool transpose,
+                              hipStream_t s);
+
+// dcn2_forward.hip
+hipError_t launch_forward(const Geo &g, const void *xt, const void *wp, const void *offset,
+                          const void *mask, const void *bias, void *out, hipStream_t s);
+
+// dcn2_backward.hip
+hipError_t launch_backward(const Geo &g, const void *xt, const void *wt, const void *offset,
+                           const void *mask, const void *grad_out, void *grad_input,
+                           void *grad_offset, void *grad_mask, void *grad_weight, void *grad_bias,
+                           float *gi_acc, float *gw_acc, float *gb_acc, hipStream_t s);
+
+}  // namespace dcn2

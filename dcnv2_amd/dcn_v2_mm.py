@@ -1,0 +1,121 @@
+"""Python operator surface, drop-in for the reference's ``dcn_v2_mm.py``.
+
+Same names, positional order and return order as the reference:
+
+* ``_DCNv2`` autograd Function, ``forward(ctx, input, weight, mask, offset,
+  bias, stride, padding)`` and a ``once_differentiable`` backward returning
+  ``(grad_input, grad_weight, grad_mask, grad_offset, grad_bias, None, ...)``
+  (reference ``dcn_v2_mm.py:15-53``);
+* ``dcn_v2_conv = _DCNv2.apply`` (``:56``);
+* ``DCNv2(in_channels, out_channels, kernel_size, stride, padding, dilation=1,
+  deformable_groups=1)`` with ``forward(input, offset, mask)`` (``:59-102``);
+* ``DCN(...)``, which predicts offset and mask with a zero-initialised conv and
+  splits its output as ``o1, o2, mask = chunk(3)``, ``offset = cat(o1, o2)``,
+  ``mask = sigmoid(mask)`` (``:105-146``).
+
+Difference from the reference, by design: ``dilation`` and
+``deformable_groups`` are forwarded to the operator (the reference accepts and
+drops them, ``:94-102``), appended as two optional trailing arguments of
+``dcn_v2_conv``.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+from torch import nn
+from torch.autograd import Function
+from torch.autograd.function import once_differentiable
+from torch.nn.modules.utils import _pair
+
+from . import _C
+
+
+class _DCNv2(Function):
+    @staticmethod
+    def forward(ctx, input, weight, mask, offset, bias, stride, padding, dilation=1,
+                deformable_groups=1):
+        ctx.stride = _pair(stride)
+        ctx.padding = _pair(padding)
+        ctx.dilation = _pair(dilation)
+        ctx.deformable_groups = int(deformable_groups)
+        output = _C.dcn_v2_forward(
+            input, weight, mask, offset, bias,
+            ctx.stride[0], ctx.stride[1], ctx.padding[0], ctx.padding[1],
+            ctx.dilation[0], ctx.dilation[1], ctx.deformable_groups)
+        ctx.save_for_backward(input, weight, mask, offset, bias)
+        return output
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, grad_output):
+        input, weight, mask, offset, bias = ctx.saved_tensors
+        grad_input, grad_offset, grad_mask, grad_weight, grad_bias = _C.dcn_v2_backward(
+            input, weight, mask, offset, bias, grad_output,
+            ctx.stride[0], ctx.stride[1], ctx.padding[0], ctx.padding[1],
+            ctx.dilation[0], ctx.dilation[1], ctx.deformable_groups)
+        return (grad_input, grad_weight, grad_mask, grad_offset, grad_bias,
+                None, None, None, None)
+
+
+dcn_v2_conv = _DCNv2.apply
+
+
+class DCNv2(nn.Module):
+    def __init__(self, in_channels, out_channels, kernel_size, stride, padding, dilation=1,
+                 deformable_groups=1):
+        super().__init__()
+        self.in_channels = in_channels
+        self.out_channels = out_channels
+        self.kernel_size = _pair(kernel_size)
+        self.stride = _pair(stride)
+        self.padding = _pair(padding)
+        self.dilation = _pair(dilation)
+        self.deformable_groups = deformable_groups
+        if in_channels % deformable_groups != 0:
+            raise ValueError("in_channels must be divisible by deformable_groups")
+        self.weight = nn.Parameter(torch.Tensor(out_channels, in_channels, *self.kernel_size))
+        self.bias = nn.Parameter(torch.Tensor(out_channels))
+        self.reset_parameters()
+
+    def reset_parameters(self):
+        # reference dcn_v2_mm.py:83-89: U(+-1/sqrt(fan_in)), zero bias
+        n = self.in_channels
+        for k in self.kernel_size:
+            n *= k
+        stdv = 1.0 / math.sqrt(n)
+        self.weight.data.uniform_(-stdv, stdv)
+        self.bias.data.zero_()
+
+    def forward(self, input, offset, mask):
+        kk = self.kernel_size[0] * self.kernel_size[1]
+        assert 2 * self.deformable_groups * kk == offset.shape[1]
+        assert self.deformable_groups * kk == mask.shape[1]
+        return dcn_v2_conv(input, self.weight, mask, offset, self.bias, self.stride,
+                           self.padding, self.dilation, self.deformable_groups)
+
+
+class DCN(DCNv2):
+    def __init__(self, in_channels, out_channels, kernel_size, stride=1, padding=0,
+                 dilation=1, deformable_groups=1):
+        super().__init__(in_channels, out_channels, kernel_size, stride, padding, dilation,
+                         deformable_groups)
+        channels_ = self.deformable_groups * 3 * self.kernel_size[0] * self.kernel_size[1]
+        # The offset/mask predictor sees the same sampling grid as the DCN
+        # (stride, padding and dilation), so its output matches Ho x Wo.
+        self.conv_offset_mask = nn.Conv2d(
+            self.in_channels, channels_, kernel_size=self.kernel_size, stride=self.stride,
+            padding=self.padding, dilation=self.dilation, bias=True)
+        self.init_offset()
+
+    def init_offset(self):
+        self.conv_offset_mask.weight.data.zero_()
+        self.conv_offset_mask.bias.data.zero_()
+
+    def forward(self, input):
+        out = self.conv_offset_mask(input)
+        o1, o2, mask = torch.chunk(out, 3, dim=1)
+        offset = torch.cat((o1, o2), dim=1)
+        mask = torch.sigmoid(mask)
+        return dcn_v2_conv(input, self.weight, mask, offset, self.bias, self.stride,
+                           self.padding, self.dilation, self.deformable_groups)

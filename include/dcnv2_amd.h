@@ -1,0 +1,105 @@
+/*
+ * dcnv2_amd -- C ABI of the MI355X (gfx950) modulated deformable convolution v2.
+ *
+ * This is the drop-in boundary for the reference's native operator module
+ * `Conv2d._C` (reference ext.cpp:15-18, name.h:15-36).  Every entry point takes
+ * plain pointers, sizes and a HIP stream handle; there are no framework types.
+ * All work is enqueued asynchronously on `stream` (a hipStream_t; NULL = the
+ * null stream) and nothing synchronises the host.  The library keeps no state
+ * between calls apart from the per-thread error message, so calls are
+ * re-entrant.
+ *
+ * Semantics are those of torchvision.ops.deform_conv2d(input, offset, weight,
+ * bias, stride, padding, dilation, mask), the comparator the reference names:
+ *   output[b, m, oy, ox] = bias[m] + sum_{c, i, j} weight[m, c, i, j]
+ *                          * mask[b, g*kh*kw + k, oy, ox]
+ *                          * bilinear(input[b, c], y, x)
+ *   k = i*kw + j,  g = c / (C / deformable_groups),
+ *   y = oy*stride_h - pad_h + i*dilation_h + offset[b, 2*(g*kh*kw + k),     oy, ox]
+ *   x = ox*stride_w - pad_w + j*dilation_w + offset[b, 2*(g*kh*kw + k) + 1, oy, ox]
+ * with bilinear() reading 0 outside the image (reference com.cu:119-148, 187).
+ *
+ * Tensor layouts are contiguous NCHW in the caller's dtype:
+ *   input  [B, C, H, W]            weight [Cout, C, kh, kw]       bias [Cout]
+ *   offset [B, 2*G*kh*kw, Ho, Wo]  mask   [B, G*kh*kw, Ho, Wo]    output [B, Cout, Ho, Wo]
+ *   Ho = (H + 2*pad_h - (dilation_h*(kh-1) + 1)) / stride_h + 1   (likewise Wo)
+ * All tensors of one call share the dtype in dcn2_desc.dtype; the GEMM
+ * accumulates in fp32 and the sampling arithmetic is fp32 for every dtype.
+ *
+ * Return value of every int function: 0 = success, otherwise a DCN2_E* code;
+ * dcn2_last_error() then describes the failure.  This replaces the reference's
+ * AT_ASSERTM / std::runtime_error paths (com.cu:209-213, 266-270, 760-761),
+ * which the Python layer turns back into RuntimeError.
+ */
+#ifndef DCNV2_AMD_H
+#define DCNV2_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DCN2_ABI_VERSION 1
+#define DCN2_API __attribute__((visibility("default")))
+
+enum dcn2_dtype { DCN2_F32 = 0, DCN2_F16 = 1, DCN2_BF16 = 2 };
+
+enum dcn2_status {
+    DCN2_OK = 0,
+    DCN2_EINVAL = 1,     /* bad geometry, dtype, null pointer or group split     */
+    DCN2_EWORKSPACE = 2, /* workspace smaller than dcn2_*_workspace_bytes()       */
+    DCN2_ELAUNCH = 3,    /* a HIP launch or runtime call failed                   */
+    DCN2_ERANGE = 4      /* a tensor exceeds the library's 32-bit index range     */
+};
+
+/* Problem description.  Mirrors the argument list of the reference's
+ * dcn_v2_forward(input, weight, mask, offset, bias, stride_h, stride_w, pad_h,
+ * pad_w) (name.h:15-24) with the shapes read off the tensors, extended by
+ * dilation and deformable groups, which the reference's Python module accepts
+ * but never forwards (dcn_v2_mm.py:67-68, 94-102). */
+typedef struct dcn2_desc {
+    int32_t batch, in_channels, height, width;
+    int32_t out_channels, kernel_h, kernel_w;
+    int32_t stride_h, stride_w, pad_h, pad_w, dilation_h, dilation_w;
+    int32_t deformable_groups;
+    int32_t dtype; /* enum dcn2_dtype */
+} dcn2_desc;
+
+/* Output spatial size for `d`; DCN2_EINVAL if it would be empty. */
+DCN2_API int dcn2_output_shape(const dcn2_desc *d, int32_t *out_h, int32_t *out_w);
+
+/* Device workspace the forward / backward need (bytes, 256-byte aligned
+ * start required).  0 is returned for an invalid description. */
+DCN2_API size_t dcn2_forward_workspace_bytes(const dcn2_desc *d);
+DCN2_API size_t dcn2_backward_workspace_bytes(const dcn2_desc *d);
+
+/* Forward.  Replaces MyDCN_forward / _C.dcn_v2_forward (com.cu:198-272,
+ * ext.cpp:16; bound in dcn_v2_mm.py:20-30).  `mask` may be NULL (all ones,
+ * DCNv1) and `bias` may be NULL (zeros).  `output` is fully overwritten. */
+DCN2_API int dcn2_forward(const dcn2_desc *d, const void *input, const void *weight, const void *mask,
+                 const void *offset, const void *bias, void *output, void *workspace,
+                 size_t workspace_bytes, void *stream);
+
+/* Backward.  Replaces MyDCN_backward / _C.dcn_v2_backward (com.cu:733-848,
+ * ext.cpp:17; bound in dcn_v2_mm.py:38-49), whose result order is
+ * [grad_input, grad_offset, grad_mask, grad_weight, grad_bias] (com.cu:845-847).
+ * All five gradient buffers are fully overwritten (not accumulated).
+ * grad_mask must be NULL exactly when mask is NULL; grad_bias may be NULL. */
+DCN2_API int dcn2_backward(const dcn2_desc *d, const void *input, const void *weight, const void *mask,
+                  const void *offset, const void *grad_output, void *grad_input,
+                  void *grad_offset, void *grad_mask, void *grad_weight, void *grad_bias,
+                  void *workspace, size_t workspace_bytes, void *stream);
+
+/* Human-readable description of the last failure on the calling thread. */
+DCN2_API const char *dcn2_last_error(void);
+
+/* Library version string ("dcnv2_amd <abi> gfx950"). */
+DCN2_API const char *dcn2_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DCNV2_AMD_H */

@@ -1,0 +1,226 @@
+"""GPU parity of the HIP path (called through the C ABI via dcnv2_amd._C).
+
+Checks: max|y - y_ref| / max|y_ref| <= 1e-2 for
+fp16/bf16 and <= 1e-4 for fp32, for the output and all five gradients.
+
+* golden fixtures (tests/golden, made by the independent grid_sample
+  formulation): every dtype, forward and backward;
+* the five BASELINE configurations at full size: forward of the first and last
+  image against the CPU oracle, forward+backward of one image against the
+  oracle in the config dtype and in an fp32 rerun, and the whole batch against
+  the independent grid_sample formulation evaluated in fp32 on the GPU;
+* edge cases: mask/bias None, Cout > 256 (two M tiles), every sample outside
+  the image, non-contiguous inputs, an empty batch.
+"""
+from __future__ import annotations
+
+import functools
+import glob
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from dcnv2_amd import _C
+from dcnv2_amd.workloads import CONFIGS, make_inputs
+from independent import forward_backward_gs, sample_positions
+from oracle import oracle
+from util import GRADS, TOL, load_fixture, rel_err
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+IN5 = ("input", "weight", "mask", "offset", "bias")
+FIXTURES = sorted(glob.glob(os.path.join(os.path.dirname(__file__), "golden", "*.npz")))
+DTYPES = [torch.float32, torch.float16, torch.bfloat16]
+
+
+def _args(geo):
+    s, p, d, G = geo["stride"], geo["padding"], geo["dilation"], geo["deformable_groups"]
+    return (s, s, p, p, d, d, G)
+
+
+def gpu_forward(t, geo):
+    return _C.dcn_v2_forward(*(None if t[k] is None else t[k].to(DEV) for k in IN5), *_args(geo))
+
+
+def gpu_backward(t, geo):
+    return _C.dcn_v2_backward(*(None if t[k] is None else t[k].to(DEV) for k in IN5),
+                              t["grad_output"].to(DEV), *_args(geo))
+
+
+def oracle_forward(t, geo):
+    return oracle.dcn_forward(*(t[k] for k in IN5), pos_f32=True, **geo)
+
+
+def oracle_backward(t, geo):
+    return oracle.dcn_backward(*(t[k] for k in IN5), t["grad_output"], pos_f32=True, **geo)
+
+
+def check(name, got, ref, tol):
+    e = rel_err(got, ref)
+    print(f"  {name}: rel_err={e:.3e} (tol {tol:.0e})")
+    assert e <= tol, f"{name}: {e:.3e} > {tol:.0e}"
+
+
+@functools.lru_cache(maxsize=4)
+def config_inputs(idx, dtype=None):
+    w = CONFIGS[idx]
+    return make_inputs(w, dtype=dtype, with_grad=True)
+
+
+def slice_batch(t, b0, b1):
+    return {k: (v[b0:b1] if k not in ("weight", "bias") and v is not None else v)
+            for k, v in t.items()}
+
+
+# --------------------------------------------------------------------------- fixtures
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+@pytest.mark.parametrize("fx", FIXTURES, ids=lambda p: os.path.basename(p)[:-4])
+def test_fixture(fx, dtype):
+    a, geo = load_fixture(fx)
+    t = {k: a[k].to(dtype) for k in IN5 + ("grad_output",)}
+    out = gpu_forward(t, geo)
+    grads = gpu_backward(t, geo)
+    torch.cuda.synchronize()
+    tol = TOL[dtype]
+    if dtype == torch.float32:
+        refs = [a["output"]] + [a[k] for k in GRADS]
+    else:  # the fixture inputs rounded to dtype, evaluated exactly by the oracle
+        refs = [oracle_forward(t, geo)] + list(oracle_backward(t, geo))
+    check("output", out, refs[0], tol)
+    for name, g, r in zip(GRADS, grads, refs[1:]):
+        check(name, g, r, tol)
+
+
+# --------------------------------------------------------------------------- configs
+@pytest.mark.parametrize("idx", range(len(CONFIGS)), ids=[w.name for w in CONFIGS])
+def test_config_forward_full_batch_vs_oracle(idx):
+    w = CONFIGS[idx]
+    t = config_inputs(idx)
+    out = gpu_forward(t, w.geometry())
+    torch.cuda.synchronize()
+    for b in sorted({0, w.B - 1}):
+        ref = oracle_forward(slice_batch(t, b, b + 1), w.geometry())
+        check(f"output[b={b}]", out[b:b + 1], ref, TOL[w.dtype])
+
+
+@pytest.mark.parametrize("fp32", [False, True], ids=["config_dtype", "fp32"])
+@pytest.mark.parametrize("idx", range(len(CONFIGS)), ids=[w.name for w in CONFIGS])
+def test_config_backward_one_image_vs_oracle(idx, fp32):
+    w = CONFIGS[idx]
+    dtype = torch.float32 if fp32 else w.dtype
+    t = slice_batch(config_inputs(idx, dtype), 0, 1)
+    out = gpu_forward(t, w.geometry())
+    grads = gpu_backward(t, w.geometry())
+    torch.cuda.synchronize()
+    check("output", out, oracle_forward(t, w.geometry()), TOL[dtype])
+    for name, g, r in zip(GRADS, grads, oracle_backward(t, w.geometry())):
+        check(name, g, r, TOL[dtype])
+
+
+@pytest.mark.parametrize("idx", range(len(CONFIGS)), ids=[w.name for w in CONFIGS])
+def test_config_full_batch_vs_gridsample(idx):
+    """Whole batch at full size against the independent formulation (fp32 on
+    the GPU, from the same rounded inputs).  grad_offset is compared only at
+    samples at least 1e-3 away from an integer coordinate: on an integer the
+    one-sided derivative depends on how each side rounds the position, and
+    those points are covered by the oracle tests above."""
+    w = CONFIGS[idx]
+    t = config_inputs(idx)
+    out = gpu_forward(t, w.geometry())
+    grads = gpu_backward(t, w.geometry())
+    ref = forward_backward_gs(*(t[k].to(DEV) for k in ("input", "weight", "offset", "mask",
+                                                         "bias")),
+                              t["grad_output"].to(DEV), dtype=torch.float32, **w.geometry())
+    torch.cuda.synchronize()
+    r_out, r_gi, r_goff, r_gm, r_gw, r_gb = ref
+    tol = TOL[w.dtype]
+    check("output", out, r_out, tol)
+    check("grad_input", grads[0], r_gi, tol)
+    check("grad_mask", grads[2], r_gm, tol)
+    check("grad_weight", grads[3], r_gw, tol)
+    check("grad_bias", grads[4], r_gb, tol)
+    y, x = sample_positions(t["offset"], w.k, w.k, w.Ho, w.Wo, **w.geometry())
+    far = lambda v: (v - v.round()).abs() > 1e-3  # noqa: E731
+    keep = (far(y) & far(x)).view(w.B, w.groups * w.k * w.k, 1, w.Ho, w.Wo)
+    keep = keep.expand(-1, -1, 2, -1, -1).reshape(t["offset"].shape)
+    got = grads[1].float().cpu()[keep]
+    refv = r_goff.float().cpu()[keep]
+    assert keep.float().mean() > 0.5
+    check("grad_offset (non-integer samples)", got, refv, tol)
+
+
+# --------------------------------------------------------------------------- edge cases
+def _small(dtype, B=2, C=12, H=9, W=11, Cout=20, k=3, s=1, p=1, d=1, G=3, seed=7, osc=2.0):
+    w = CONFIGS[0].with_(B=B, C=C, H=H, W=W, Cout=Cout, k=k, stride=s, pad=p, dil=d, groups=G,
+                         seed=seed, offset_dist=f"normal:{osc}", backward=True)
+    return w, make_inputs(w, dtype=dtype)
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+def test_mask_and_bias_none(dtype):
+    w, t = _small(dtype)
+    t["mask"] = None
+    t["bias"] = None
+    out = gpu_forward(t, w.geometry())
+    grads = gpu_backward(t, w.geometry())
+    torch.cuda.synchronize()
+    assert grads[2] is None and grads[4] is None
+    check("output", out, oracle_forward(t, w.geometry()), TOL[dtype])
+    rg = oracle_backward(t, w.geometry())
+    for name, g, r in zip(GRADS, grads, rg):
+        if g is not None:
+            check(name, g, r, TOL[dtype])
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+def test_cout_beyond_one_tile(dtype):
+    w, t = _small(dtype, Cout=300, C=70, G=1, H=10, W=13)
+    out = gpu_forward(t, w.geometry())
+    grads = gpu_backward(t, w.geometry())
+    torch.cuda.synchronize()
+    check("output", out, oracle_forward(t, w.geometry()), TOL[dtype])
+    for name, g, r in zip(GRADS, grads, oracle_backward(t, w.geometry())):
+        check(name, g, r, TOL[dtype])
+
+
+def test_all_samples_outside_give_bias():
+    w, t = _small(torch.float32)
+    t["offset"] = torch.full_like(t["offset"], 1e4)
+    out = gpu_forward(t, w.geometry())
+    grads = gpu_backward(t, w.geometry())
+    torch.cuda.synchronize()
+    expect = t["bias"].view(1, -1, 1, 1).expand_as(out.cpu())
+    assert torch.equal(out.cpu(), expect)
+    for g in (grads[0], grads[1], grads[2], grads[3]):
+        assert torch.count_nonzero(g) == 0
+    torch.testing.assert_close(grads[4].cpu(), t["grad_output"].sum((0, 2, 3)))
+
+
+def test_non_contiguous_inputs():
+    w, t = _small(torch.float16)
+    ref = gpu_forward(t, w.geometry())
+    nc = {k: (v.transpose(-1, -2).contiguous().transpose(-1, -2) if v is not None and v.dim() == 4
+              else v) for k, v in t.items()}
+    assert not nc["input"].is_contiguous()
+    out = gpu_forward(nc, w.geometry())
+    torch.cuda.synchronize()
+    assert torch.equal(out.cpu(), ref.cpu())
+
+
+def test_empty_batch():
+    w, t = _small(torch.float32, B=0)
+    out = gpu_forward(t, w.geometry())
+    grads = gpu_backward(t, w.geometry())
+    torch.cuda.synchronize()
+    assert tuple(out.shape) == (0, w.Cout, w.Ho, w.Wo)
+    assert torch.count_nonzero(grads[3]) == 0 and torch.count_nonzero(grads[4]) == 0
+
+
+def test_forward_deterministic():
+    w, t = _small(torch.bfloat16, G=1, C=64)
+    a = gpu_forward(t, w.geometry())
+    b = gpu_forward(t, w.geometry())
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
