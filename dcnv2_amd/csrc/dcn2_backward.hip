@@ -489,11 +489,12 @@ static hipError_t backward_t(const Geo &g, const BwdParams &p0, void *grad_input
     {
         const size_t n_gi = (size_t)g.B * g.H * g.W * g.cs;
         const size_t n_gw = (size_t)g.Mp * g.Kp;
+        // gb_acc is null when the caller wants no grad_bias; nothing reads it then.
         float *bufs[3] = {p.gi_acc, p.gw_acc, p.gb_acc};
         const size_t counts[3] = {n_gi, n_gw, (size_t)g.Mp};
         for (int i = 0; i < 3; ++i) {
             const size_t n4 = (counts[i] + 3) / 4;
-            if (n4 == 0) continue;
+            if (n4 == 0 || bufs[i] == nullptr) continue;
             const unsigned blocks = (unsigned)std::min<size_t>((n4 + 255) / 256, 4096);
             fill_zero_kernel<<<blocks, 256, 0, s>>>((float4 *)bufs[i], n4);
             if ((e = hipGetLastError()) != hipSuccess) return e;
