@@ -1,0 +1,205 @@
+#!/usr/bin/env python
+"""Headline benchmark of dcnv2_amd on one MI355X.
+
+Metric: DCNv2 forward TFLOPS by the reference README formula
+(README.md:17-19: B*Hout*Wout*Cout*(10*kh*kw*C + 2*kh*kw)) at the README shape
+B8 C64 128x128 Cout256 3x3 fp16, plus forward+backward
+milliseconds at the same shape (config 2).
+
+A step is one forward over one batch of synthetic inputs already resident in
+HBM.  W untimed warm-up steps, then K steps bracketed by device
+synchronisation and HIP events on the stream the kernels run on.  The
+``roofline`` object covers the dominant kernel (the fused forward kernel):
+achieved = algorithmic GEMM FLOPs per launch (2*B*Cout*Hout*Wout*C*kh*kw) /
+its average duration, measured with the library's per-stage HIP events over a
+second timed loop.  ``cpu_baseline`` times the float32 CPU oracle
+(oracle/dcn_oracle.c, OpenMP) on a bounded sample of the same workload.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_FP16_TFLOPS = 2500.0   # MI355X dense fp16/bf16 MFMA
+PEAK_FP32_TFLOPS = 157.3
+REF_README_TFLOPS = 90.2    # reference README.md:14 (RTX 3090, com_2buffer_cpasyc.cu)
+METRIC = "DCNv2 fwd TFLOPS (README formula) @B8 C64 128² Co256 3×3 fp16; fwd+bwd ms"
+
+
+def _events_ms(fn, steps, torch):
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(steps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def _stage_avgs(_C, names):
+    out = {}
+    for s in names:
+        ms, n = _C.profile_read(s)
+        if n:
+            out[s] = ms / n
+    return out
+
+
+def _traffic():
+    """HBM bytes per launch of the forward kernel measured with rocprofv3 PMC
+    counters (profiles/fwd_kernel_traffic.json, see profiles/README.md)."""
+    path = os.path.join(ROOT, "profiles", "fwd_kernel_traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get("hbm_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def cpu_baseline(w, seconds, threads):
+    """Times the float32 oracle forward on image 0 of workload `w`."""
+    import numpy as np  # noqa: F401
+    from dcnv2_amd.workloads import make_inputs
+    from oracle import oracle
+
+    one = w.with_(B=1)
+    t = make_inputs(one, dtype=None)
+    args = [t[k].float().numpy() for k in ("input", "weight", "mask", "offset", "bias")]
+    geo = one.geometry()
+    oracle.dcn_forward(*args, **geo, precision="f32", nthreads=threads)  # warm-up
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        oracle.dcn_forward(*args, **geo, precision="f32", nthreads=threads)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or reps >= 200:
+            break
+    return {
+        "value": one.readme_flops() * reps / el / 1e12,
+        "unit": "TFLOPS (README formula)",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{reps} x forward of image 0 of {w.name} (B=1 of {w.B}), float32, "
+                  f"{el:.1f} s, C oracle with OpenMP",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one GPU; the batch-sharded multi-GPU path is "
+              "described in DESIGN.md but not benchmarked (run with --gpus 1)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from dcnv2_amd import _C
+    from dcnv2_amd.workloads import CONFIGS
+
+    dev = torch.device("cuda:0")
+    fwd_w, fb_w = CONFIGS[1], CONFIGS[2]
+
+    def load(w):
+        from dcnv2_amd.workloads import make_inputs
+        return {k: v.to(dev) for k, v in make_inputs(w).items()}
+
+    t = load(fwd_w)
+    geo = (fwd_w.stride, fwd_w.stride, fwd_w.pad, fwd_w.pad, fwd_w.dil, fwd_w.dil,
+           fwd_w.groups)
+    fargs = (t["input"], t["weight"], t["mask"], t["offset"], t["bias"])
+
+    def fwd():
+        return _C.dcn_v2_forward(*fargs, *geo)
+
+    for _ in range(args.warmup):
+        fwd()
+    ms = _events_ms(fwd, args.steps, torch)
+    value = fwd_w.readme_flops() / (ms * 1e-3) / 1e12
+
+    # second loop with per-stage events for the kernel roofline
+    _C.profile_enable(True)
+    _stage_avgs(_C, _C.STAGES)  # clear
+    _events_ms(fwd, args.steps, torch)
+    fstages = _stage_avgs(_C, ("fwd_pack", "fwd_main"))
+    _C.profile_enable(False)
+    kern_ms = fstages["fwd_main"]
+    achieved = fwd_w.gemm_flops() / (kern_ms * 1e-3) / 1e12
+
+    # forward + backward at the same shape (config 2)
+    t2 = load(fb_w)
+    b_args = (t2["input"], t2["weight"], t2["mask"], t2["offset"], t2["bias"])
+
+    def fwd_bwd():
+        _C.dcn_v2_forward(*b_args, *geo)
+        return _C.dcn_v2_backward(*b_args, t2["grad_output"], *geo)
+
+    fb_steps = max(5, args.steps // 4)
+    for _ in range(max(2, args.warmup // 2)):
+        fwd_bwd()
+    fb_ms = _events_ms(fwd_bwd, fb_steps, torch)
+    _C.profile_enable(True)
+    _stage_avgs(_C, _C.STAGES)
+    _events_ms(fwd_bwd, fb_steps, torch)
+    bstages = _stage_avgs(_C, _C.STAGES)
+    _C.profile_enable(False)
+
+    result = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "TFLOPS (README formula)",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": round(value / REF_README_TFLOPS, 3),
+        "baseline_note": "90.2 README-formula TFLOPS of com_2buffer_cpasyc.cu on an RTX 3090 "
+                         "(README.md:14); different hardware",
+        "dtype": "fp16",
+        "data": "synthetic (seeded, BASELINE.json config distributions; inputs resident in HBM)",
+        "config": {"workload": "c1_readme_fwd: B8 C64 H128 W128 Cout256 3x3 s1 p1 d1 dg1 fp16, "
+                               "forward", "global_batch": fwd_w.B, "parallelism": "single GPU"},
+        "fwd_real_tflops": round(fwd_w.gemm_flops() / (ms * 1e-3) / 1e12, 2),
+        "fwd_bwd_ms": round(fb_ms, 5),
+        "fwd_bwd_workload": "c2_readme_fwd_bwd: same shape, forward + all five gradients, fp16",
+        "stages_ms": {"forward": {k: round(v, 5) for k, v in fstages.items()},
+                      "forward_backward": {k: round(v, 5) for k, v in bstages.items()}},
+        "roofline": {
+            "bound": "mfma",
+            "kernel": "dcn2_fwd_kernel<f16,4,2> (fused sampling + 32x32x16 MFMA)",
+            "achieved": round(achieved, 2),
+            "peak": PEAK_FP16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_FP16_TFLOPS, 4),
+            "traffic": _traffic(),
+            "algorithmic_flops_per_launch": fwd_w.gemm_flops(),
+            "kernel_ms": round(kern_ms, 5),
+        },
+    }
+    if not args.no_cpu:
+        threads = max(1, min(16, os.cpu_count() or 1))
+        result["cpu_baseline"] = cpu_baseline(fwd_w, args.cpu_seconds, threads)
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -73,6 +73,11 @@ def lib() -> ctypes.CDLL:
             L.dcn2_last_error.restype = ctypes.c_char_p
             L.dcn2_version.argtypes = []
             L.dcn2_version.restype = ctypes.c_char_p
+            L.dcn2_profile_enable.argtypes = [ctypes.c_int]
+            L.dcn2_profile_enable.restype = ctypes.c_int
+            L.dcn2_profile_read.argtypes = [ctypes.c_int, ctypes.POINTER(ctypes.c_double),
+                                            ctypes.POINTER(ctypes.c_int)]
+            L.dcn2_profile_read.restype = ctypes.c_int
             _lib = L
     return _lib
 
@@ -214,3 +219,21 @@ def dcn_v2_backward(input, weight, mask, offset, bias, grad_output, stride_h, st
 
 def version() -> str:
     return lib().dcn2_version().decode()
+
+
+STAGES = ("fwd_pack", "fwd_main", "bwd_pack", "bwd_colgrad", "bwd_gradw", "bwd_gather",
+          "bwd_final")
+
+
+def profile_enable(on: bool = True) -> None:
+    """Per-stage HIP-event timing of the calls made on this thread."""
+    lib().dcn2_profile_enable(1 if on else 0)
+
+
+def profile_read(stage: str):
+    """(total_ms, launches) recorded for `stage` since the last read; waits for
+    the recorded events."""
+    ms, n = ctypes.c_double(), ctypes.c_int()
+    if lib().dcn2_profile_read(STAGES.index(stage), ctypes.byref(ms), ctypes.byref(n)) != 0:
+        raise _err("profile_read")
+    return ms.value, n.value

@@ -14,6 +14,7 @@
 #include "../../include/dcnv2_amd.h"
 #include "dcn2_common.h"
 #include "dcn2_kernels.h"
+#include "dcn2_profile.h"
 
 namespace dcn2 {
 
@@ -82,7 +83,8 @@ static int make_geo(const dcn2_desc *d, Geo &g) {
     const long long Kp = (long long)g.KK * g.cs;
     if ((long long)g.H * g.W * g.cs >= lim || (long long)g.C * g.H * g.W >= lim ||
         (long long)g.Ho * g.Wo * g.Cout >= lim || (long long)g.Ho * g.Wo * 2 * g.G * g.KK >= lim ||
-        Kp * g.Mp >= lim || (long long)g.Ho * g.Wo >= lim || g.B > 65535)
+        Kp * g.Mp >= lim || (long long)g.Ho * g.Wo >= lim || g.B > 65535 ||
+        (long long)g.B * g.G * g.KK * g.Ho * g.Wo >= lim || g.H > 32767 || g.W > 32767)
         return fail(DCN2_ERANGE, "dcn2: problem exceeds the 32-bit per-image index range");
     g.Kp = (int)Kp;
     return DCN2_OK;
@@ -95,6 +97,8 @@ FwdWorkspace fwd_workspace(const Geo &g) {
     o += align256((size_t)g.B * g.H * g.W * g.cs * g.esz);
     w.wp = o;
     o += align256((size_t)g.Mp * g.Kp * g.esz);
+    w.tab = o;
+    o += align256((size_t)(g.Kp / g.KC) * 16);
     w.total = o;
     return w;
 }
@@ -106,12 +110,21 @@ BwdWorkspace bwd_workspace(const Geo &g) {
     o += align256((size_t)g.B * g.H * g.W * g.cs * g.esz);
     w.wt = o;
     o += align256((size_t)g.Mp * g.Kp * g.esz);
+    w.tab = o;
+    o += align256((size_t)(g.Kp / g.KC) * 16);
     w.gi_acc = o;
     o += align256((size_t)g.B * g.H * g.W * g.cs * sizeof(float));
     w.gw_acc = o;
     o += align256((size_t)g.Mp * g.Kp * sizeof(float));
     w.gb_acc = o;
     o += align256((size_t)g.Mp * sizeof(float));
+    const GatherGeo gg = gather_geometry(g);
+    w.cgm = o;
+    o += align256((size_t)g.B * g.G * g.KK * g.N * g.Cgp * g.esz);
+    w.rec = o;
+    o += align256((size_t)gg.nbuckets * gg.cap * 16);
+    w.cnt = o;
+    o += align256((size_t)gg.nbuckets * sizeof(int) + 16);
     w.total = o;
     return w;
 }
@@ -166,10 +179,16 @@ int dcn2_forward(const dcn2_desc *d, const void *input, const void *weight, cons
     if (g.B == 0) return DCN2_OK;
     hipStream_t s = (hipStream_t)stream;
     char *base = (char *)workspace;
-    void *xt = base + ws.xt, *wp = base + ws.wp;
+    void *xt = base + ws.xt, *wp = base + ws.wp, *tab = base + ws.tab;
+    prof_begin(DCN2_STAGE_FWD_PACK, s);
     if ((rc = check_launch(launch_pack_input(g, input, xt, s), "pack_input"))) return rc;
-    if ((rc = check_launch(launch_pack_weight(g, weight, wp, false, s), "pack_weight"))) return rc;
-    return check_launch(launch_forward(g, xt, wp, offset, mask, bias, output, s), "forward");
+    if ((rc = check_launch(launch_pack_weight(g, weight, wp, tab, false, s), "pack_weight")))
+        return rc;
+    prof_end(DCN2_STAGE_FWD_PACK, s);
+    prof_begin(DCN2_STAGE_FWD_MAIN, s);
+    rc = check_launch(launch_forward(g, xt, wp, tab, offset, mask, bias, output, s), "forward");
+    prof_end(DCN2_STAGE_FWD_MAIN, s);
+    return rc;
 }
 
 int dcn2_backward(const dcn2_desc *d, const void *input, const void *weight, const void *mask,
@@ -192,17 +211,19 @@ int dcn2_backward(const dcn2_desc *d, const void *input, const void *weight, con
                     ws.total, workspace_bytes);
     hipStream_t s = (hipStream_t)stream;
     char *base = (char *)workspace;
-    void *xt = base + ws.xt, *wt = base + ws.wt;
+    void *xt = base + ws.xt, *wt = base + ws.wt, *tab = base + ws.tab;
+    prof_begin(DCN2_STAGE_BWD_PACK, s);
     if (g.B > 0) {
         if ((rc = check_launch(launch_pack_input(g, input, xt, s), "pack_input"))) return rc;
     }
-    if ((rc = check_launch(launch_pack_weight(g, weight, wt, true, s), "pack_weight_t")))
+    if ((rc = check_launch(launch_pack_weight(g, weight, wt, tab, true, s), "pack_weight_t")))
         return rc;
-    return check_launch(launch_backward(g, xt, wt, offset, mask, grad_output,
+    prof_end(DCN2_STAGE_BWD_PACK, s);
+    return check_launch(launch_backward(g, xt, wt, tab, offset, mask, grad_output,
                                         grad_input, grad_offset, grad_mask, grad_weight,
                                         grad_bias, (float *)(base + ws.gi_acc),
                                         (float *)(base + ws.gw_acc), (float *)(base + ws.gb_acc),
-                                        s),
+                                        base + ws.cgm, base + ws.rec, (int *)(base + ws.cnt), s),
                         "backward");
 }
 

@@ -20,28 +20,70 @@
 //     grad_bias from the same gO fragments.
 //  finalize kernels: fp32 accumulators -> caller dtype and layout.
 #include <algorithm>
+#include <type_traits>
 
 #include "dcn2_common.h"
 #include "dcn2_sampler.h"
 #include "dcn2_kernels.h"
+#include "dcn2_profile.h"
 #include "../../include/dcnv2_amd.h"
 
 namespace dcn2 {
 
 struct BwdParams {
-    const void *xt, *wt, *offset, *mask, *gout;
+    const void *xt, *wt, *tab, *offset, *mask, *gout;
     void *goff, *gmask;
     float *gi_acc, *gw_acc, *gb_acc;
     int B, H, W, Cout, kh, kw, sh, sw, ph, pw, dh, dw, G, Cg, Cgp, Ho, Wo, Kp, Mp;
     int tiles_per_img, splits;
     int go_vec;  // grad_output rows can be read with 16-byte loads (N % 8 == 0, aligned base)
+    // grad_input gather: cell-tile buckets (see dcn2_gi_gather_kernel)
+    void *cgm;          // [B*G*KK*N][Cgp] masked column gradient rows, call dtype
+    int4 *rec;          // [nbuckets][cap] sample records
+    int *cnt;           // [nbuckets] records appended per bucket
+    int ntx, nty, cap;  // cell tiles per row / column, bucket capacity
 };
 
-// Per-pixel sampling record written by the reduction phase for the scatter.
+// Cell tiles of the grad_input gather: a sample with floor corner (y0, x0)
+// belongs to cell (y0+1, x0+1) of the (H+1) x (W+1) cell grid, and cells are
+// grouped in kCellTile x kCellTile tiles, one bucket per (image, group, tile).
+constexpr int kCellTile = 16;
+
+// Per-pixel sampling record written by the reduction phase for the
+// grad_input phase.  mode 0: no corner inside the image (nothing to add);
+// 1: appended to its cell-tile bucket (write the masked column-gradient row);
+// 2: bucket full (add to grad_input directly with atomics).
 struct Desc {
     int off[4];
     float w[4];  // masked bilinear weight of each corner, 0 outside the image
+    int sidx;    // dense sample index ((b*G + g)*KK + tap)*N + n
+    float m;     // mask value
+    int mode;
+    int pad;
 };
+
+// Appends this lane's record to bucket `key` when `want`; wavefront-aggregated:
+// one atomic per distinct bucket among the wave's lanes.  Returns the slot or
+// -1 when the bucket is full (or !want).
+__device__ __forceinline__ int bucket_append(bool want, int key, int *cnt, int cap) {
+    const int lane = threadIdx.x & 63;
+    unsigned long long active = __ballot(want);
+    int slot = -1;
+    while (active) {
+        const int leader = __ffsll((long long)active) - 1;
+        const int lkey = __shfl(key, leader, 64);
+        const unsigned long long same = __ballot(want && key == lkey) & active;
+        int base = 0;
+        if (lane == leader) base = atomicAdd(cnt + lkey, __popcll(same));
+        base = __shfl(base, leader, 64);
+        if ((same >> lane) & 1ull) {
+            const int rank = __popcll(same & ((1ull << lane) - 1ull));
+            slot = base + rank < cap ? base + rank : -1;
+        }
+        active &= ~same;
+    }
+    return slot;
+}
 
 template <typename T, int KPL> struct FragSet;
 template <typename T> struct FragSet<T, 1> {
@@ -96,7 +138,7 @@ __global__ __launch_bounds__(512) void dcn2_colgrad_kernel(const BwdParams p) {
 
     // gO fragments (MFMA B operand, [m][n]): n = this wave's 32-pixel block.
     frag gfr[NMS];
-    auto load_go = [&](int mc) {
+    auto load_go = [&](int mc) __attribute__((always_inline)) {
         const int n = n0 + nb * 32 + (lane & 31);
 #pragma unroll
         for (int s = 0; s < NMS; ++s) {
@@ -119,6 +161,7 @@ __global__ __launch_bounds__(512) void dcn2_colgrad_kernel(const BwdParams p) {
         oxr = nr - oyr * p.Wo;
     }
     float racc[3] = {0.0f, 0.0f, 0.0f};  // grad_mask, grad_off_y, grad_off_x (lq == 0)
+    int gmode = 0, gsidx = 0;             // grad_input mode of (pr, tap, g), see Desc
 
     for (int ch = 0; ch < nch; ++ch) {
         const int tg = ch / cpg, cc = ch - tg * cpg;
@@ -174,6 +217,23 @@ __global__ __launch_bounds__(512) void dcn2_colgrad_kernel(const BwdParams p) {
                     f32x4{acc[4 * j], acc[4 * j + 1], acc[4 * j + 2], acc[4 * j + 3]};
             }
         }
+        // grad_input bookkeeping, once per (tap, group): append the sample to
+        // the bucket of its cell tile.  The slot decision holds for all
+        // channel chunks of the group.
+        if (cc == 0) {
+            const bool any = live && (sp.vy0 || sp.vy1) && (sp.vx0 || sp.vx1);
+            const int cy = sp.y0 + 1, cx = sp.x0 + 1;
+            const int key = ((b * p.G + g) * p.nty + cy / kCellTile) * p.ntx + cx / kCellTile;
+            const int sidx = ((b * p.G + g) * KK + tap) * N + nr;
+            const int slot = bucket_append(any && lq == 0, key, p.cnt, p.cap);
+            if (slot >= 0) {
+                p.rec[(size_t)key * p.cap + slot] =
+                    make_int4(sidx, (sp.y0 & 0xffff) | (int)((unsigned)sp.x0 << 16), __float_as_int(sp.ly),
+                              __float_as_int(sp.lx));
+            }
+            gmode = !any ? 0 : (slot >= 0 ? 1 : 2);
+            gsidx = sidx;
+        }
         if (lq == 0) {
             Desc d;
 #pragma unroll
@@ -181,6 +241,10 @@ __global__ __launch_bounds__(512) void dcn2_colgrad_kernel(const BwdParams p) {
                 d.off[q] = cr.off[q];
                 d.w[q] = cr.w[q];
             }
+            d.sidx = gsidx;
+            d.m = mv;
+            d.mode = gmode;
+            d.pad = 0;
             sD[pr] = d;
         }
         __syncthreads();
@@ -238,21 +302,29 @@ __global__ __launch_bounds__(512) void dcn2_colgrad_kernel(const BwdParams p) {
             }
         }
 
-        // grad_input scatter: lane = channel, one corner run per instruction.
+        // grad_input: lane = channel.  Bucketed samples store their masked
+        // column-gradient row (one contiguous run per wave instruction) for
+        // the gather kernel; samples of a full bucket add to grad_input here.
         {
             const int c = lane % KC, sub = lane / KC;
             const bool cvalid = cc * KC + c < p.Cg;
             float *gib = gi + g * p.Cgp + cc * KC + c;
+            T *cgm = (T *)p.cgm + cc * KC + c;
             for (int it = 0; it < BN / (8 * PPW); ++it) {
                 const int pl = (it * 8 + wave) * PPW + sub;
-                if (n0 + pl >= N || !cvalid) continue;
+                if (n0 + pl >= N) continue;
+                const Desc d = sD[pl];
+                if (d.mode == 0) continue;
                 float v = sCG[0][pl][c];
 #pragma unroll
                 for (int w2 = 1; w2 < WPB; ++w2) v += sCG[w2][pl][c];
-                const Desc d = sD[pl];
+                if (d.mode == 1) {
+                    cgm[(size_t)d.sidx * p.Cgp] = from_f32<T>(v * d.m);
+                } else if (cvalid) {
 #pragma unroll
-                for (int q = 0; q < 4; ++q)
-                    if (d.w[q] != 0.0f) unsafeAtomicAdd(gib + d.off[q], v * d.w[q]);
+                    for (int q = 0; q < 4; ++q)
+                        if (d.w[q] != 0.0f) unsafeAtomicAdd(gib + d.off[q], v * d.w[q]);
+                }
             }
         }
         __syncthreads();
@@ -280,7 +352,7 @@ template <> struct GwLayout<bf16> {
 
 __device__ __forceinline__ int gw_swz(int k) { return ((k & 15) ^ (k >> 3)) & 15; }
 
-template <typename T, int MB>
+template <typename T, int MB, bool MASK>
 __global__ __launch_bounds__(512) void dcn2_gradw_kernel(const BwdParams p) {
     using M = Mma<T>;
     using frag = typename M::frag;
@@ -309,39 +381,58 @@ __global__ __launch_bounds__(512) void dcn2_gradw_kernel(const BwdParams p) {
         kblk0 = wave - mblk * KB;
         active = wave < NBLK;
     }
-    const bool do_bias = p.gb_acc != nullptr && blockIdx.y == 0 && kblk0 == 0 && active;
-    const int ch = blockIdx.y, sp = blockIdx.x, S = p.splits;
-    const int mrow = blockIdx.z * 32 * MB + mblk * 32 + (lane & 31);
+    // Work item = (pixel-tile range sp, K chunk ch, M chunk mc), handed to XCDs
+    // in contiguous ranges with the range index slowest, so one XCD works on
+    // consecutive pixel tiles (same images) for all chunks.
+    const int nch = p.Kp / KC, nmc = p.Mp / (32 * MB);
+    const int wi = xcd_remap(blockIdx.x, p.splits * nch * nmc);
+    const int mc = wi % nmc, ch = (wi / nmc) % nch, sp = wi / (nmc * nch);
+    const bool do_bias = p.gb_acc != nullptr && ch == 0 && kblk0 == 0 && active;
+    const int mrow = mc * 32 * MB + mblk * 32 + (lane & 31);
     const int N = p.Ho * p.Wo, KK = p.kh * p.kw, cs = p.G * p.Cgp;
     const int T_total = p.B * p.tiles_per_img;
+    // contiguous range of pixel tiles [t_begin, t_end) of this work item
+    const int t_begin = (int)((long)T_total * sp / p.splits);
+    const int t_end = (int)((long)T_total * (sp + 1) / p.splits);
 
     SampleGeo sg;
     sg.H = p.H; sg.W = p.W; sg.kh = p.kh; sg.kw = p.kw; sg.sh = p.sh; sg.sw = p.sw;
     sg.ph = p.ph; sg.pw = p.pw; sg.dh = p.dh; sg.dw = p.dw; sg.G = p.G; sg.Cgp = p.Cgp;
     sg.Wo = p.Wo; sg.N = N; sg.cs = cs; sg.KK = KK;
-    Sampler<T, 1> smp;
+    const ChunkEnt cp = ((const ChunkEnt *)p.tab)[ch];
+    // Two sampler register sets / offset-mask sets alternate between even and
+    // odd tiles (loop unrolled by two): offset/mask loads run 3 tiles ahead of
+    // the MFMA, corner gathers 2 ahead, the LDS store 1 ahead.
+    Sampler<T, 1, MASK> smp[2];
+    smp[0].init(tid);
+    smp[1].init(tid);
+    SlotOM<T, 1> om[2];
 
-    auto issue_tile = [&](int t) {
+    auto load_om_tile = [&](int t, SlotOM<T, 1> &o) __attribute__((always_inline)) {
         const int b = t / p.tiles_per_img, n0 = (t - b * p.tiles_per_img) * BN;
-        smp.bind(n0, sg, tid);
-        smp.issue(ch, sg, (const T *)p.xt + (size_t)b * p.H * p.W * cs,
-                  (const T *)p.offset + (size_t)b * p.G * KK * 2 * N,
-                  p.mask ? (const T *)p.mask + (size_t)b * p.G * KK * N : nullptr);
+        smp[0].load_om(n0, cp.x, sg, tid, (const T *)p.offset + (size_t)b * p.G * KK * 2 * N,
+                       MASK ? (const T *)p.mask + (size_t)b * p.G * KK * N : nullptr, o);
     };
-    auto store_stage = [&](int buf) {
+    auto issue_tile = [&](auto set_c, int t, const SlotOM<T, 1> &o) __attribute__((always_inline)) {
+        constexpr int set = decltype(set_c)::value;
+        const int b = t / p.tiles_per_img;
+        smp[set].issue(cp, sg, (const T *)p.xt + (size_t)b * p.H * p.W * cs, o);
+    };
+    auto store_stage = [&](auto set_c, int buf) __attribute__((always_inline)) {
+        constexpr int set = decltype(set_c)::value;
         const int pl = tid >> 2;
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
             float v[16 / sizeof(T)];
-            smp.blend(0, u, v);
+            smp[set].blend(0, u, v);
             if constexpr (KMAJ) {
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
-                    const int k = smp.q[0] * CPS + u * 8 + e;
+                    const int k = smp[set].q * CPS + u * 8 + e;
                     sC[buf][k][((pl >> 3) ^ gw_swz(k)) * 8 + (pl & 7)] = (T)v[e];
                 }
             } else {
-                *reinterpret_cast<uint4 *>(&sC[buf][pl][smp.q[0] * CPS + u * 4]) = pack16<T>(v);
+                *reinterpret_cast<uint4 *>(&sC[buf][pl][smp[set].q * CPS + u * 4]) = pack16<T>(v);
             }
         }
     };
@@ -354,7 +445,7 @@ __global__ __launch_bounds__(512) void dcn2_gradw_kernel(const BwdParams p) {
     float bsum = 0.0f;
 
     const bool aligned = p.go_vec != 0;
-    auto load_a = [&](frag &a, int t, int ks) {
+    auto load_a = [&](frag &a, int t, int ks) __attribute__((always_inline)) {
         const int b = t / p.tiles_per_img, n0 = (t - b * p.tiles_per_img) * BN;
         const int n = n0 + ks * KSTEP + (lane >> 5) * KPL;
         const T *row = (const T *)p.gout + ((size_t)b * p.Cout + mrow) * N;
@@ -368,47 +459,81 @@ __global__ __launch_bounds__(512) void dcn2_gradw_kernel(const BwdParams p) {
             }
         }
     };
+    // gO fragments of a whole tile are prefetched one step ahead for 2-byte
+    // types (8 registers of 16 bytes); fp32 (64 one-float steps) loads at use.
+    constexpr bool PREA = KPL == 8;
+    frag a_cur[PREA ? NKS : 1], a_nxt[PREA ? NKS : 1];
+    auto load_a_tile = [&](frag (&a)[PREA ? NKS : 1], int t) {
+        if constexpr (PREA) {
+#pragma unroll
+            for (int ks = 0; ks < NKS; ++ks) load_a(a[ks], t, ks);
+        }
+    };
 
-    if (sp < T_total) {
-        issue_tile(sp);
-        store_stage(0);
-    }
-    __syncthreads();
-    int it = 0;
-    for (int t = sp; t < T_total; t += S, ++it) {
-        const int buf = it & 1;
-        const bool more = t + S < T_total;
-        if (more) issue_tile(t + S);
-        if (active) {
+    auto mfma_tile = [&](int t, int buf) __attribute__((always_inline)) {
+        if (!active) return;
 #pragma unroll
-            for (int ks = 0; ks < NKS; ++ks) {
-                frag a;
+        for (int ks = 0; ks < NKS; ++ks) {
+            frag a;
+            if constexpr (PREA) {
+                a = a_cur[ks];
+            } else {
                 load_a(a, t, ks);
-                if (do_bias) {
-                    if constexpr (KPL == 1) {
-                        bsum += to_f32(a);
-                    } else {
+            }
+            if (do_bias) {
+                if constexpr (KPL == 1) {
+                    bsum += to_f32(a);
+                } else {
 #pragma unroll
-                        for (int e = 0; e < KPL; ++e) bsum += to_f32(a[e]);
-                    }
-                }
-#pragma unroll
-                for (int i = 0; i < BPW; ++i) {
-                    const int k = (kblk0 + i) * 32 + (lane & 31);
-                    frag bf;
-                    if constexpr (KMAJ) {
-                        const int nblk = ks * 2 + (lane >> 5);
-                        bf = *reinterpret_cast<const frag *>(
-                            &sC[buf][k][(nblk ^ gw_swz(k)) * 8]);
-                    } else {
-                        bf = sC[buf][ks * KSTEP + (lane >> 5)][k];
-                    }
-                    acc[i] = M::mma(a, bf, acc[i]);
+                    for (int e = 0; e < KPL; ++e) bsum += to_f32(a[e]);
                 }
             }
+#pragma unroll
+            for (int i = 0; i < BPW; ++i) {
+                const int k = (kblk0 + i) * 32 + (lane & 31);
+                frag bf;
+                if constexpr (KMAJ) {
+                    const int nblk = ks * 2 + (lane >> 5);
+                    bf = *reinterpret_cast<const frag *>(&sC[buf][k][(nblk ^ gw_swz(k)) * 8]);
+                } else {
+                    bf = sC[buf][ks * KSTEP + (lane >> 5)][k];
+                }
+                acc[i] = M::mma(a, bf, acc[i]);
+            }
         }
-        if (more) store_stage(buf ^ 1);
+    };
+
+    // One step for tile t (the it-th of this work item, set S = it % 2).
+    auto step = [&](auto s_c, int t) __attribute__((always_inline)) {
+        constexpr int S = decltype(s_c)::value;
+        constexpr int O = S ^ 1;
+        if (t + 3 < t_end) load_om_tile(t + 3, om[O]);
+        if (t + 1 < t_end && active) load_a_tile(a_nxt, t + 1);
+        if (t + 2 < t_end) issue_tile(std::integral_constant<int, S>{}, t + 2, om[S]);
+        mfma_tile(t, S);
+        if (t + 1 < t_end) {
+            store_stage(std::integral_constant<int, O>{}, O);
+            if constexpr (PREA) {
+#pragma unroll
+                for (int ks = 0; ks < NKS; ++ks) a_cur[ks] = a_nxt[ks];
+            }
+        }
         __syncthreads();
+    };
+
+    if (t_begin < t_end) {
+        load_om_tile(t_begin, om[0]);
+        if (t_begin + 1 < t_end) load_om_tile(t_begin + 1, om[1]);
+        if (active) load_a_tile(a_cur, t_begin);
+        issue_tile(std::integral_constant<int, 0>{}, t_begin, om[0]);
+        if (t_begin + 2 < t_end) load_om_tile(t_begin + 2, om[0]);
+        if (t_begin + 1 < t_end) issue_tile(std::integral_constant<int, 1>{}, t_begin + 1, om[1]);
+        store_stage(std::integral_constant<int, 0>{}, 0);
+    }
+    __syncthreads();
+    for (int t = t_begin; t < t_end; t += 2) {
+        step(std::integral_constant<int, 0>{}, t);
+        if (t + 1 < t_end) step(std::integral_constant<int, 1>{}, t + 1);
     }
 
     if (!active) return;
@@ -417,13 +542,93 @@ __global__ __launch_bounds__(512) void dcn2_gradw_kernel(const BwdParams p) {
         const int k = ch * KC + (kblk0 + i) * 32 + (lane & 31);
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            const int m = blockIdx.z * 32 * MB + mblk * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            const int m = mc * 32 * MB + mblk * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
             if (m < p.Cout) unsafeAtomicAdd(p.gw_acc + (size_t)m * p.Kp + k, acc[i][r]);
         }
     }
     if (do_bias) {
         bsum += shfl_xor_f(bsum, 32);
         if (lane < 32 && mrow < p.Cout) unsafeAtomicAdd(p.gb_acc + mrow, bsum);
+    }
+}
+
+
+// ---------------------------------------------------------------------------
+// grad_input gather.  One block per bucket (image, group, 16x16 cell tile):
+// every record of the bucket adds its masked column-gradient row, times the
+// four bilinear corner weights, into an LDS tile of the (TS+1) x (TS+1)
+// pixels its corners can reach (ds_add, lane = channel).  The tile is then
+// added to grad_input: interior pixels (reachable from this tile's cells only)
+// by a plain read-modify-write, the one-pixel border ring, shared with the
+// neighbouring tiles, by fp32 atomics.  This replaces one global atomic per
+// (sample, corner, channel) -- the reference's col2im scatter, com.cu:553-609
+// -- by one per border pixel and channel.
+template <typename T>
+__global__ __launch_bounds__(512) void dcn2_gi_gather_kernel(const BwdParams p) {
+    constexpr int KC = Mma<T>::KC;
+    constexpr int TS = kCellTile, TW = TS + 1;
+    constexpr int RPW = 64 / KC;  // records per wave instruction
+    constexpr int UNR = 4;        // records in flight per lane group
+    __shared__ __attribute__((aligned(16))) float acc[TW * TW][KC];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nb = p.B * p.G * p.nty * p.ntx;
+    const int bucket = xcd_remap(blockIdx.x, nb);
+    const int tx = bucket % p.ntx, ty = (bucket / p.ntx) % p.nty;
+    const int bg = bucket / (p.ntx * p.nty), b = bg / p.G, g = bg - b * p.G;
+    const int count = min(p.cnt[bucket], p.cap);
+    const int4 *__restrict__ recs = p.rec + (size_t)bucket * p.cap;
+    const int oy = ty * TS - 1, ox = tx * TS - 1;  // pixel of local (0, 0)
+    const int cs = p.G * p.Cgp, cpg = p.Cgp / KC;
+    const int c = lane % KC, sub = lane / KC;
+    float *__restrict__ gi = p.gi_acc + (size_t)b * p.H * p.W * cs + g * p.Cgp;
+
+    for (int cc = 0; cc < cpg; ++cc) {
+        for (int e = tid; e < TW * TW * KC / 4; e += 512)
+            reinterpret_cast<float4 *>(&acc[0][0])[e] = make_float4(0.f, 0.f, 0.f, 0.f);
+        __syncthreads();
+        const T *__restrict__ cgm = (const T *)p.cgm + cc * KC + c;
+        for (int r0 = (wave * RPW + sub) * UNR; r0 < count; r0 += 8 * RPW * UNR) {
+            int4 rc[UNR];
+            float v[UNR];
+#pragma unroll
+            for (int u = 0; u < UNR; ++u)
+                rc[u] = r0 + u < count ? recs[r0 + u] : make_int4(-1, 0, 0, 0);
+#pragma unroll
+            for (int u = 0; u < UNR; ++u)
+                v[u] = rc[u].x >= 0 ? to_f32(cgm[(size_t)rc[u].x * p.Cgp]) : 0.0f;
+#pragma unroll
+            for (int u = 0; u < UNR; ++u) {
+                if (rc[u].x < 0) continue;
+                const int y0 = (int)(short)(rc[u].y & 0xffff), x0 = rc[u].y >> 16;
+                const float ly = __int_as_float(rc[u].z), lx = __int_as_float(rc[u].w);
+                const float hy = 1.0f - ly, hx = 1.0f - lx;
+                const int ly0 = y0 - oy, lx0 = x0 - ox;
+                const bool r0v = y0 >= 0, r1v = y0 + 1 < p.H;
+                const bool c0v = x0 >= 0, c1v = x0 + 1 < p.W;
+                float *a = &acc[ly0 * TW + lx0][c];
+                if (r0v && c0v) atomicAdd(a, v[u] * (hy * hx));
+                if (r0v && c1v) atomicAdd(a + KC, v[u] * (hy * lx));
+                if (r1v && c0v) atomicAdd(a + TW * KC, v[u] * (ly * hx));
+                if (r1v && c1v) atomicAdd(a + (TW + 1) * KC, v[u] * (ly * lx));
+            }
+        }
+        __syncthreads();
+        for (int e = tid; e < TW * TW * KC; e += 512) {
+            const int pix = e / KC, ch = e - pix * KC;
+            const int py = pix / TW, px = pix - py * TW;
+            const int Y = oy + py, X = ox + px;
+            if (Y < 0 || Y >= p.H || X < 0 || X >= p.W || cc * KC + ch >= p.Cg) continue;
+            const float val = acc[pix][ch];
+            if (val == 0.0f) continue;
+            float *dst = gi + ((size_t)Y * p.W + X) * cs + cc * KC + ch;
+            const bool interior = py >= 1 && py <= TS - 1 && px >= 1 && px <= TS - 1;
+            if (interior)
+                *dst += val;
+            else
+                unsafeAtomicAdd(dst, val);
+        }
+        __syncthreads();
     }
 }
 
@@ -486,13 +691,15 @@ static hipError_t backward_t(const Geo &g, const BwdParams &p0, void *grad_input
     BwdParams p = p0;
     hipError_t e;
     // 1. zero the fp32 accumulators
+    prof_begin(DCN2_STAGE_BWD_PACK, s);
     {
         const size_t n_gi = (size_t)g.B * g.H * g.W * g.cs;
         const size_t n_gw = (size_t)g.Mp * g.Kp;
         // gb_acc is null when the caller wants no grad_bias; nothing reads it then.
-        float *bufs[3] = {p.gi_acc, p.gw_acc, p.gb_acc};
-        const size_t counts[3] = {n_gi, n_gw, (size_t)g.Mp};
-        for (int i = 0; i < 3; ++i) {
+        float *bufs[4] = {p.gi_acc, p.gw_acc, p.gb_acc, (float *)p.cnt};
+        const size_t counts[4] = {n_gi, n_gw, (size_t)g.Mp,
+                                  (size_t)g.B * g.G * p.nty * p.ntx};
+        for (int i = 0; i < 4; ++i) {
             const size_t n4 = (counts[i] + 3) / 4;
             if (n4 == 0 || bufs[i] == nullptr) continue;
             const unsigned blocks = (unsigned)std::min<size_t>((n4 + 255) / 256, 4096);
@@ -500,18 +707,30 @@ static hipError_t backward_t(const Geo &g, const BwdParams &p0, void *grad_input
             if ((e = hipGetLastError()) != hipSuccess) return e;
         }
     }
+    prof_end(DCN2_STAGE_BWD_PACK, s);
     if (g.B > 0) {
         // 2. column gradient: grad_offset, grad_mask, grad_input accumulation
+        prof_begin(DCN2_STAGE_BWD_COLGRAD, s);
         {
             dim3 grid(p.tiles_per_img, g.B);
             // fp32 keeps the 128-wide M chunk: 256 would hold 128 gO registers.
-            if (sizeof(T) == 2 && g.Mp % 256 == 0)
-                dcn2_colgrad_kernel<T, 256><<<grid, 512, 0, s>>>(p);
-            else
+            if constexpr (sizeof(T) == 2) {
+                if (g.Mp % 256 == 0)
+                    dcn2_colgrad_kernel<T, 256><<<grid, 512, 0, s>>>(p);
+                else
+                    dcn2_colgrad_kernel<T, 128><<<grid, 512, 0, s>>>(p);
+            } else {
                 dcn2_colgrad_kernel<T, 128><<<grid, 512, 0, s>>>(p);
+            }
             if ((e = hipGetLastError()) != hipSuccess) return e;
         }
+        prof_end(DCN2_STAGE_BWD_COLGRAD, s);
+        prof_begin(DCN2_STAGE_BWD_GATHER, s);
+        dcn2_gi_gather_kernel<T><<<g.B * g.G * p.nty * p.ntx, 512, 0, s>>>(p);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+        prof_end(DCN2_STAGE_BWD_GATHER, s);
         // 3. grad_weight / grad_bias
+        prof_begin(DCN2_STAGE_BWD_GRADW, s);
         {
             const int nch = g.Kp / g.KC;
             const int mb = (g.Mp % 256 == 0) ? 8 : 4;
@@ -520,14 +739,23 @@ static hipError_t backward_t(const Geo &g, const BwdParams &p0, void *grad_input
             int S = 1024 / (nch * nmc);
             S = std::max(1, std::min(S, T_total));
             p.splits = S;
-            dim3 grid(S, nch, nmc);
-            if (mb == 8)
-                dcn2_gradw_kernel<T, 8><<<grid, 512, 0, s>>>(p);
-            else
-                dcn2_gradw_kernel<T, 4><<<grid, 512, 0, s>>>(p);
+            const int grid = S * nch * nmc;
+            if (mb == 8) {
+                if (p.mask)
+                    dcn2_gradw_kernel<T, 8, true><<<grid, 512, 0, s>>>(p);
+                else
+                    dcn2_gradw_kernel<T, 8, false><<<grid, 512, 0, s>>>(p);
+            } else {
+                if (p.mask)
+                    dcn2_gradw_kernel<T, 4, true><<<grid, 512, 0, s>>>(p);
+                else
+                    dcn2_gradw_kernel<T, 4, false><<<grid, 512, 0, s>>>(p);
+            }
             if ((e = hipGetLastError()) != hipSuccess) return e;
         }
+        prof_end(DCN2_STAGE_BWD_GRADW, s);
         // 4. grad_input to the caller's layout
+        prof_begin(DCN2_STAGE_BWD_FINAL, s);
         {
             const int HW = g.H * g.W;
             dim3 grid(ceil_div(HW, 64), g.cs / 32, g.B);
@@ -535,8 +763,10 @@ static hipError_t backward_t(const Geo &g, const BwdParams &p0, void *grad_input
                                                        g.Cgp, g.cs);
             if ((e = hipGetLastError()) != hipSuccess) return e;
         }
+        prof_end(DCN2_STAGE_BWD_FINAL, s);
     }
     // 5. grad_weight / grad_bias to the caller's layout
+    prof_begin(DCN2_STAGE_BWD_FINAL, s);
     {
         const long total = std::max<long>((long)g.Cout * g.C * g.KK, g.Cout);
         finalize_gw_kernel<T><<<(unsigned)((total + 255) / 256), 256, 0, s>>>(
@@ -544,16 +774,33 @@ static hipError_t backward_t(const Geo &g, const BwdParams &p0, void *grad_input
             g.G, g.Kp);
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }
+    prof_end(DCN2_STAGE_BWD_FINAL, s);
     return hipSuccess;
 }
 
-hipError_t launch_backward(const Geo &g, const void *xt, const void *wt, const void *offset,
+GatherGeo gather_geometry(const Geo &g) {
+    GatherGeo gg;
+    gg.ntx = ceil_div(g.W + 1, kCellTile);
+    gg.nty = ceil_div(g.H + 1, kCellTile);
+    gg.nbuckets = (long)g.B * g.G * gg.ntx * gg.nty;
+    const long samples = (long)g.B * g.G * g.KK * g.N;
+    const long avg = gg.nbuckets ? (samples + gg.nbuckets - 1) / gg.nbuckets : 0;
+    // Room for twice the mean occupancy; a fuller bucket spills its excess to
+    // the direct-atomic path, which is slower but equally exact.
+    gg.cap = (int)std::min<long>(2 * avg + 256, (long)kCellTile * kCellTile * g.KK * 4);
+    return gg;
+}
+
+hipError_t launch_backward(const Geo &g, const void *xt, const void *wt, const void *tab,
+                           const void *offset,
                            const void *mask, const void *grad_out, void *grad_input,
                            void *grad_offset, void *grad_mask, void *grad_weight, void *grad_bias,
-                           float *gi_acc, float *gw_acc, float *gb_acc, hipStream_t s) {
+                           float *gi_acc, float *gw_acc, float *gb_acc, void *cgm, void *rec,
+                           int *cnt, hipStream_t s) {
     BwdParams p;
     p.xt = xt;
     p.wt = wt;
+    p.tab = tab;
     p.offset = offset;
     p.mask = mask;
     p.gout = grad_out;
@@ -584,6 +831,13 @@ hipError_t launch_backward(const Geo &g, const void *xt, const void *wt, const v
     p.tiles_per_img = ceil_div(g.N, 128);
     p.splits = 1;
     p.go_vec = (g.N % 8 == 0) && (((uintptr_t)grad_out & 15) == 0);
+    const GatherGeo gg = gather_geometry(g);
+    p.cgm = cgm;
+    p.rec = (int4 *)rec;
+    p.cnt = cnt;
+    p.ntx = gg.ntx;
+    p.nty = gg.nty;
+    p.cap = gg.cap;
     switch (g.dtype) {
     case DCN2_F16: return backward_t<f16>(g, p, grad_input, grad_weight, grad_bias, s);
     case DCN2_BF16: return backward_t<bf16>(g, p, grad_input, grad_weight, grad_bias, s);

@@ -125,6 +125,17 @@ __device__ __forceinline__ Corners make_corners(const SamplePos &s, float m, int
 }
 
 __host__ __device__ constexpr inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
+
+// Number of XCDs of an MI355X; workgroup ids are dispatched round-robin over them.
+constexpr int kXcds = 8;
+
+// Bijection on [0, n): workgroup id -> work item such that the ids dispatched
+// to one XCD (id % 8 == x) receive one contiguous range of work items.
+__device__ __forceinline__ int xcd_remap(int id, int n) {
+    const int x = id % kXcds, slot = id / kXcds;
+    const int q = n / kXcds, r = n % kXcds;
+    return x * q + (x < r ? x : r) + slot;
+}
 __host__ __device__ constexpr inline int round_up(int a, int b) { return ceil_div(a, b) * b; }
 
 }  // namespace dcn2

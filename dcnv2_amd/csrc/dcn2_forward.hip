@@ -7,13 +7,15 @@
 // walks K in chunks of KC channels of one (tap, group):
 //
 //   for chunk ch:                       (double-buffered LDS stage sB[2])
+//     load offset/mask of ch+3                       -- raw bits, used next step
 //     issue A (weight) fragment loads for ch+1      -- global/L2, 16 B per lane
-//     compute descriptors + issue corner gathers for ch+1   -- channels-last xt
+//     descriptors + corner gathers for ch+2          -- channels-last xt
 //     MFMA over sB[ch&1]                             -- matrix cores
-//     finish the bilinear blend of ch+1 and store it to sB[(ch+1)&1]
+//     bilinear blend of ch+1 (gathered one step ago) -> sB[(ch+1)&1]
 //     barrier
 //
-// so the gathers and the blend of the next chunk overlap the MFMA of this one.
+// so a corner gather has a whole step (an MFMA phase and a barrier) to land
+// before its blend, and its offsets were loaded a step before that.
 // Each sampled value is produced once per workgroup and reused by every output
 // channel of the tile.
 //
@@ -21,6 +23,8 @@
 // sub-tile = 2x2 MFMA 32x32 blocks.  Sampling slot = (pixel, quarter of the
 // chunk): 4 lanes cover one pixel's KC channels, so one corner of one pixel is
 // read as a contiguous KC*sizeof(T)-byte run across 4 adjacent lanes.
+#include <type_traits>
+
 #include "dcn2_common.h"
 #include "dcn2_sampler.h"
 #include "dcn2_kernels.h"
@@ -29,17 +33,19 @@
 namespace dcn2 {
 
 struct FwdParams {
-    const void *xt, *wp, *offset, *mask, *bias;
+    const void *xt, *wp, *tab, *offset, *mask, *bias;
     void *out;
     int H, W, Cout, kh, kw, sh, sw, ph, pw, dh, dw, G, Cgp, Ho, Wo, Kp;
+    int ntiles, mtiles, tiles;  // pixel tiles per image, M tiles, B*ntiles*mtiles
 };
 
-template <typename T, int WM, int WN>
+template <typename T, int WM, int WN, int JB, bool MASK>
 __global__ __launch_bounds__(512) void dcn2_fwd_kernel(const FwdParams p) {
     using M = Mma<T>;
     using frag = typename M::frag;
     constexpr int KC = M::KC, KPL = M::KPL, KSTEP = M::KSTEP, NKS = KC / KSTEP;
-    constexpr int BN = 64 * WN;
+    constexpr int BN = 32 * JB * WN;            // each wave: 64 rows x 32*JB pixels
+    static_assert(WM * WN == 8, "8 waves");
     constexpr int CPS = KC / 4;                 // channels per sampling slot
     constexpr int U4 = CPS * sizeof(T) / 16;    // 16-byte registers per corner per slot (2)
     constexpr int SPT = BN * 4 / 512;           // sampling slots per thread
@@ -50,93 +56,142 @@ __global__ __launch_bounds__(512) void dcn2_fwd_kernel(const FwdParams p) {
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave / WN, wn = wave - wm * WN;
-    const int n0 = blockIdx.x * BN, m0 = blockIdx.y * (64 * WM), b = blockIdx.z;
+    // Tiles are numbered (image, pixel tile, M tile) and handed to XCDs in
+    // contiguous ranges: consecutive workgroup ids go round-robin over the 8
+    // XCDs, so XCD x receives the ids x, x+8, ... and is given the x-th range.
+    // Neighbouring tiles of one image then share that XCD's L2 for their
+    // corner gathers.
+    const int t = xcd_remap(blockIdx.x, p.tiles);
+    const int mt = t % p.mtiles, nt = (t / p.mtiles) % p.ntiles, b = t / (p.mtiles * p.ntiles);
+    const int n0 = nt * BN, m0 = mt * (64 * WM);
     const int N = p.Ho * p.Wo, KK = p.kh * p.kw, cs = p.G * p.Cgp;
-    const int nch = KK * p.G * (p.Cgp / KC);
+    const int nch = p.Kp / KC, last = nch - 1;
 
     const T *__restrict__ xt = (const T *)p.xt + (size_t)b * p.H * p.W * cs;
     const T *__restrict__ offs = (const T *)p.offset + (size_t)b * p.G * KK * 2 * N;
-    const T *__restrict__ msk = p.mask ? (const T *)p.mask + (size_t)b * p.G * KK * N : nullptr;
+    const T *__restrict__ msk = MASK ? (const T *)p.mask + (size_t)b * p.G * KK * N : nullptr;
+    const ChunkEnt *__restrict__ tab = (const ChunkEnt *)p.tab;
 
     SampleGeo sg;
     sg.H = p.H; sg.W = p.W; sg.kh = p.kh; sg.kw = p.kw; sg.sh = p.sh; sg.sw = p.sw;
     sg.ph = p.ph; sg.pw = p.pw; sg.dh = p.dh; sg.dw = p.dw; sg.G = p.G; sg.Cgp = p.Cgp;
     sg.Wo = p.Wo; sg.N = N; sg.cs = cs; sg.KK = KK;
-    Sampler<T, SPT> smp;
-    smp.bind(n0, sg, tid);
 
-    // Bilinear blend of the gathered corners, stored to LDS stage `buf` as
+    // Chunk c lives in set c % 2 of every pipeline buffer: offset/mask bits
+    // om, corner gathers smp, A fragments a and the LDS stage sB.  The loop
+    // is unrolled by two so that every set index is a compile-time constant,
+    // and stages past the last chunk re-read the last chunk (clamped table
+    // index) instead of branching, so one step is one basic block and the
+    // scheduler can interleave its MFMA with the VALU work of the next chunk.
+    Sampler<T, SPT, MASK> smp[2];
+    smp[0].init(tid);
+    smp[1].init(tid);
+    SlotOM<T, SPT> om[2];
+    frag a[2][2][NKS];
+
+    auto ent = [&](int ch) __attribute__((always_inline)) { return tab[min(ch, last)]; };
+
+    // Bilinear blend of sampler set SET, stored to LDS stage SET as
     // [pixel][channel] rows (the MFMA B-operand order).
-    auto store_stage = [&](int buf) {
+    auto store_stage = [&](auto set_c) __attribute__((always_inline)) {
+        constexpr int SET = decltype(set_c)::value;
 #pragma unroll
         for (int s = 0; s < SPT; ++s) {
             const int pl = (tid + s * 512) >> 2;
-            uint4 *dst = reinterpret_cast<uint4 *>(&sB[buf][pl][smp.q[s] * CPS]);
+            uint4 *dst = reinterpret_cast<uint4 *>(&sB[SET][pl][smp[SET].q * CPS]);
 #pragma unroll
             for (int u = 0; u < U4; ++u) {
                 float v[16 / sizeof(T)];
-                smp.blend(s, u, v);
+                smp[SET].blend(s, u, v);
                 dst[u] = pack16<T>(v);
             }
         }
     };
 
-    // A (weight) fragments: rows m0 + wm*64 + i*32 + lane%32.
-    const T *wrow[2];
+    // A (weight) fragments of rows m0 + wm*64 + i*32 + lane%32, packed in
+    // fragment order (pack_weight_kernel layout 0): the fragment (row block
+    // rb, chunk ch, step ks) is 64 lanes x KPL contiguous elements.
+    const T *wfrag[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
-        wrow[i] = (const T *)p.wp + (size_t)(m0 + wm * 64 + i * 32 + (lane & 31)) * p.Kp +
-                  (lane >> 5) * KPL;
-    frag a_cur[2][NKS], a_nxt[2][NKS];
-    auto load_a = [&](frag (&a)[2][NKS], int ch) {
+        wfrag[i] = (const T *)p.wp + ((size_t)((m0 + wm * 64 + i * 32) / 32) * nch * NKS * 64 +
+                                      lane) * KPL;
+    auto load_a = [&](auto set_c, int ch) __attribute__((always_inline)) {
+        constexpr int SET = decltype(set_c)::value;
+        const int c = min(ch, last) * NKS * 64 * KPL;
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
             for (int ks = 0; ks < NKS; ++ks)
-                a[i][ks] = *reinterpret_cast<const frag *>(wrow[i] + ch * KC + ks * KSTEP);
+                a[SET][i][ks] = *reinterpret_cast<const frag *>(wfrag[i] + c + ks * 64 * KPL);
     };
 
-    f32x16 acc[2][2];
+    f32x16 acc[2][JB];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < JB; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    // Prologue: chunk 0 into stage 0.
-    load_a(a_cur, 0);
-    smp.issue(0, sg, xt, offs, msk);
-    store_stage(0);
-    __syncthreads();
+    auto mfma_chunk = [&](auto set_c) __attribute__((always_inline)) {
+        constexpr int SET = decltype(set_c)::value;
+        frag bf[NKS][JB];
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks)
+#pragma unroll
+            for (int j = 0; j < JB; ++j)
+                bf[ks][j] = *reinterpret_cast<const frag *>(
+                    &sB[SET][(wn * JB + j) * 32 + (lane & 31)][ks * KSTEP + (lane >> 5) * KPL]);
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks)
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < JB; ++j)
+                    acc[i][j] = M::mma(a[SET][i][ks], bf[ks][j], acc[i][j]);
+    };
 
-    for (int ch = 0; ch < nch; ++ch) {
-        const int buf = ch & 1;
-        const bool more = ch + 1 < nch;
-        if (more) {
-            load_a(a_nxt, ch + 1);
-            smp.issue(ch + 1, sg, xt, offs, msk);
-        }
+    // One pipeline step for chunk ch, set S = ch % 2, O = S ^ 1:
+    //   offset/mask bits of ch+3 -> om[O]     A fragments of ch+1 -> a[O]
+    //   corner gathers of ch+2 (om[S]) -> smp[S]
+    //   MFMA of ch (a[S], sB[S])              blend of ch+1 (smp[O]) -> sB[O]
+    auto step = [&](auto s_c, int ch) __attribute__((always_inline)) {
+        constexpr int S = decltype(s_c)::value;
+        constexpr int O = S ^ 1;
+        const ChunkEnt e3 = ent(ch + 3), e2 = ent(ch + 2);
+        smp[0].load_om(n0, e3.x, sg, tid, offs, msk, om[O]);
+        load_a(std::integral_constant<int, O>{}, ch + 1);
+        smp[S].issue(e2, sg, xt, om[S]);
+        mfma_chunk(std::integral_constant<int, S>{});
+        store_stage(std::integral_constant<int, O>{});
+        // Interleave: each MFMA (32 cycles of the matrix core) is followed by
+        // a slice of the blend / descriptor VALU work and one LDS read.
+        __builtin_amdgcn_sched_group_barrier(0x100, JB * NKS, 0);  // all B-fragment reads
 #pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) {
-            frag bf[2];
-#pragma unroll
-            for (int j = 0; j < 2; ++j)
-                bf[j] = *reinterpret_cast<const frag *>(
-                    &sB[buf][wn * 64 + j * 32 + (lane & 31)][ks * KSTEP + (lane >> 5) * KPL]);
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int j = 0; j < 2; ++j) acc[i][j] = M::mma(a_cur[i][ks], bf[j], acc[i][j]);
-        }
-        if (more) {
-            store_stage(buf ^ 1);
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int ks = 0; ks < NKS; ++ks) a_cur[i][ks] = a_nxt[i][ks];
+        for (int i = 0; i < 2 * JB * NKS; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  // VALU
         }
         __syncthreads();
+    };
+
+    // Prologue: offset/mask bits of chunks 0, 1, 2; gathers of chunks 0 and
+    // 1; chunk 0 blended into stage 0.
+    {
+        const ChunkEnt e0 = ent(0), e1 = ent(1), e2 = ent(2);
+        smp[0].load_om(n0, e0.x, sg, tid, offs, msk, om[0]);
+        smp[0].load_om(n0, e1.x, sg, tid, offs, msk, om[1]);
+        load_a(std::integral_constant<int, 0>{}, 0);
+        smp[0].issue(e0, sg, xt, om[0]);
+        smp[0].load_om(n0, e2.x, sg, tid, offs, msk, om[0]);
+        smp[1].issue(e1, sg, xt, om[1]);
+        store_stage(std::integral_constant<int, 0>{});
+        __syncthreads();
+    }
+    for (int ch = 0; ch < nch; ch += 2) {
+        step(std::integral_constant<int, 0>{}, ch);
+        if (ch + 1 < nch) step(std::integral_constant<int, 1>{}, ch + 1);
     }
 
     // Epilogue: + bias, round to T, NCHW store.
@@ -150,33 +205,43 @@ __global__ __launch_bounds__(512) void dcn2_fwd_kernel(const FwdParams p) {
             if (m >= p.Cout) continue;
             const float bv = bias ? to_f32(bias[m]) : 0.0f;
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int n = n0 + wn * 64 + j * 32 + (lane & 31);
+            for (int j = 0; j < JB; ++j) {
+                const int n = n0 + (wn * JB + j) * 32 + (lane & 31);
                 if (n < N) out[(size_t)m * N + n] = from_f32<T>(acc[i][j][r] + bv);
             }
         }
     }
 }
 
-template <typename T, int WM, int WN>
-static hipError_t launch_fwd_t(const Geo &g, const FwdParams &p, hipStream_t s) {
-    dim3 grid(ceil_div(g.N, 64 * WN), g.Mp / (64 * WM), g.B);
-    dcn2_fwd_kernel<T, WM, WN><<<grid, 512, 0, s>>>(p);
+template <typename T, int WM, int WN, int JB>
+static hipError_t launch_fwd_t(const Geo &g, const FwdParams &p0, hipStream_t s) {
+    FwdParams p = p0;
+    p.ntiles = ceil_div(g.N, 32 * JB * WN);
+    p.mtiles = g.Mp / (64 * WM);
+    p.tiles = g.B * p.ntiles * p.mtiles;
+    if (p.mask)
+        dcn2_fwd_kernel<T, WM, WN, JB, true><<<p.tiles, 512, 0, s>>>(p);
+    else
+        dcn2_fwd_kernel<T, WM, WN, JB, false><<<p.tiles, 512, 0, s>>>(p);
     return hipGetLastError();
 }
 
+// Block tile 256x128 (8 waves of 64x64) when Cout > 128, else 128x128 (8
+// waves of 64x32); both sample 128 pixels, one slot per thread.
 template <typename T>
 static hipError_t launch_fwd_dt(const Geo &g, const FwdParams &p, hipStream_t s) {
-    if (g.BM == 256) return launch_fwd_t<T, 4, 2>(g, p, s);
-    return launch_fwd_t<T, 2, 4>(g, p, s);
+    if (g.BM == 256) return launch_fwd_t<T, 4, 2, 2>(g, p, s);
+    return launch_fwd_t<T, 2, 4, 1>(g, p, s);
 }
 
-hipError_t launch_forward(const Geo &g, const void *xt, const void *wp, const void *offset,
-                          const void *mask, const void *bias, void *out, hipStream_t s) {
+hipError_t launch_forward(const Geo &g, const void *xt, const void *wp, const void *tab,
+                          const void *offset, const void *mask, const void *bias, void *out,
+                          hipStream_t s) {
     if (g.B == 0) return hipSuccess;
     FwdParams p;
     p.xt = xt;
     p.wp = wp;
+    p.tab = tab;
     p.offset = offset;
     p.mask = mask;
     p.bias = bias;

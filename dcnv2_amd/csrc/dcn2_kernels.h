@@ -26,28 +26,38 @@ struct Geo {
 
 // Workspace carving shared by forward and backward (byte offsets).
 struct FwdWorkspace {
-    size_t xt, wp, total;
+    size_t xt, wp, tab, total;
 };
 FwdWorkspace fwd_workspace(const Geo &g);
 
 struct BwdWorkspace {
-    size_t xt, wt, gi_acc, gw_acc, gb_acc, total;
+    size_t xt, wt, tab, gi_acc, gw_acc, gb_acc, cgm, rec, cnt, total;
 };
 BwdWorkspace bwd_workspace(const Geo &g);
 
+// Bucket geometry of the grad_input gather (dcn2_backward.hip).
+struct GatherGeo {
+    int ntx, nty, cap;
+    long nbuckets;
+};
+GatherGeo gather_geometry(const Geo &g);
+
 // dcn2_pack.hip
 hipError_t launch_pack_input(const Geo &g, const void *input, void *xt, hipStream_t s);
-hipError_t launch_pack_weight(const Geo &g, const void *weight, void *wp, bool transpose,
-                              hipStream_t s);
+hipError_t launch_pack_weight(const Geo &g, const void *weight, void *wp, void *tab,
+                              bool transpose, hipStream_t s);
 
 // dcn2_forward.hip
-hipError_t launch_forward(const Geo &g, const void *xt, const void *wp, const void *offset,
-                          const void *mask, const void *bias, void *out, hipStream_t s);
+hipError_t launch_forward(const Geo &g, const void *xt, const void *wp, const void *tab,
+                          const void *offset, const void *mask, const void *bias, void *out,
+                          hipStream_t s);
 
 // dcn2_backward.hip
-hipError_t launch_backward(const Geo &g, const void *xt, const void *wt, const void *offset,
+hipError_t launch_backward(const Geo &g, const void *xt, const void *wt, const void *tab,
+                           const void *offset,
                            const void *mask, const void *grad_out, void *grad_input,
                            void *grad_offset, void *grad_mask, void *grad_weight, void *grad_bias,
-                           float *gi_acc, float *gw_acc, float *gb_acc, hipStream_t s);
+                           float *gi_acc, float *gw_acc, float *gb_acc, void *cgm, void *rec,
+                           int *cnt, hipStream_t s);
 
 }  // namespace dcn2

@@ -51,21 +51,49 @@ __global__ __launch_bounds__(256) void pack_input_kernel(const T *__restrict__ i
     }
 }
 
-// One thread per packed element.  transpose=false: dst[m][k]; true: dst[k][m].
+// One thread per packed element.  layout 0 (forward): MFMA A-fragment order,
+// dst[((rb*nch + ch)*nks + ks)*64 + lane][e] holds W'[32*rb + lane%32]
+// [ch*kc + ks*kstep + (lane/32)*kpl + e], so one wave's fragment load is one
+// contiguous run; layout 1 (backward): the transpose dst[k][m].
+// The first nch threads also write the chunk table: for chunk ch of the K
+// order (tap, group, channel chunk of kc channels) tab[ch] = {offset/mask
+// plane g*KK + tap, row term ki*dh, column term kj*dw, channel base
+// g*Cgp + cc*kc}; the sampling kernels read it with scalar loads instead of
+// dividing the chunk index every step.
 template <typename T>
 __global__ __launch_bounds__(256) void pack_weight_kernel(const T *__restrict__ w,
-                                                          T *__restrict__ dst, int Cout, int C,
-                                                          int KK, int G, int Cg, int Cgp,
-                                                          int Mp, int Kp, int transpose) {
+                                                          T *__restrict__ dst, int4 *__restrict__ tab,
+                                                          int Cout, int C, int KK, int kw, int dh,
+                                                          int dw, int G, int Cg, int Cgp, int kc,
+                                                          int kstep, int kpl, int Mp, int Kp,
+                                                          int transpose) {
     const long idx = (long)blockIdx.x * 256 + threadIdx.x;
+    const int nch = Kp / kc;
+    if (tab && idx < nch) {
+        const int cpg = Cgp / kc;
+        const int tg = (int)idx / cpg, cc = (int)idx - tg * cpg;
+        const int tap = tg / G, g = tg - tap * G;
+        const int ki = tap / kw, kj = tap - ki * kw;
+        tab[idx] = make_int4(g * KK + tap, ki * dh, kj * dw, g * Cgp + cc * kc);
+    }
     if (idx >= (long)Mp * Kp) return;
     int m, k;
     if (transpose) {
         k = (int)(idx / Mp);
         m = (int)(idx - (long)k * Mp);
     } else {
-        m = (int)(idx / Kp);
-        k = (int)(idx - (long)m * Kp);
+        // decompose the fragment-order index
+        const int nks = kc / kstep;
+        const int e = (int)(idx % kpl);
+        long r = idx / kpl;
+        const int lane = (int)(r % 64);
+        r /= 64;
+        const int ks = (int)(r % nks);
+        r /= nks;
+        const int ch = (int)(r % nch);
+        const int rb = (int)(r / nch);
+        m = rb * 32 + (lane & 31);
+        k = ch * kc + ks * kstep + (lane >> 5) * kpl + e;
     }
     const int gc = G * Cgp;
     const int tap = k / gc, r = k - tap * gc;
@@ -94,19 +122,22 @@ hipError_t launch_pack_input(const Geo &g, const void *input, void *xt, hipStrea
 }
 
 template <typename T>
-static hipError_t pack_weight_t(const Geo &g, const void *w, void *dst, bool tr, hipStream_t s) {
+static hipError_t pack_weight_t(const Geo &g, const void *w, void *dst, void *tab, bool tr,
+                                hipStream_t s) {
     const long total = (long)g.Mp * g.Kp;
     pack_weight_kernel<T><<<(unsigned)((total + 255) / 256), 256, 0, s>>>(
-        (const T *)w, (T *)dst, g.Cout, g.C, g.KK, g.G, g.Cg, g.Cgp, g.Mp, g.Kp, tr ? 1 : 0);
+        (const T *)w, (T *)dst, (int4 *)tab, g.Cout, g.C, g.KK, g.kw, g.dh, g.dw, g.G, g.Cg,
+        g.Cgp, g.KC, g.dtype == DCN2_F32 ? 2 : 16, g.dtype == DCN2_F32 ? 1 : 8, g.Mp, g.Kp,
+        tr ? 1 : 0);
     return hipGetLastError();
 }
 
-hipError_t launch_pack_weight(const Geo &g, const void *weight, void *wp, bool transpose,
-                              hipStream_t s) {
+hipError_t launch_pack_weight(const Geo &g, const void *weight, void *wp, void *tab,
+                              bool transpose, hipStream_t s) {
     switch (g.dtype) {
-    case DCN2_F16: return pack_weight_t<f16>(g, weight, wp, transpose, s);
-    case DCN2_BF16: return pack_weight_t<bf16>(g, weight, wp, transpose, s);
-    default: return pack_weight_t<float>(g, weight, wp, transpose, s);
+    case DCN2_F16: return pack_weight_t<f16>(g, weight, wp, tab, transpose, s);
+    case DCN2_BF16: return pack_weight_t<bf16>(g, weight, wp, tab, transpose, s);
+    default: return pack_weight_t<float>(g, weight, wp, tab, transpose, s);
     }
 }
 

@@ -58,59 +58,67 @@ struct SampleGeo {
     int H, W, kh, kw, sh, sw, ph, pw, dh, dw, G, Cgp, Wo, N, cs, KK;
 };
 
-// SPT slots per thread: slot s of thread tid is tid + 512*s.
-template <typename T, int SPT> struct Sampler {
+// Raw offset/mask bits and output-pixel coordinates of one chunk for the SPT
+// slots of a thread.  Kept unconverted so that the load can be issued one
+// pipeline step before its first use without forcing an early wait.
+template <typename T, int SPT> struct SlotOM {
+    int n[SPT], by[SPT], bx[SPT];
+    T dy[SPT], dx[SPT], m[SPT];
+};
+
+// Chunk table entry (written by pack_weight_kernel): x = offset/mask plane
+// g*KK + tap, y = ki*dh, z = kj*dw, w = first channel g*Cgp + cc*KC of the
+// chunk inside a pixel's channel vector.
+typedef int4 ChunkEnt;
+
+// SPT slots per thread: slot s of thread tid is tid + 512*s, covering output
+// pixel n0 + slot/4 and channel quarter slot%4 of the chunk.  MASK: a mask
+// tensor is present (else every mask value is 1).
+template <typename T, int SPT, bool MASK> struct Sampler {
     static constexpr int KC = Mma<T>::KC;
     static constexpr int CPS = KC / 4;               // channels per slot
     static constexpr int U4 = CPS * sizeof(T) / 16;  // 16-byte registers per corner (2)
     static_assert(U4 == 2, "a slot covers 32 bytes of one corner");
 
-    int n[SPT], q[SPT], by[SPT], bx[SPT];
+    int q;  // channel quarter of every slot of this thread (512 % 4 == 0)
     uint4 raw[SPT][4][U4];
     float w[SPT][4];
 
-    // Binds the slots to output pixels n0 + slot/4 of the current image.
-    __device__ __forceinline__ void bind(int n0, const SampleGeo &sg, int tid) {
+    __device__ __forceinline__ void init(int tid) { q = tid & 3; }
+
+    // Offset/mask bits of plane `plane` for the pixels n0 + slot/4 of the
+    // image whose offset/mask planes start at offs/msk.
+    __device__ __forceinline__ void load_om(int n0, int plane, const SampleGeo &sg, int tid,
+                                            const T *__restrict__ offs,
+                                            const T *__restrict__ msk,
+                                            SlotOM<T, SPT> &om) const {
 #pragma unroll
         for (int s = 0; s < SPT; ++s) {
-            const int slot = tid + s * 512;
-            n[s] = n0 + (slot >> 2);
-            q[s] = slot & 3;
-            const int nn = n[s] < sg.N ? n[s] : 0;
+            const int n = n0 + ((tid + s * 512) >> 2);
+            om.n[s] = n;
+            const int nn = n < sg.N ? n : 0;
             const int oy = nn / sg.Wo, ox = nn - oy * sg.Wo;
-            by[s] = oy * sg.sh - sg.ph;
-            bx[s] = ox * sg.sw - sg.pw;
+            om.by[s] = oy * sg.sh - sg.ph;
+            om.bx[s] = ox * sg.sw - sg.pw;
+            const size_t ob = (size_t)plane * 2 * sg.N + nn;
+            om.dy[s] = offs[ob];
+            om.dx[s] = offs[ob + sg.N];
+            if constexpr (MASK) om.m[s] = msk[(size_t)plane * sg.N + nn];
         }
     }
 
-    // Descriptors and corner gathers of chunk `ch` (K order tap, group,
-    // channel chunk).  offs/msk/xt point at the current image.
-    __device__ __forceinline__ void issue(int ch, const SampleGeo &sg, const T *__restrict__ xt,
-                                          const T *__restrict__ offs,
-                                          const T *__restrict__ msk) {
-        const int cpg = sg.Cgp / KC;
-        const int tg = ch / cpg, cc = ch - tg * cpg;
-        const int tap = tg / sg.G, g = tg - tap * sg.G;
-        const int ki = tap / sg.kw, kj = tap - ki * sg.kw;
+    // Descriptors and corner gathers of the chunk `e` from `om`.
+    __device__ __forceinline__ void issue(const ChunkEnt &e, const SampleGeo &sg,
+                                          const T *__restrict__ xt, const SlotOM<T, SPT> &om) {
 #pragma unroll
         for (int s = 0; s < SPT; ++s) {
-            Corners c;
-            if (n[s] < sg.N) {
-                const size_t ob = ((size_t)g * sg.KK + tap) * 2 * sg.N + n[s];
-                const float dy = to_f32(offs[ob]);
-                const float dx = to_f32(offs[ob + sg.N]);
-                const float mv = msk ? to_f32(msk[((size_t)g * sg.KK + tap) * sg.N + n[s]]) : 1.0f;
-                const float y = (float)(by[s] + ki * sg.dh) + dy;
-                const float x = (float)(bx[s] + kj * sg.dw) + dx;
-                c = make_corners(sample_pos(y, x, sg.H, sg.W), mv, sg.W, sg.cs);
-            } else {
-#pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    c.off[k] = 0;
-                    c.w[k] = 0.0f;
-                }
-            }
-            const int cbase = g * sg.Cgp + cc * KC + q[s] * CPS;
+            const float y = (float)(om.by[s] + e.y) + to_f32(om.dy[s]);
+            const float x = (float)(om.bx[s] + e.z) + to_f32(om.dx[s]);
+            float mv = 1.0f;
+            if constexpr (MASK) mv = to_f32(om.m[s]);
+            mv = om.n[s] < sg.N ? mv : 0.0f;  // pixels past N sample 0
+            const Corners c = make_corners(sample_pos(y, x, sg.H, sg.W), mv, sg.W, sg.cs);
+            const int cbase = e.w + q * CPS;
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
                 w[s][k] = c.w[k];
@@ -125,11 +133,10 @@ template <typename T, int SPT> struct Sampler {
     __device__ __forceinline__ void blend(int s, int u, float *acc) const {
         constexpr int E = Unpack<T>::E;
         float v[E];
-        Unpack<T>::run(raw[s][0][u], v);
 #pragma unroll
-        for (int e = 0; e < E; ++e) acc[e] = w[s][0] * v[e];
+        for (int e = 0; e < E; ++e) acc[e] = 0.0f;
 #pragma unroll
-        for (int k = 1; k < 4; ++k) {
+        for (int k = 0; k < 4; ++k) {
             Unpack<T>::run(raw[s][k][u], v);
 #pragma unroll
             for (int e = 0; e < E; ++e) acc[e] = fmaf(w[s][k], v[e], acc[e]);

@@ -92,6 +92,26 @@ DCN2_API int dcn2_backward(const dcn2_desc *d, const void *input, const void *we
                   void *grad_offset, void *grad_mask, void *grad_weight, void *grad_bias,
                   void *workspace, size_t workspace_bytes, void *stream);
 
+/* Per-stage kernel timing (no counterpart in the reference, whose timing loops
+ * live inside its forward, com_2buffer_cpasyc.cu:334-392).  While enabled on
+ * the calling thread, every stage of dcn2_forward / dcn2_backward is bracketed
+ * by HIP events recorded on the call's stream; dcn2_profile_read() waits for
+ * the recorded events, returns the summed milliseconds and launch count of
+ * one stage, and clears that stage.  Disabled by default; enabling adds two
+ * event records per stage and nothing else. */
+enum dcn2_stage {
+    DCN2_STAGE_FWD_PACK = 0,     /* input / weight repacking of the forward      */
+    DCN2_STAGE_FWD_MAIN = 1,     /* fused sampling + MFMA forward kernel          */
+    DCN2_STAGE_BWD_PACK = 2,     /* repacking and accumulator clearing            */
+    DCN2_STAGE_BWD_COLGRAD = 3,  /* column gradient, grad_offset, grad_mask       */
+    DCN2_STAGE_BWD_GRADW = 4,    /* grad_weight / grad_bias                        */
+    DCN2_STAGE_BWD_GATHER = 5,   /* grad_input accumulation                       */
+    DCN2_STAGE_BWD_FINAL = 6,    /* conversion to the caller's dtype and layout   */
+    DCN2_STAGE_COUNT = 7
+};
+DCN2_API int dcn2_profile_enable(int on);
+DCN2_API int dcn2_profile_read(int stage, double *total_ms, int *launches);
+
 /* Human-readable description of the last failure on the calling thread. */
 DCN2_API const char *dcn2_last_error(void);
 
