@@ -198,13 +198,16 @@ __global__ __launch_bounds__(512) void dcn2_colgrad_kernel(const BwdParams p) {
         f32x16 acc;
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
-        const T *wrow = wt + (size_t)(ch * KC + kb * 32 + (lane & 31)) * p.Mp + wr * MPW +
-                        (lane >> 5) * KPL;
+        // A = W'^T in fragment order (pack_weight_kernel layout 1): the
+        // fragment (row block ch*KC/32 + kb, step ms) is one contiguous run.
+        const T *wrow = wt + ((size_t)(ch * KC / 32 + kb) * (p.Mp / KSTEP) + wr * (MPW / KSTEP)) *
+                                 64 * KPL + lane * KPL;
         for (int mc = 0; mc < nmc; ++mc) {
             if (nmc > 1) load_go(mc);
 #pragma unroll
             for (int s = 0; s < NMS; ++s) {
-                const frag a = *reinterpret_cast<const frag *>(wrow + mc * MCH + s * KSTEP);
+                const frag a = *reinterpret_cast<const frag *>(
+                    wrow + (size_t)(mc * (MCH / KSTEP) + s) * 64 * KPL);
                 acc = M::mma(a, gfr[s], acc);
             }
         }
@@ -463,7 +466,7 @@ __global__ __launch_bounds__(512) void dcn2_gradw_kernel(const BwdParams p) {
     // types (8 registers of 16 bytes); fp32 (64 one-float steps) loads at use.
     constexpr bool PREA = KPL == 8;
     frag a_cur[PREA ? NKS : 1], a_nxt[PREA ? NKS : 1];
-    auto load_a_tile = [&](frag (&a)[PREA ? NKS : 1], int t) {
+    auto load_a_tile = [&](frag (&a)[PREA ? NKS : 1], int t) __attribute__((always_inline)) {
         if constexpr (PREA) {
 #pragma unroll
             for (int ks = 0; ks < NKS; ++ks) load_a(a[ks], t, ks);
@@ -554,22 +557,32 @@ __global__ __launch_bounds__(512) void dcn2_gradw_kernel(const BwdParams p) {
 
 
 // ---------------------------------------------------------------------------
-// grad_input gather.  One block per bucket (image, group, 16x16 cell tile):
-// every record of the bucket adds its masked column-gradient row, times the
-// four bilinear corner weights, into an LDS tile of the (TS+1) x (TS+1)
-// pixels its corners can reach (ds_add, lane = channel).  The tile is then
-// added to grad_input: interior pixels (reachable from this tile's cells only)
-// by a plain read-modify-write, the one-pixel border ring, shared with the
-// neighbouring tiles, by fp32 atomics.  This replaces one global atomic per
-// (sample, corner, channel) -- the reference's col2im scatter, com.cu:553-609
-// -- by one per border pixel and channel.
+// grad_input gather.  One block per bucket (image, group, 16x16 cell tile).
+// The records of the bucket are counting-sorted by cell in LDS; then the
+// cells are visited in four passes by the parity of their (row, column), so
+// that cells handled concurrently have disjoint 2x2 corner footprints.  A
+// lane group (lane = channel) sums the masked column-gradient rows of one
+// cell's records times each of the four bilinear corner weights in registers
+// and adds the four sums to an LDS tile of the (TS+1) x (TS+1) reachable
+// pixels with plain read-modify-writes -- no atomics in the inner loop.  The
+// tile is then added to grad_input: interior pixels (reachable from this
+// tile's cells only) by a plain read-modify-write, the one-pixel border ring,
+// shared with the neighbouring tiles, by fp32 atomics.  This replaces one
+// global atomic per (sample, corner, channel) -- the reference's col2im
+// scatter, com.cu:553-609 -- by one per border pixel and channel.
+constexpr int kGatherCapMax = 8192;  // records of one bucket the LDS sort holds
+
 template <typename T>
 __global__ __launch_bounds__(512) void dcn2_gi_gather_kernel(const BwdParams p) {
-    constexpr int KC = Mma<T>::KC;
-    constexpr int TS = kCellTile, TW = TS + 1;
-    constexpr int RPW = 64 / KC;  // records per wave instruction
-    constexpr int UNR = 4;        // records in flight per lane group
+    constexpr int KC = Mma<T>::KC;  // channels per pass (one lane each)
+    constexpr int TS = kCellTile, TW = TS + 1, NCELL = TS * TS;
+    constexpr int CPW = 64 / KC;    // cells processed side by side per wave
+    constexpr int RPT = kGatherCapMax / 512;
+    constexpr int UNR = 4;
     __shared__ __attribute__((aligned(16))) float acc[TW * TW][KC];
+    __shared__ int ccnt[NCELL];
+    __shared__ int cstart[NCELL + 1];
+    __shared__ unsigned short order[kGatherCapMax];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int nb = p.B * p.G * p.nty * p.ntx;
@@ -583,37 +596,95 @@ __global__ __launch_bounds__(512) void dcn2_gi_gather_kernel(const BwdParams p) 
     const int c = lane % KC, sub = lane / KC;
     float *__restrict__ gi = p.gi_acc + (size_t)b * p.H * p.W * cs + g * p.Cgp;
 
+    // 1. counting sort by cell: rank within the cell from an LDS counter
+    for (int i = tid; i < NCELL; i += 512) ccnt[i] = 0;
+    __syncthreads();
+    int key[RPT];  // (cell << 16) | rank, or -1
+#pragma unroll
+    for (int k = 0; k < RPT; ++k) {
+        const int r = tid + k * 512;
+        key[k] = -1;
+        if (r < count) {
+            const int yx = recs[r].y;
+            const int cy = (int)(short)(yx & 0xffff) - oy, cx = (yx >> 16) - ox;  // in [0, TS)
+            const int cell = cy * TS + cx;
+            key[k] = (cell << 16) | atomicAdd(&ccnt[cell], 1);
+        }
+    }
+    __syncthreads();
+    if (wave == 0) {  // exclusive scan of the 256 counts: 4 per lane + wave scan
+        int v[4], s = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[i] = ccnt[lane * 4 + i];
+            s += v[i];
+        }
+        int incl = s;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const int o = __shfl_up(incl, d, 64);
+            if (lane >= d) incl += o;
+        }
+        int run = incl - s;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            cstart[lane * 4 + i] = run;
+            run += v[i];
+        }
+        if (lane == 63) cstart[NCELL] = run;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < RPT; ++k)
+        if (key[k] >= 0)
+            order[cstart[key[k] >> 16] + (key[k] & 0xffff)] = (unsigned short)(tid + k * 512);
+    __syncthreads();
+
     for (int cc = 0; cc < cpg; ++cc) {
         for (int e = tid; e < TW * TW * KC / 4; e += 512)
             reinterpret_cast<float4 *>(&acc[0][0])[e] = make_float4(0.f, 0.f, 0.f, 0.f);
         __syncthreads();
         const T *__restrict__ cgm = (const T *)p.cgm + cc * KC + c;
-        for (int r0 = (wave * RPW + sub) * UNR; r0 < count; r0 += 8 * RPW * UNR) {
-            int4 rc[UNR];
-            float v[UNR];
+        // 2. four parity passes over the cells
+        for (int par = 0; par < 4; ++par) {
+            const int pyb = par >> 1, pxb = par & 1;
+            for (int i = wave * CPW + sub; i < NCELL / 4; i += 8 * CPW) {
+                const int cyl = 2 * (i / (TS / 2)) + pyb, cxl = 2 * (i % (TS / 2)) + pxb;
+                const int cell = cyl * TS + cxl;
+                const int r0 = cstart[cell], r1 = cstart[cell + 1];
+                float s00 = 0.f, s01 = 0.f, s10 = 0.f, s11 = 0.f;
+                for (int r = r0; r < r1; r += UNR) {
+                    int4 rc[UNR];
+                    float v[UNR];
 #pragma unroll
-            for (int u = 0; u < UNR; ++u)
-                rc[u] = r0 + u < count ? recs[r0 + u] : make_int4(-1, 0, 0, 0);
+                    for (int u = 0; u < UNR; ++u)
+                        rc[u] = r + u < r1 ? recs[order[r + u]] : make_int4(-1, 0, 0, 0);
 #pragma unroll
-            for (int u = 0; u < UNR; ++u)
-                v[u] = rc[u].x >= 0 ? to_f32(cgm[(size_t)rc[u].x * p.Cgp]) : 0.0f;
+                    for (int u = 0; u < UNR; ++u)
+                        v[u] = rc[u].x >= 0 ? to_f32(cgm[(size_t)rc[u].x * p.Cgp]) : 0.0f;
 #pragma unroll
-            for (int u = 0; u < UNR; ++u) {
-                if (rc[u].x < 0) continue;
-                const int y0 = (int)(short)(rc[u].y & 0xffff), x0 = rc[u].y >> 16;
-                const float ly = __int_as_float(rc[u].z), lx = __int_as_float(rc[u].w);
-                const float hy = 1.0f - ly, hx = 1.0f - lx;
-                const int ly0 = y0 - oy, lx0 = x0 - ox;
-                const bool r0v = y0 >= 0, r1v = y0 + 1 < p.H;
-                const bool c0v = x0 >= 0, c1v = x0 + 1 < p.W;
-                float *a = &acc[ly0 * TW + lx0][c];
-                if (r0v && c0v) atomicAdd(a, v[u] * (hy * hx));
-                if (r0v && c1v) atomicAdd(a + KC, v[u] * (hy * lx));
-                if (r1v && c0v) atomicAdd(a + TW * KC, v[u] * (ly * hx));
-                if (r1v && c1v) atomicAdd(a + (TW + 1) * KC, v[u] * (ly * lx));
+                    for (int u = 0; u < UNR; ++u) {
+                        const float ly = __int_as_float(rc[u].z), lx = __int_as_float(rc[u].w);
+                        const float hy = 1.0f - ly, hx = 1.0f - lx;
+                        s00 = fmaf(v[u], hy * hx, s00);
+                        s01 = fmaf(v[u], hy * lx, s01);
+                        s10 = fmaf(v[u], ly * hx, s10);
+                        s11 = fmaf(v[u], ly * lx, s11);
+                    }
+                }
+                // corners of cell (cyl, cxl): local pixels (cyl..cyl+1, cxl..cxl+1)
+                const int Y = oy + cyl, X = ox + cxl;
+                float *a = &acc[cyl * TW + cxl][c];
+                if (r1 > r0) {
+                    if (Y >= 0 && X >= 0) a[0] += s00;
+                    if (Y >= 0 && X + 1 < p.W) a[KC] += s01;
+                    if (Y + 1 < p.H && X >= 0) a[TW * KC] += s10;
+                    if (Y + 1 < p.H && X + 1 < p.W) a[(TW + 1) * KC] += s11;
+                }
             }
+            __syncthreads();
         }
-        __syncthreads();
+        // 3. add the tile to grad_input
         for (int e = tid; e < TW * TW * KC; e += 512) {
             const int pix = e / KC, ch = e - pix * KC;
             const int py = pix / TW, px = pix - py * TW;
@@ -787,7 +858,7 @@ GatherGeo gather_geometry(const Geo &g) {
     const long avg = gg.nbuckets ? (samples + gg.nbuckets - 1) / gg.nbuckets : 0;
     // Room for twice the mean occupancy; a fuller bucket spills its excess to
     // the direct-atomic path, which is slower but equally exact.
-    gg.cap = (int)std::min<long>(2 * avg + 256, (long)kCellTile * kCellTile * g.KK * 4);
+    gg.cap = (int)std::min<long>(2 * avg + 256, kGatherCapMax);
     return gg;
 }
 

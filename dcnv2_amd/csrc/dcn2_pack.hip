@@ -54,7 +54,9 @@ __global__ __launch_bounds__(256) void pack_input_kernel(const T *__restrict__ i
 // One thread per packed element.  layout 0 (forward): MFMA A-fragment order,
 // dst[((rb*nch + ch)*nks + ks)*64 + lane][e] holds W'[32*rb + lane%32]
 // [ch*kc + ks*kstep + (lane/32)*kpl + e], so one wave's fragment load is one
-// contiguous run; layout 1 (backward): the transpose dst[k][m].
+// contiguous run; layout 1 (backward): the same for the transpose W'^T (rows
+// k, reduction m): dst[((kb*(Mp/kstep) + ms)*64 + lane)][e] holds
+// W'[ms*kstep + (lane/32)*kpl + e][32*kb + lane%32].
 // The first nch threads also write the chunk table: for chunk ch of the K
 // order (tap, group, channel chunk of kc channels) tab[ch] = {offset/mask
 // plane g*KK + tap, row term ki*dh, column term kj*dw, channel base
@@ -79,8 +81,15 @@ __global__ __launch_bounds__(256) void pack_weight_kernel(const T *__restrict__ 
     if (idx >= (long)Mp * Kp) return;
     int m, k;
     if (transpose) {
-        k = (int)(idx / Mp);
-        m = (int)(idx - (long)k * Mp);
+        const int nms = Mp / kstep;
+        const int e = (int)(idx % kpl);
+        long r = idx / kpl;
+        const int lane = (int)(r % 64);
+        r /= 64;
+        const int ms = (int)(r % nms);
+        const int kb = (int)(r / nms);
+        k = kb * 32 + (lane & 31);
+        m = ms * kstep + (lane >> 5) * kpl + e;
     } else {
         // decompose the fragment-order index
         const int nks = kc / kstep;
