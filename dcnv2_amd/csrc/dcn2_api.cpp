@@ -120,7 +120,7 @@ BwdWorkspace bwd_workspace(const Geo &g) {
     o += align256((size_t)g.Mp * sizeof(float));
     const GatherGeo gg = gather_geometry(g);
     w.cgm = o;
-    o += align256((size_t)g.B * g.G * g.KK * g.N * g.Cgp * g.esz);
+    o += align256((size_t)gg.nbuckets * gg.cap * g.Cgp * g.esz);
     w.rec = o;
     o += align256((size_t)gg.nbuckets * gg.cap * 16);
     w.cnt = o;

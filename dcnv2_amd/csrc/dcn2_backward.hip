@@ -38,7 +38,7 @@ struct BwdParams {
     int tiles_per_img, splits;
     int go_vec;  // grad_output rows can be read with 16-byte loads (N % 8 == 0, aligned base)
     // grad_input gather: cell-tile buckets (see dcn2_gi_gather_kernel)
-    void *cgm;          // [B*G*KK*N][Cgp] masked column gradient rows, call dtype
+    void *cgm;          // [nbuckets*cap][Cgp] masked column gradient rows, call dtype
     int4 *rec;          // [nbuckets][cap] sample records
     int *cnt;           // [nbuckets] records appended per bucket
     int ntx, nty, cap;  // cell tiles per row / column, bucket capacity
@@ -56,7 +56,7 @@ constexpr int kCellTile = 16;
 struct Desc {
     int off[4];
     float w[4];  // masked bilinear weight of each corner, 0 outside the image
-    int sidx;    // dense sample index ((b*G + g)*KK + tap)*N + n
+    int sidx;    // row of the masked column gradient: bucket*cap + slot
     float m;     // mask value
     int mode;
     int pad;
@@ -227,15 +227,14 @@ __global__ __launch_bounds__(512) void dcn2_colgrad_kernel(const BwdParams p) {
             const bool any = live && (sp.vy0 || sp.vy1) && (sp.vx0 || sp.vx1);
             const int cy = sp.y0 + 1, cx = sp.x0 + 1;
             const int key = ((b * p.G + g) * p.nty + cy / kCellTile) * p.ntx + cx / kCellTile;
-            const int sidx = ((b * p.G + g) * KK + tap) * N + nr;
             const int slot = bucket_append(any && lq == 0, key, p.cnt, p.cap);
+            const int row = key * p.cap + slot;  // bucket-slot row of the column gradient
             if (slot >= 0) {
-                p.rec[(size_t)key * p.cap + slot] =
-                    make_int4(sidx, (sp.y0 & 0xffff) | (int)((unsigned)sp.x0 << 16), __float_as_int(sp.ly),
-                              __float_as_int(sp.lx));
+                p.rec[row] = make_int4(row, (sp.y0 & 0xffff) | (int)((unsigned)sp.x0 << 16),
+                                       __float_as_int(sp.ly), __float_as_int(sp.lx));
             }
             gmode = !any ? 0 : (slot >= 0 ? 1 : 2);
-            gsidx = sidx;
+            gsidx = row;
         }
         if (lq == 0) {
             Desc d;
@@ -558,31 +557,29 @@ __global__ __launch_bounds__(512) void dcn2_gradw_kernel(const BwdParams p) {
 
 // ---------------------------------------------------------------------------
 // grad_input gather.  One block per bucket (image, group, 16x16 cell tile).
-// The records of the bucket are counting-sorted by cell in LDS; then the
-// cells are visited in four passes by the parity of their (row, column), so
-// that cells handled concurrently have disjoint 2x2 corner footprints.  A
-// lane group (lane = channel) sums the masked column-gradient rows of one
-// cell's records times each of the four bilinear corner weights in registers
-// and adds the four sums to an LDS tile of the (TS+1) x (TS+1) reachable
-// pixels with plain read-modify-writes -- no atomics in the inner loop.  The
-// tile is then added to grad_input: interior pixels (reachable from this
-// tile's cells only) by a plain read-modify-write, the one-pixel border ring,
-// shared with the neighbouring tiles, by fp32 atomics.  This replaces one
-// global atomic per (sample, corner, channel) -- the reference's col2im
-// scatter, com.cu:553-609 -- by one per border pixel and channel.
-constexpr int kGatherCapMax = 8192;  // records of one bucket the LDS sort holds
+// The records of the bucket are counting-sorted by cell in LDS, together with
+// their fractional sample coordinates.  Then every pixel of the (TS+1)^2 window
+// the tile's corners can reach is pulled by one lane group (lane = channel):
+// pixel (py, px) is corner 00 of cell (py, px), 01 of (py, px-1), 10 of
+// (py-1, px) and 11 of (py-1, px-1), so its value is the sum over the records
+// of those four cells of (bilinear corner weight) x (masked column-gradient
+// row), computed in a register with up to UNR independent row loads in
+// flight.  Interior pixels (reachable from this tile's cells only) are
+// complete and added by a plain read-modify-write; the one-pixel border ring,
+// shared with the neighbouring tiles, is added with fp32 atomics.  This
+// replaces one global atomic per (sample, corner, channel) -- the reference's
+// col2im scatter, com.cu:553-609 -- by one per border pixel and channel.
+constexpr int kGatherCapMax = 4096;  // records of one bucket the LDS sort holds
 
 template <typename T>
 __global__ __launch_bounds__(512) void dcn2_gi_gather_kernel(const BwdParams p) {
-    constexpr int KC = Mma<T>::KC;  // channels per pass (one lane each)
+    constexpr int KC = Mma<T>::KC;  // channels per pass
     constexpr int TS = kCellTile, TW = TS + 1, NCELL = TS * TS;
-    constexpr int CPW = 64 / KC;    // cells processed side by side per wave
     constexpr int RPT = kGatherCapMax / 512;
-    constexpr int UNR = 4;
-    __shared__ __attribute__((aligned(16))) float acc[TW * TW][KC];
     __shared__ int ccnt[NCELL];
     __shared__ int cstart[NCELL + 1];
-    __shared__ unsigned short order[kGatherCapMax];
+    __shared__ unsigned short sslot[kGatherCapMax];   // bucket slot, sorted by cell
+    __shared__ float2 sfrac[kGatherCapMax];           // (ly, lx), sorted by cell
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int nb = p.B * p.G * p.nty * p.ntx;
@@ -593,21 +590,23 @@ __global__ __launch_bounds__(512) void dcn2_gi_gather_kernel(const BwdParams p) 
     const int4 *__restrict__ recs = p.rec + (size_t)bucket * p.cap;
     const int oy = ty * TS - 1, ox = tx * TS - 1;  // pixel of local (0, 0)
     const int cs = p.G * p.Cgp, cpg = p.Cgp / KC;
-    const int c = lane % KC, sub = lane / KC;
     float *__restrict__ gi = p.gi_acc + (size_t)b * p.H * p.W * cs + g * p.Cgp;
 
-    // 1. counting sort by cell: rank within the cell from an LDS counter
+    // 1. counting sort by cell (cell = local row * TS + local column)
     for (int i = tid; i < NCELL; i += 512) ccnt[i] = 0;
     __syncthreads();
     int key[RPT];  // (cell << 16) | rank, or -1
+    float2 fr[RPT];
 #pragma unroll
     for (int k = 0; k < RPT; ++k) {
         const int r = tid + k * 512;
         key[k] = -1;
+        fr[k] = make_float2(0.f, 0.f);
         if (r < count) {
-            const int yx = recs[r].y;
-            const int cy = (int)(short)(yx & 0xffff) - oy, cx = (yx >> 16) - ox;  // in [0, TS)
+            const int4 rc = recs[r];
+            const int cy = (int)(short)(rc.y & 0xffff) - oy, cx = (rc.y >> 16) - ox;  // [0, TS)
             const int cell = cy * TS + cx;
+            fr[k] = make_float2(__int_as_float(rc.z), __int_as_float(rc.w));
             key[k] = (cell << 16) | atomicAdd(&ccnt[cell], 1);
         }
     }
@@ -635,71 +634,93 @@ __global__ __launch_bounds__(512) void dcn2_gi_gather_kernel(const BwdParams p) 
     }
     __syncthreads();
 #pragma unroll
-    for (int k = 0; k < RPT; ++k)
-        if (key[k] >= 0)
-            order[cstart[key[k] >> 16] + (key[k] & 0xffff)] = (unsigned short)(tid + k * 512);
+    for (int k = 0; k < RPT; ++k) {
+        if (key[k] < 0) continue;
+        const int pos = cstart[key[k] >> 16] + (key[k] & 0xffff);
+        sslot[pos] = (unsigned short)(tid + k * 512);
+        sfrac[pos] = fr[k];
+    }
     __syncthreads();
 
+    // 2. pull every pixel of the window.  A wave takes one pixel at a time;
+    //    its lanes are (record rs, channel group co): lane (rs, co) loads 16
+    //    bytes (EPL channels) of the row of record rs, so one load instruction
+    //    fetches RPB whole rows, and the RPB partial sums of a channel group
+    //    are reduced across lanes at the end of the pixel.
+    constexpr int EPL = 16 / sizeof(T);  // channels per lane per row
+    constexpr int LPR = KC / EPL;        // lanes per row (8)
+    constexpr int RPB = 64 / LPR;        // rows per load instruction (8)
+    static_assert(LPR == 8, "a 16-byte lane slice of a KC-channel row");
+    const int co = lane % LPR, rs = lane / LPR;
     for (int cc = 0; cc < cpg; ++cc) {
-        for (int e = tid; e < TW * TW * KC / 4; e += 512)
-            reinterpret_cast<float4 *>(&acc[0][0])[e] = make_float4(0.f, 0.f, 0.f, 0.f);
-        __syncthreads();
-        const T *__restrict__ cgm = (const T *)p.cgm + cc * KC + c;
-        // 2. four parity passes over the cells
-        for (int par = 0; par < 4; ++par) {
-            const int pyb = par >> 1, pxb = par & 1;
-            for (int i = wave * CPW + sub; i < NCELL / 4; i += 8 * CPW) {
-                const int cyl = 2 * (i / (TS / 2)) + pyb, cxl = 2 * (i % (TS / 2)) + pxb;
-                const int cell = cyl * TS + cxl;
-                const int r0 = cstart[cell], r1 = cstart[cell + 1];
-                float s00 = 0.f, s01 = 0.f, s10 = 0.f, s11 = 0.f;
-                for (int r = r0; r < r1; r += UNR) {
-                    int4 rc[UNR];
-                    float v[UNR];
+        const T *__restrict__ rows = (const T *)p.cgm + ((size_t)bucket * p.cap) * p.Cgp +
+                                     cc * KC + co * EPL;
+        for (int pl = wave; pl < TW * TW; pl += 8) {
+            const int py = pl / TW, px = pl - py * TW;
+            const int Y = oy + py, X = ox + px;
+            if (Y < 0 || Y >= p.H || X < 0 || X >= p.W) continue;
+            // record ranges of the four cells whose corner q is this pixel
+            int beg[4], len[4];
 #pragma unroll
-                    for (int u = 0; u < UNR; ++u)
-                        rc[u] = r + u < r1 ? recs[order[r + u]] : make_int4(-1, 0, 0, 0);
+            for (int q = 0; q < 4; ++q) {
+                const int cy = py - (q >> 1), cx = px - (q & 1);
+                const bool in = cy >= 0 && cy < TS && cx >= 0 && cx < TS;
+                const int cell = cy * TS + cx;
+                beg[q] = in ? cstart[cell] : 0;
+                len[q] = in ? cstart[cell + 1] - beg[q] : 0;
+            }
+            const int e1 = len[0], e2 = e1 + len[1], e3 = e2 + len[2], tot = e3 + len[3];
+            float sum[EPL];
 #pragma unroll
-                    for (int u = 0; u < UNR; ++u)
-                        v[u] = rc[u].x >= 0 ? to_f32(cgm[(size_t)rc[u].x * p.Cgp]) : 0.0f;
+            for (int e = 0; e < EPL; ++e) sum[e] = 0.0f;
+            constexpr int UNR = 2;
+            for (int j0 = 0; j0 < tot; j0 += RPB * UNR) {
+                uint4 raw[UNR];
+                float wgt[UNR];
 #pragma unroll
-                    for (int u = 0; u < UNR; ++u) {
-                        const float ly = __int_as_float(rc[u].z), lx = __int_as_float(rc[u].w);
-                        const float hy = 1.0f - ly, hx = 1.0f - lx;
-                        s00 = fmaf(v[u], hy * hx, s00);
-                        s01 = fmaf(v[u], hy * lx, s01);
-                        s10 = fmaf(v[u], ly * hx, s10);
-                        s11 = fmaf(v[u], ly * lx, s11);
+                for (int u = 0; u < UNR; ++u) {
+                    const int j = j0 + u * RPB + rs;
+                    const int q = (j >= e1) + (j >= e2) + (j >= e3);
+                    const int pos = (q == 0 ? beg[0] + j : q == 1 ? beg[1] + j - e1
+                                    : q == 2 ? beg[2] + j - e2 : beg[3] + j - e3);
+                    wgt[u] = 0.0f;
+                    raw[u] = make_uint4(0, 0, 0, 0);
+                    if (j < tot) {
+                        const float2 f = sfrac[pos];
+                        const float wy = (q & 2) ? f.x : 1.0f - f.x;
+                        const float wx = (q & 1) ? f.y : 1.0f - f.y;
+                        wgt[u] = wy * wx;
+                        raw[u] = *reinterpret_cast<const uint4 *>(rows +
+                                                                  (size_t)sslot[pos] * p.Cgp);
                     }
                 }
-                // corners of cell (cyl, cxl): local pixels (cyl..cyl+1, cxl..cxl+1)
-                const int Y = oy + cyl, X = ox + cxl;
-                float *a = &acc[cyl * TW + cxl][c];
-                if (r1 > r0) {
-                    if (Y >= 0 && X >= 0) a[0] += s00;
-                    if (Y >= 0 && X + 1 < p.W) a[KC] += s01;
-                    if (Y + 1 < p.H && X >= 0) a[TW * KC] += s10;
-                    if (Y + 1 < p.H && X + 1 < p.W) a[(TW + 1) * KC] += s11;
+#pragma unroll
+                for (int u = 0; u < UNR; ++u) {
+                    float v[EPL];
+                    Unpack<T>::run(raw[u], v);
+#pragma unroll
+                    for (int e = 0; e < EPL; ++e) sum[e] = fmaf(wgt[u], v[e], sum[e]);
                 }
             }
-            __syncthreads();
+            if (tot == 0) continue;
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) {
+#pragma unroll
+                for (int d = LPR; d < 64; d <<= 1) sum[e] += __shfl_xor(sum[e], d, 64);
+            }
+            if (rs != 0) continue;
+            float *dst = gi + ((size_t)Y * p.W + X) * cs + cc * KC + co * EPL;
+            const int cvalid = min(EPL, p.Cg - (cc * KC + co * EPL));
+            if (py >= 1 && py <= TS - 1 && px >= 1 && px <= TS - 1) {
+#pragma unroll
+                for (int e = 0; e < EPL; ++e)
+                    if (e < cvalid) dst[e] += sum[e];
+            } else {
+#pragma unroll
+                for (int e = 0; e < EPL; ++e)
+                    if (e < cvalid && sum[e] != 0.0f) unsafeAtomicAdd(dst + e, sum[e]);
+            }
         }
-        // 3. add the tile to grad_input
-        for (int e = tid; e < TW * TW * KC; e += 512) {
-            const int pix = e / KC, ch = e - pix * KC;
-            const int py = pix / TW, px = pix - py * TW;
-            const int Y = oy + py, X = ox + px;
-            if (Y < 0 || Y >= p.H || X < 0 || X >= p.W || cc * KC + ch >= p.Cg) continue;
-            const float val = acc[pix][ch];
-            if (val == 0.0f) continue;
-            float *dst = gi + ((size_t)Y * p.W + X) * cs + cc * KC + ch;
-            const bool interior = py >= 1 && py <= TS - 1 && px >= 1 && px <= TS - 1;
-            if (interior)
-                *dst += val;
-            else
-                unsafeAtomicAdd(dst, val);
-        }
-        __syncthreads();
     }
 }
 
