@@ -1,0 +1,268 @@
+"""Host-side checks that need no GPU.
+
+* the C-ABI library loads and exports every entry point ``include/dcnv2_amd.h``
+  declares;
+* its host-only entry points: output shape, workspace sizes, argument
+  validation and error codes/messages (no kernel is launched by any of them);
+* the Python operator surface: the reference's argument checks raise
+  ``RuntimeError`` (``com.cu:209-213, 760-761``), and there is no CPU
+  fallback;
+* autograd plumbing of ``_DCNv2``/``DCN`` (reference ``dcn_v2_mm.py:15-56,
+  133-137``): with ``_C`` replaced by the CPU oracle, the module's gradients
+  equal the independent grid_sample formulation's, which pins the argument
+  order, the ``(gI, gOff, gMask, gW, gB)`` -> ``(gI, gW, gMask, gOff, gB)``
+  remapping and the chunk/cat/sigmoid split;
+* the workload table and FLOP formulas used by bench.py.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+
+import dcnv2_amd
+from dcnv2_amd import _C, dcn_v2_mm
+from dcnv2_amd.workloads import CONFIGS, make_inputs
+from independent import deform_conv2d_gs
+from oracle import oracle
+from util import rel_err
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "dcnv2_amd.h")
+
+
+@pytest.fixture(scope="module")
+def L():
+    if not os.path.exists(_C.library_path()):
+        from dcnv2_amd import build
+        build.build()
+    return _C.lib()
+
+
+def header_functions():
+    text = open(HEADER).read()
+    return re.findall(r"DCN2_API\s+[\w\s\*]+?\b(dcn2_\w+)\s*\(", text)
+
+
+def desc(B=2, C=8, H=9, W=10, Co=5, kh=3, kw=3, sh=1, sw=1, ph=1, pw=1, dh=1, dw=1, G=1,
+         dtype=0):
+    return _C.Desc(B, C, H, W, Co, kh, kw, sh, sw, ph, pw, dh, dw, G, dtype)
+
+
+def out_hw(L, d):
+    ho, wo = ctypes.c_int32(-1), ctypes.c_int32(-1)
+    rc = L.dcn2_output_shape(ctypes.byref(d), ctypes.byref(ho), ctypes.byref(wo))
+    return rc, ho.value, wo.value
+
+
+# -- the C ABI -----------------------------------------------------------------
+def test_exports_every_declared_symbol(L):
+    names = header_functions()
+    assert set(names) >= {"dcn2_forward", "dcn2_backward", "dcn2_output_shape",
+                          "dcn2_forward_workspace_bytes", "dcn2_backward_workspace_bytes",
+                          "dcn2_last_error", "dcn2_version"}
+    raw = ctypes.CDLL(_C.library_path())
+    for n in names:
+        assert hasattr(raw, n), n
+
+
+def test_version(L):
+    assert L.dcn2_version().decode().startswith("dcnv2_amd")
+
+
+@pytest.mark.parametrize("geo", [
+    dict(H=9, W=10, kh=3, kw=3, sh=1, sw=1, ph=1, pw=1, dh=1, dw=1),
+    dict(H=128, W=128, kh=3, kw=3, sh=2, sw=2, ph=2, pw=2, dh=2, dw=2),
+    dict(H=7, W=5, kh=5, kw=3, sh=1, sw=2, ph=2, pw=0, dh=1, dw=1),
+    dict(H=6, W=6, kh=1, kw=1, sh=1, sw=1, ph=0, pw=0, dh=1, dw=1),
+])
+def test_output_shape_matches_formula(L, geo):
+    d = desc(**geo)
+    rc, ho, wo = out_hw(L, d)
+    assert rc == 0
+    assert ho == oracle.out_size(geo["H"], geo["kh"], geo["sh"], geo["ph"], geo["dh"])
+    assert wo == oracle.out_size(geo["W"], geo["kw"], geo["sw"], geo["pw"], geo["dw"])
+
+
+@pytest.mark.parametrize("bad,code,msg", [
+    (dict(G=3), 1, "divisible"),
+    (dict(dtype=7), 1, "dtype"),
+    (dict(C=0), 1, "shape"),
+    (dict(sh=0), 1, "stride"),
+    (dict(H=2, W=2, ph=0, pw=0), 1, "empty output"),
+    (dict(H=40000, W=4), 4, "32-bit"),
+    (dict(B=70000), 4, "32-bit"),
+])
+def test_invalid_descriptors(L, bad, code, msg):
+    d = desc(**bad)
+    rc, _, _ = out_hw(L, d)
+    assert rc == code
+    assert msg in L.dcn2_last_error().decode()
+    assert L.dcn2_forward_workspace_bytes(ctypes.byref(d)) == 0
+    assert L.dcn2_backward_workspace_bytes(ctypes.byref(d)) == 0
+
+
+def test_workspace_sizes(L):
+    for dtype, esz in ((0, 4), (1, 2), (2, 2)):
+        small, big = desc(dtype=dtype), desc(B=4, dtype=dtype)
+        fs, fb = (L.dcn2_forward_workspace_bytes(ctypes.byref(x)) for x in (small, big))
+        bs, bb = (L.dcn2_backward_workspace_bytes(ctypes.byref(x)) for x in (small, big))
+        assert 0 < fs < fb and 0 < bs < bb
+        assert fs % 256 == 0 and bs % 256 == 0
+        # at least the channels-last input copy (channels padded to the chunk)
+        Cgp = 32 if dtype == 0 else 64
+        assert fs >= 2 * 9 * 10 * Cgp * esz
+    # empty batch still has a valid workspace (weight packing)
+    assert L.dcn2_forward_workspace_bytes(ctypes.byref(desc(B=0))) > 0
+
+
+def test_entry_points_reject_before_any_launch(L):
+    """Error paths that return before touching the device."""
+    d = desc()
+    vp = ctypes.c_void_p
+    fake = vp(0x1000)
+    # invalid descriptor
+    rc = L.dcn2_forward(ctypes.byref(desc(G=3)), fake, fake, None, fake, None, fake,
+                        fake, 1 << 20, None)
+    assert rc == 1
+    # null input pointer
+    rc = L.dcn2_forward(ctypes.byref(d), None, fake, None, fake, None, fake, fake, 1 << 20,
+                        None)
+    assert rc == 1 and "null" in L.dcn2_last_error().decode()
+    # workspace too small / misaligned
+    need = L.dcn2_forward_workspace_bytes(ctypes.byref(d))
+    rc = L.dcn2_forward(ctypes.byref(d), fake, fake, None, fake, None, fake, vp(0x10000),
+                        need - 1, None)
+    assert rc == 2 and str(need) in L.dcn2_last_error().decode()
+    rc = L.dcn2_forward(ctypes.byref(d), fake, fake, None, fake, None, fake, vp(0x10010),
+                        need, None)
+    assert rc == 2
+    # backward: grad_mask must be given exactly when mask is
+    rc = L.dcn2_backward(ctypes.byref(d), fake, fake, fake, fake, fake, fake, fake, None,
+                         fake, None, fake, 1 << 30, None)
+    assert rc == 1 and "grad_mask" in L.dcn2_last_error().decode()
+    need = L.dcn2_backward_workspace_bytes(ctypes.byref(d))
+    rc = L.dcn2_backward(ctypes.byref(d), fake, fake, None, fake, fake, fake, fake, None,
+                         fake, None, vp(0x10000), need - 256, None)
+    assert rc == 2
+
+
+# -- the Python operator surface -------------------------------------------------
+def _cpu_case(dtype=torch.float32):
+    return make_inputs(CONFIGS[0], dtype=dtype, with_grad=True)
+
+
+def test_cpu_tensors_raise_runtime_error():
+    t = _cpu_case()
+    with pytest.raises(RuntimeError, match="GPU"):
+        _C.dcn_v2_forward(t["input"], t["weight"], t["mask"], t["offset"], t["bias"],
+                          1, 1, 1, 1)
+    with pytest.raises(RuntimeError, match="GPU"):
+        _C.dcn_v2_backward(t["input"], t["weight"], t["mask"], t["offset"], t["bias"],
+                           t["grad_output"], 1, 1, 1, 1)
+
+
+def test_module_without_gpu_raises_not_falls_back():
+    m = dcnv2_amd.DCN(4, 4, 3, 1, 1)
+    with pytest.raises(RuntimeError):
+        m(torch.randn(1, 4, 6, 6))
+
+
+# -- autograd plumbing with _C replaced by the CPU oracle -------------------------
+def _oracle_forward(input, weight, mask, offset, bias, sh, sw, ph, pw, dh=1, dw=1, G=1):
+    assert sh == sw and ph == pw and dh == dw
+    out = oracle.dcn_forward(input, weight, mask, offset, bias, sh, ph, dh, G)
+    return torch.from_numpy(out)
+
+
+def _oracle_backward(input, weight, mask, offset, bias, grad_output, sh, sw, ph, pw, dh=1,
+                     dw=1, G=1):
+    gi, goff, gm, gw, gb = oracle.dcn_backward(input, weight, mask, offset, bias, grad_output,
+                                               sh, ph, dh, G)
+    gb = torch.from_numpy(gb) if bias is not None else None
+    gm = torch.from_numpy(gm) if mask is not None else None
+    return [torch.from_numpy(gi), torch.from_numpy(goff), gm, torch.from_numpy(gw), gb]
+
+
+@pytest.fixture
+def oracle_C(monkeypatch):
+    monkeypatch.setattr(dcn_v2_mm._C, "dcn_v2_forward", _oracle_forward)
+    monkeypatch.setattr(dcn_v2_mm._C, "dcn_v2_backward", _oracle_backward)
+
+
+def test_dcn_v2_conv_gradients_in_reference_order(oracle_C):
+    g = torch.Generator().manual_seed(0)
+    f64 = torch.float64
+    x = torch.randn(2, 4, 7, 8, generator=g, dtype=f64)
+    w = torch.randn(3, 4, 3, 3, generator=g, dtype=f64)
+    off = torch.randn(2, 2 * 2 * 9, 4, 4, generator=g, dtype=f64) * 1.5
+    m = torch.rand(2, 2 * 9, 4, 4, generator=g, dtype=f64)
+    b = torch.randn(3, generator=g, dtype=f64)
+    go = torch.randn(2, 3, 4, 4, generator=g, dtype=f64)
+    ours = [t.clone().requires_grad_(True) for t in (x, w, m, off, b)]
+    y = dcnv2_amd.dcn_v2_conv(*ours, 2, 1, 1, 2)
+    y.backward(go)
+    ref = [t.clone().requires_grad_(True) for t in (x, w, off, m, b)]
+    y_ref = deform_conv2d_gs(*ref, stride=2, padding=1, dilation=1, deformable_groups=2)
+    y_ref.backward(go)
+    assert rel_err(y, y_ref) < 1e-12
+    ref_by_name = dict(zip(("input", "weight", "offset", "mask", "bias"), ref))
+    for name, t in zip(("input", "weight", "mask", "offset", "bias"), ours):
+        assert rel_err(t.grad, ref_by_name[name].grad) < 1e-12, name
+
+
+def test_dcn_module_split_and_sigmoid(oracle_C):
+    """DCN: offset = cat(o1, o2), mask = sigmoid(third chunk) of the predictor
+    output; with a non-zero predictor the whole module (predictor included)
+    matches the independent formulation, values and parameter gradients."""
+    torch.manual_seed(1)
+    mod = dcnv2_amd.DCN(4, 3, 3, stride=1, padding=1, dilation=1, deformable_groups=2).double()
+    assert not mod.conv_offset_mask.weight.any()  # zero-initialised, reference :129-131
+    with torch.no_grad():
+        mod.conv_offset_mask.weight.normal_(0, 0.3)
+        mod.conv_offset_mask.bias.normal_(0, 0.3)
+    x = torch.randn(2, 4, 6, 6, dtype=torch.float64, requires_grad=True)
+    y = mod(x)
+    go = torch.randn_like(y)
+    y.backward(go)
+    grads = {n: p.grad.clone() for n, p in mod.named_parameters()}
+    gx = x.grad.clone()
+
+    x2 = x.detach().clone().requires_grad_(True)
+    params = {n: p.detach().clone().requires_grad_(True) for n, p in mod.named_parameters()}
+    om = torch.nn.functional.conv2d(x2, params["conv_offset_mask.weight"],
+                                    params["conv_offset_mask.bias"], padding=1)
+    o1, o2, mk = torch.chunk(om, 3, dim=1)
+    y2 = deform_conv2d_gs(x2, params["weight"], torch.cat((o1, o2), 1), torch.sigmoid(mk),
+                          params["bias"], stride=1, padding=1, dilation=1, deformable_groups=2)
+    y2.backward(go)
+    assert rel_err(y, y2) < 1e-12
+    assert rel_err(gx, x2.grad) < 1e-10
+    for n, p in params.items():
+        assert rel_err(grads[n], p.grad) < 1e-10, n
+
+
+def test_reference_import_shims():
+    import Conv2d
+    import dcn_v2_mm as shim
+    assert Conv2d._C is _C
+    assert shim.DCN is dcnv2_amd.DCN and shim.dcn_v2_conv is dcnv2_amd.dcn_v2_conv
+
+
+# -- workloads ---------------------------------------------------------------
+def test_workload_flops_and_determinism():
+    c1 = CONFIGS[1]
+    assert c1.gemm_flops() == pytest.approx(3.8655e10, rel=1e-4)
+    assert c1.readme_flops() == pytest.approx(1.93878e11, rel=1e-5)
+    assert CONFIGS[3].gemm_flops() == pytest.approx(7.7309e10, rel=1e-4)
+    assert CONFIGS[4].gemm_flops() == pytest.approx(9.6637e9, rel=1e-4)
+    a = make_inputs(CONFIGS[0])
+    b = make_inputs(CONFIGS[0])
+    for k in a:
+        if a[k] is not None:
+            assert torch.equal(a[k], b[k]), k
+    assert np.isfinite(a["offset"].numpy()).all()

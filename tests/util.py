@@ -11,7 +11,7 @@ GRADS = ("grad_input", "grad_offset", "grad_mask", "grad_weight", "grad_bias")
 
 def rel_err(a, ref) -> float:
     if isinstance(a, torch.Tensor):
-        a = a.detach().float().cpu().double().numpy()
+        a = a.detach().cpu().double().numpy()
     if isinstance(ref, torch.Tensor):
         ref = ref.detach().cpu().double().numpy()
     a = np.asarray(a, dtype=np.float64)
