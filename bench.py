@@ -16,6 +16,11 @@ second timed loop.  ``cpu_baseline`` times the float32 CPU oracle
 (oracle/dcn_oracle.c, OpenMP) on a bounded sample of the same workload.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+Profiling aids (not part of the headline line's workload): ``--mode fwd`` runs
+only the forward loops (for ``rocprofv3 --pmc`` passes), ``--copy-mib N``
+first runs one plain device-to-device copy of N MiB, the calibration kernel
+whose FETCH_SIZE/WRITE_SIZE readings scale the forward kernel's.
 """
 from __future__ import annotations
 
@@ -56,14 +61,18 @@ def _stage_avgs(_C, names):
 
 
 def _traffic():
-    """HBM bytes per launch of the forward kernel measured with rocprofv3 PMC
-    counters (profiles/fwd_kernel_traffic.json, see profiles/README.md)."""
-    path = os.path.join(ROOT, "profiles", "fwd_kernel_traffic.json")
+    """HBM bytes per launch of the forward kernel, from the two rocprofv3 PMC
+    passes (FETCH_SIZE, WRITE_SIZE) summarised in
+    profiles/fwd_kernel_traffic_c1.md (its ``hbm_bytes_per_launch:`` line)."""
+    path = os.path.join(ROOT, "profiles", "fwd_kernel_traffic_c1.md")
     try:
         with open(path) as f:
-            return json.load(f).get("hbm_bytes_per_launch")
+            for line in f:
+                if line.startswith("hbm_bytes_per_launch:"):
+                    return int(float(line.split(":", 1)[1]))
     except (OSError, ValueError):
-        return None
+        pass
+    return None
 
 
 def cpu_baseline(w, seconds, threads):
@@ -101,6 +110,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--mode", choices=("full", "fwd"), default="full")
+    ap.add_argument("--copy-mib", type=int, default=0)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU; the batch-sharded multi-GPU path is "
@@ -127,6 +138,14 @@ def main():
     def fwd():
         return _C.dcn_v2_forward(*fargs, *geo)
 
+    if args.copy_mib:
+        n = args.copy_mib << 20
+        src = torch.ones(n, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+
     for _ in range(args.warmup):
         fwd()
     ms = _events_ms(fwd, args.steps, torch)
@@ -140,6 +159,11 @@ def main():
     _C.profile_enable(False)
     kern_ms = fstages["fwd_main"]
     achieved = fwd_w.gemm_flops() / (kern_ms * 1e-3) / 1e12
+
+    if args.mode == "fwd":
+        print(json.dumps({"mode": "fwd", "ms_per_step": round(ms, 5),
+                          "kernel_ms": round(kern_ms, 5)}), flush=True)
+        return
 
     # forward + backward at the same shape (config 2)
     t2 = load(fb_w)
@@ -183,7 +207,7 @@ def main():
                       "forward_backward": {k: round(v, 5) for k, v in bstages.items()}},
         "roofline": {
             "bound": "mfma",
-            "kernel": "dcn2_fwd_kernel<f16,4,2> (fused sampling + 32x32x16 MFMA)",
+            "kernel": "dcn2_fwd_kernel<f16,4,2,2,true> (fused sampling + 32x32x16 MFMA)",
             "achieved": round(achieved, 2),
             "peak": PEAK_FP16_TFLOPS,
             "unit": "TFLOP/s",
