@@ -156,12 +156,20 @@ __global__ __launch_bounds__(512) void dcn2_fwd_kernel(const FwdParams p) {
     //   offset/mask bits of ch+3 -> om[O]     A fragments of ch+1 -> a[O]
     //   corner gathers of ch+2 (om[S]) -> smp[S]
     //   MFMA of ch (a[S], sB[S])              blend of ch+1 (smp[O]) -> sB[O]
+    // Chunk-table entries of ch+2 and ch+3 are held in scalar registers and
+    // the entry of ch+4 is fetched one step ahead, so no step starts by
+    // waiting for a scalar load.
+    ChunkEnt e2 = ent(2), e3 = ent(3);
     auto step = [&](auto s_c, int ch) __attribute__((always_inline)) {
         constexpr int S = decltype(s_c)::value;
         constexpr int O = S ^ 1;
-        const ChunkEnt e3 = ent(ch + 3), e2 = ent(ch + 2);
+        // Loads whose results the next step consumes go first, so that the
+        // in-order load counter lets the next step wait for them without
+        // also waiting for this step's corner gathers.
         smp[0].load_om(n0, e3.x, sg, tid, offs, msk, om[O]);
         load_a(std::integral_constant<int, O>{}, ch + 1);
+        const ChunkEnt e4 = ent(ch + 4);
+        __builtin_amdgcn_sched_barrier(0);
         smp[S].issue(e2, sg, xt, om[S]);
         mfma_chunk(std::integral_constant<int, S>{});
         store_stage(std::integral_constant<int, O>{});
@@ -174,12 +182,14 @@ __global__ __launch_bounds__(512) void dcn2_fwd_kernel(const FwdParams p) {
             __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  // VALU
         }
         __syncthreads();
+        e2 = e3;
+        e3 = e4;
     };
 
     // Prologue: offset/mask bits of chunks 0, 1, 2; gathers of chunks 0 and
     // 1; chunk 0 blended into stage 0.
     {
-        const ChunkEnt e0 = ent(0), e1 = ent(1), e2 = ent(2);
+        const ChunkEnt e0 = ent(0), e1 = ent(1);
         smp[0].load_om(n0, e0.x, sg, tid, offs, msk, om[0]);
         smp[0].load_om(n0, e1.x, sg, tid, offs, msk, om[1]);
         load_a(std::integral_constant<int, 0>{}, 0);
@@ -189,10 +199,12 @@ __global__ __launch_bounds__(512) void dcn2_fwd_kernel(const FwdParams p) {
         store_stage(std::integral_constant<int, 0>{});
         __syncthreads();
     }
-    for (int ch = 0; ch < nch; ch += 2) {
+    int ch = 0;
+    for (; ch + 1 < nch; ch += 2) {
         step(std::integral_constant<int, 0>{}, ch);
-        if (ch + 1 < nch) step(std::integral_constant<int, 1>{}, ch + 1);
+        step(std::integral_constant<int, 1>{}, ch + 1);
     }
+    if (ch < nch) step(std::integral_constant<int, 0>{}, ch);
 
     // Epilogue: + bias, round to T, NCHW store.
     T *out = (T *)p.out + (size_t)b * p.Cout * N;
