@@ -39,12 +39,13 @@ struct FwdParams {
     int ntiles, mtiles, tiles;  // pixel tiles per image, M tiles, B*ntiles*mtiles
 };
 
-template <typename T, int WM, int WN, int JB, bool MASK>
+template <typename T, int WM, int WN, int IB, int JB, bool MASK>
 __global__ __launch_bounds__(512) void dcn2_fwd_kernel(const FwdParams p) {
     using M = Mma<T>;
     using frag = typename M::frag;
     constexpr int KC = M::KC, KPL = M::KPL, KSTEP = M::KSTEP, NKS = KC / KSTEP;
-    constexpr int BN = 32 * JB * WN;            // each wave: 64 rows x 32*JB pixels
+    constexpr int BN = 32 * JB * WN;            // each wave: 32*IB rows x 32*JB pixels
+    constexpr int BM = 32 * IB * WM;
     static_assert(WM * WN == 8, "8 waves");
     constexpr int CPS = KC / 4;                 // channels per sampling slot
     constexpr int U4 = CPS * sizeof(T) / 16;    // 16-byte registers per corner per slot (2)
@@ -63,7 +64,7 @@ __global__ __launch_bounds__(512) void dcn2_fwd_kernel(const FwdParams p) {
     // corner gathers.
     const int t = xcd_remap(blockIdx.x, p.tiles);
     const int mt = t % p.mtiles, nt = (t / p.mtiles) % p.ntiles, b = t / (p.mtiles * p.ntiles);
-    const int n0 = nt * BN, m0 = mt * (64 * WM);
+    const int n0 = nt * BN, m0 = mt * BM;
     const int N = p.Ho * p.Wo, KK = p.kh * p.kw, cs = p.G * p.Cgp;
     const int nch = p.Kp / KC, last = nch - 1;
 
@@ -87,7 +88,7 @@ __global__ __launch_bounds__(512) void dcn2_fwd_kernel(const FwdParams p) {
     smp[0].init(tid);
     smp[1].init(tid);
     SlotOM<T, SPT> om[2];
-    frag a[2][2][NKS];
+    frag a[2][IB][NKS];
 
     auto ent = [&](int ch) __attribute__((always_inline)) { return tab[min(ch, last)]; };
 
@@ -111,24 +112,24 @@ __global__ __launch_bounds__(512) void dcn2_fwd_kernel(const FwdParams p) {
     // A (weight) fragments of rows m0 + wm*64 + i*32 + lane%32, packed in
     // fragment order (pack_weight_kernel layout 0): the fragment (row block
     // rb, chunk ch, step ks) is 64 lanes x KPL contiguous elements.
-    const T *wfrag[2];
+    const T *wfrag[IB];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
-        wfrag[i] = (const T *)p.wp + ((size_t)((m0 + wm * 64 + i * 32) / 32) * nch * NKS * 64 +
+    for (int i = 0; i < IB; ++i)
+        wfrag[i] = (const T *)p.wp + ((size_t)((m0 + wm * 32 * IB + i * 32) / 32) * nch * NKS * 64 +
                                       lane) * KPL;
     auto load_a = [&](auto set_c, int ch) __attribute__((always_inline)) {
         constexpr int SET = decltype(set_c)::value;
         const int c = min(ch, last) * NKS * 64 * KPL;
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < IB; ++i)
 #pragma unroll
             for (int ks = 0; ks < NKS; ++ks)
                 a[SET][i][ks] = *reinterpret_cast<const frag *>(wfrag[i] + c + ks * 64 * KPL);
     };
 
-    f32x16 acc[2][JB];
+    f32x16 acc[IB][JB];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < IB; ++i)
 #pragma unroll
         for (int j = 0; j < JB; ++j)
 #pragma unroll
@@ -146,7 +147,7 @@ __global__ __launch_bounds__(512) void dcn2_fwd_kernel(const FwdParams p) {
 #pragma unroll
         for (int ks = 0; ks < NKS; ++ks)
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
+            for (int i = 0; i < IB; ++i)
 #pragma unroll
                 for (int j = 0; j < JB; ++j)
                     acc[i][j] = M::mma(a[SET][i][ks], bf[ks][j], acc[i][j]);
@@ -177,7 +178,7 @@ __global__ __launch_bounds__(512) void dcn2_fwd_kernel(const FwdParams p) {
         // a slice of the blend / descriptor VALU work and one LDS read.
         __builtin_amdgcn_sched_group_barrier(0x100, JB * NKS, 0);  // all B-fragment reads
 #pragma unroll
-        for (int i = 0; i < 2 * JB * NKS; ++i) {
+        for (int i = 0; i < IB * JB * NKS; ++i) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
             __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  // VALU
         }
@@ -210,10 +211,10 @@ __global__ __launch_bounds__(512) void dcn2_fwd_kernel(const FwdParams p) {
     T *out = (T *)p.out + (size_t)b * p.Cout * N;
     const T *bias = (const T *)p.bias;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < IB; ++i) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            const int m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            const int m = m0 + wm * 32 * IB + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
             if (m >= p.Cout) continue;
             const float bv = bias ? to_f32(bias[m]) : 0.0f;
 #pragma unroll
@@ -225,16 +226,16 @@ __global__ __launch_bounds__(512) void dcn2_fwd_kernel(const FwdParams p) {
     }
 }
 
-template <typename T, int WM, int WN, int JB>
+template <typename T, int WM, int WN, int IB, int JB>
 static hipError_t launch_fwd_t(const Geo &g, const FwdParams &p0, hipStream_t s) {
     FwdParams p = p0;
     p.ntiles = ceil_div(g.N, 32 * JB * WN);
-    p.mtiles = g.Mp / (64 * WM);
+    p.mtiles = g.Mp / (32 * IB * WM);
     p.tiles = g.B * p.ntiles * p.mtiles;
     if (p.mask)
-        dcn2_fwd_kernel<T, WM, WN, JB, true><<<p.tiles, 512, 0, s>>>(p);
+        dcn2_fwd_kernel<T, WM, WN, IB, JB, true><<<p.tiles, 512, 0, s>>>(p);
     else
-        dcn2_fwd_kernel<T, WM, WN, JB, false><<<p.tiles, 512, 0, s>>>(p);
+        dcn2_fwd_kernel<T, WM, WN, IB, JB, false><<<p.tiles, 512, 0, s>>>(p);
     return hipGetLastError();
 }
 
@@ -242,8 +243,8 @@ static hipError_t launch_fwd_t(const Geo &g, const FwdParams &p0, hipStream_t s)
 // waves of 64x32); both sample 128 pixels, one slot per thread.
 template <typename T>
 static hipError_t launch_fwd_dt(const Geo &g, const FwdParams &p, hipStream_t s) {
-    if (g.BM == 256) return launch_fwd_t<T, 4, 2, 2>(g, p, s);
-    return launch_fwd_t<T, 2, 4, 1>(g, p, s);
+    if (g.BM == 256) return launch_fwd_t<T, 8, 1, 1, 4>(g, p, s);
+    return launch_fwd_t<T, 2, 4, 2, 1>(g, p, s);
 }
 
 hipError_t launch_forward(const Geo &g, const void *xt, const void *wp, const void *tab,
