@@ -37,6 +37,7 @@ struct FwdParams {
     void *out;
     int H, W, Cout, kh, kw, sh, sw, ph, pw, dh, dw, G, Cgp, Ho, Wo, Kp;
     int ntiles, mtiles, tiles;  // pixel tiles per image, M tiles, B*ntiles*mtiles
+    int out_vec;                // output rows can be written with 16-byte stores
 };
 
 template <typename T, int WM, int WN, int IB, int JB, bool MASK>
@@ -53,7 +54,14 @@ __global__ __launch_bounds__(512) void dcn2_fwd_kernel(const FwdParams p) {
     constexpr int LDK = KC + 16 / sizeof(T);    // LDS pitch (elements) of one pixel row
     static_assert(U4 == 2, "slot is 32 bytes per corner");
 
-    __shared__ __attribute__((aligned(16))) T sB[2][BN][LDK];
+    // LDS: the two sampled-column stages during the K loop; afterwards the
+    // same memory stages each wave's output tile for 16-byte row stores.
+    constexpr int LDO = 32 * JB + 16 / sizeof(T);  // pitch (elements) of an output row
+    constexpr size_t kStageBytes = sizeof(T) * 2 * BN * LDK;
+    constexpr size_t kOutBytes = sizeof(T) == 2 ? sizeof(T) * 8 * 32 * IB * LDO : 0;
+    __shared__ __attribute__((aligned(16))) char smem[kStageBytes > kOutBytes ? kStageBytes
+                                                                              : kOutBytes];
+    T(&sB)[2][BN][LDK] = *reinterpret_cast<T(*)[2][BN][LDK]>(smem);
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave / WN, wn = wave - wm * WN;
@@ -127,13 +135,19 @@ __global__ __launch_bounds__(512) void dcn2_fwd_kernel(const FwdParams p) {
                 a[SET][i][ks] = *reinterpret_cast<const frag *>(wfrag[i] + c + ks * 64 * KPL);
     };
 
+    // The accumulators start at the bias of their output row, so the
+    // epilogue only rounds and stores.
     f32x16 acc[IB][JB];
+    const T *bias = (const T *)p.bias;
 #pragma unroll
     for (int i = 0; i < IB; ++i)
 #pragma unroll
-        for (int j = 0; j < JB; ++j)
+        for (int r = 0; r < 16; ++r) {
+            const int m = m0 + wm * 32 * IB + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            const float bv = (bias && m < p.Cout) ? to_f32(bias[m]) : 0.0f;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+            for (int j = 0; j < JB; ++j) acc[i][j][r] = bv;
+        }
 
     auto mfma_chunk = [&](auto set_c) __attribute__((always_inline)) {
         constexpr int SET = decltype(set_c)::value;
@@ -207,20 +221,47 @@ __global__ __launch_bounds__(512) void dcn2_fwd_kernel(const FwdParams p) {
     }
     if (ch < nch) step(std::integral_constant<int, 0>{}, ch);
 
-    // Epilogue: + bias, round to T, NCHW store.
+    // Epilogue: round to T and store NCHW.  For 2-byte types with aligned,
+    // 8-divisible rows each wave stages its 32*IB x 32*JB tile in LDS (the K
+    // loop's stages are free after its last barrier) and writes whole 16-byte
+    // row segments; otherwise every lane stores its own elements.
     T *out = (T *)p.out + (size_t)b * p.Cout * N;
-    const T *bias = (const T *)p.bias;
+    if constexpr (sizeof(T) == 2) {
+        if (p.out_vec) {
+            T *so = reinterpret_cast<T *>(smem) + (size_t)wave * 32 * IB * LDO;
+#pragma unroll
+            for (int i = 0; i < IB; ++i)
+#pragma unroll
+                for (int j = 0; j < JB; ++j)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        so[(i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * LDO + j * 32 +
+                           (lane & 31)] = from_f32<T>(acc[i][j][r]);
+            // each row is 32*JB elements = 4*JB segments of 8; a wave
+            // instruction covers 64 segments
+            constexpr int SEG = 4 * JB, ROWS = 32 * IB;
+#pragma unroll
+            for (int it = 0; it < ROWS * SEG / 64; ++it) {
+                const int sidx = it * 64 + lane;
+                const int row = sidx / SEG, seg = sidx - row * SEG;
+                const int m = m0 + wm * ROWS + row, n = n0 + wn * 32 * JB + seg * 8;
+                const uint4 v = *reinterpret_cast<const uint4 *>(so + row * LDO + seg * 8);
+                if (m < p.Cout && n < N)  // N % 8 == 0: a segment is all in or all out
+                    *reinterpret_cast<uint4 *>(out + (size_t)m * N + n) = v;
+            }
+            return;
+        }
+    }
 #pragma unroll
     for (int i = 0; i < IB; ++i) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int m = m0 + wm * 32 * IB + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
             if (m >= p.Cout) continue;
-            const float bv = bias ? to_f32(bias[m]) : 0.0f;
 #pragma unroll
             for (int j = 0; j < JB; ++j) {
                 const int n = n0 + (wn * JB + j) * 32 + (lane & 31);
-                if (n < N) out[(size_t)m * N + n] = from_f32<T>(acc[i][j][r] + bv);
+                if (n < N) out[(size_t)m * N + n] = from_f32<T>(acc[i][j][r]);
             }
         }
     }
@@ -232,6 +273,7 @@ static hipError_t launch_fwd_t(const Geo &g, const FwdParams &p0, hipStream_t s)
     p.ntiles = ceil_div(g.N, 32 * JB * WN);
     p.mtiles = g.Mp / (32 * IB * WM);
     p.tiles = g.B * p.ntiles * p.mtiles;
+    p.out_vec = (g.N % 8 == 0) && (((uintptr_t)p.out & 15) == 0);
     if (p.mask)
         dcn2_fwd_kernel<T, WM, WN, IB, JB, true><<<p.tiles, 512, 0, s>>>(p);
     else
