@@ -181,8 +181,7 @@ int dcn2_forward(const dcn2_desc *d, const void *input, const void *weight, cons
     char *base = (char *)workspace;
     void *xt = base + ws.xt, *wp = base + ws.wp, *tab = base + ws.tab;
     prof_begin(DCN2_STAGE_FWD_PACK, s);
-    if ((rc = check_launch(launch_pack_input(g, input, xt, s), "pack_input"))) return rc;
-    if ((rc = check_launch(launch_pack_weight(g, weight, wp, tab, false, s), "pack_weight")))
+    if ((rc = check_launch(launch_pack(g, input, xt, weight, wp, tab, false, s), "pack")))
         return rc;
     prof_end(DCN2_STAGE_FWD_PACK, s);
     prof_begin(DCN2_STAGE_FWD_MAIN, s);
@@ -213,10 +212,7 @@ int dcn2_backward(const dcn2_desc *d, const void *input, const void *weight, con
     char *base = (char *)workspace;
     void *xt = base + ws.xt, *wt = base + ws.wt, *tab = base + ws.tab;
     prof_begin(DCN2_STAGE_BWD_PACK, s);
-    if (g.B > 0) {
-        if ((rc = check_launch(launch_pack_input(g, input, xt, s), "pack_input"))) return rc;
-    }
-    if ((rc = check_launch(launch_pack_weight(g, weight, wt, tab, true, s), "pack_weight_t")))
+    if ((rc = check_launch(launch_pack(g, input, xt, weight, wt, tab, true, s), "pack")))
         return rc;
     prof_end(DCN2_STAGE_BWD_PACK, s);
     return check_launch(launch_backward(g, xt, wt, tab, offset, mask, grad_output,

@@ -42,10 +42,10 @@ struct GatherGeo {
 };
 GatherGeo gather_geometry(const Geo &g);
 
-// dcn2_pack.hip
-hipError_t launch_pack_input(const Geo &g, const void *input, void *xt, hipStream_t s);
-hipError_t launch_pack_weight(const Geo &g, const void *weight, void *wp, void *tab,
-                              bool transpose, hipStream_t s);
+// dcn2_pack.hip: input -> xt (skipped when B == 0) and weight -> wp + chunk
+// table in one launch; transpose selects the backward's W'^T fragment order.
+hipError_t launch_pack(const Geo &g, const void *input, void *xt, const void *weight, void *wp,
+                       void *tab, bool transpose, hipStream_t s);
 
 // dcn2_forward.hip
 hipError_t launch_forward(const Geo &g, const void *xt, const void *wp, const void *tab,

@@ -1,61 +1,88 @@
-// Repacking kernels that run ahead of the fused forward/backward.
+// Repacking that runs ahead of the fused forward/backward, as one launch:
 //
-// pack_input : NCHW input -> channels-last xt [B][H*W][G*Cgp] with zeroed
-//              padding channels, so a bilinear corner is one contiguous channel
-//              vector (16-byte loads) instead of C scattered scalars.  The
-//              reference samples NCHW directly, one scalar per thread
-//              (com.cu:151-195).
-// pack_weight: [Cout][C][kh][kw] -> [Mp][Kp] (or its transpose [Kp][Mp]) with
-//              K ordered (tap, group, channel) and zero padding, the operand
-//              order of the MFMA A fragments.
+// input : NCHW input -> channels-last xt [B][H*W][G*Cgp] with zeroed padding
+//         channels, so a bilinear corner is one contiguous channel vector
+//         (16-byte loads) instead of C scattered scalars.  The reference
+//         samples NCHW directly, one scalar per thread (com.cu:151-195).
+// weight: [Cout][C][kh][kw] -> MFMA fragment order of W' [Mp][Kp] (or of its
+//         transpose) with K ordered (tap, group, channel) and zero padding,
+//         plus the chunk table.
+//
+// Blocks [0, nin) transpose 64 pixels x CT channels of the input each (CT*esz
+// = 128 bytes, one channel chunk of a pixel); blocks [nin, nin + nw) pack 256
+// weight elements each.  Both halves are independent, so the (small, latency
+// bound) weight packing overlaps the (bandwidth bound) input transpose.
 #include "dcn2_common.h"
 #include "dcn2_kernels.h"
 #include "../../include/dcnv2_amd.h"
 
 namespace dcn2 {
 
-// 64 pixels x 32 padded channels per block, transposed through LDS.
+struct PackParams {
+    const void *in, *w;
+    void *xt, *wp;
+    int4 *tab;
+    int B, C, HW, Cg, Cgp, cs;     // input geometry
+    int pxt, cht, nin;             // pixel tiles, channel tiles per image, input blocks
+    int in_vec;                    // HW % E == 0 and 16-byte aligned input: vector loads
+    int Cout, KK, kw, dh, dw, G;   // weight geometry
+    int kc, kstep, kpl, Mp, Kp;    // MFMA packing
+    int transpose;                 // 0: forward A fragments, 1: backward W'^T fragments
+};
+
+// Input transpose: 64 pixels x CT padded channels per block, 256 threads.
 template <typename T>
-__global__ __launch_bounds__(256) void pack_input_kernel(const T *__restrict__ in,
-                                                         T *__restrict__ xt, int C, int HW,
-                                                         int Cg, int Cgp, int cs) {
-    __shared__ T tile[32][64 + 2];
-    const int px0 = blockIdx.x * 64, cp0 = blockIdx.y * 32, b = blockIdx.z;
+__device__ __forceinline__ void pack_input_block(const PackParams &p, int blk) {
+    constexpr int E = 16 / sizeof(T);     // elements per 16-byte vector
+    constexpr int CT = 128 / sizeof(T);   // channels per block (128 bytes of a pixel)
+    constexpr int LDP = 64 + E;           // LDS pitch (elements) of one channel row
+    __shared__ __attribute__((aligned(16))) T tile[CT][LDP];
+    const T *__restrict__ in = (const T *)p.in;
+    T *__restrict__ xt = (T *)p.xt;
     const int tid = threadIdx.x;
-    {
-        const int pl = tid & 63, px = px0 + pl;
+    const int pt = blk % p.pxt, ct = (blk / p.pxt) % p.cht, b = blk / (p.pxt * p.cht);
+    const int px0 = pt * 64, cp0 = ct * CT;
+
+    // load: CT channel rows of 64 pixels, E pixels per lane
+    constexpr int LPR = 64 / E;  // lanes per channel row
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int cl = (tid >> 6) + 4 * i;
-            const int cp = cp0 + cl;
-            const int g = cp / Cgp, ci = cp - g * Cgp;
-            T v = (T)0.0f;
-            if (ci < Cg && px < HW) v = in[((size_t)b * C + g * Cg + ci) * HW + px];
-            tile[cl][pl] = v;
+    for (int k = 0; k < CT * LPR / 256; ++k) {
+        const int idx = tid + k * 256;
+        const int cl = idx / LPR, po = (idx - cl * LPR) * E;
+        const int cp = cp0 + cl, g = cp / p.Cgp, ci = cp - g * p.Cgp;
+        const bool live = ci < p.Cg;
+        const T *src = in + ((size_t)b * p.C + g * p.Cg + (live ? ci : 0)) * p.HW + px0 + po;
+        if (p.in_vec) {
+            uint4 v = make_uint4(0, 0, 0, 0);
+            if (live && px0 + po < p.HW) v = *reinterpret_cast<const uint4 *>(src);
+            *reinterpret_cast<uint4 *>(&tile[cl][po]) = v;
+        } else {
+#pragma unroll
+            for (int e = 0; e < E; ++e)
+                tile[cl][po + e] = (live && px0 + po + e < p.HW) ? src[e] : (T)0.0f;
         }
     }
     __syncthreads();
-    const int pl = tid >> 2, cq = tid & 3, px = px0 + pl;
-    if (px < HW) {
-        T vals[8];
+    // store: one 16-byte run of E channels of one pixel per lane
+    constexpr int VPP = CT / E;  // vectors per pixel
 #pragma unroll
-        for (int k = 0; k < 8; ++k) vals[k] = tile[cq * 8 + k][pl];
-        T *dst = xt + ((size_t)b * HW + px) * cs + cp0 + cq * 8;
-        if constexpr (sizeof(T) == 2) {
-            *reinterpret_cast<uint4 *>(dst) = __builtin_bit_cast(uint4, vals);
-        } else {
-            const uint4 *src = reinterpret_cast<const uint4 *>(vals);
-            reinterpret_cast<uint4 *>(dst)[0] = src[0];
-            reinterpret_cast<uint4 *>(dst)[1] = src[1];
-        }
+    for (int k = 0; k < 64 * VPP / 256; ++k) {
+        const int idx = tid + k * 256;
+        const int pl = idx / VPP, cg = (idx - pl * VPP) * E;
+        if (px0 + pl >= p.HW) continue;
+        T v[E];
+#pragma unroll
+        for (int e = 0; e < E; ++e) v[e] = tile[cg + e][pl];
+        *reinterpret_cast<uint4 *>(xt + ((size_t)b * p.HW + px0 + pl) * p.cs + cp0 + cg) =
+            __builtin_bit_cast(uint4, v);
     }
 }
 
-// One thread per packed element.  layout 0 (forward): MFMA A-fragment order,
-// dst[((rb*nch + ch)*nks + ks)*64 + lane][e] holds W'[32*rb + lane%32]
-// [ch*kc + ks*kstep + (lane/32)*kpl + e], so one wave's fragment load is one
-// contiguous run; layout 1 (backward): the same for the transpose W'^T (rows
-// k, reduction m): dst[((kb*(Mp/kstep) + ms)*64 + lane)][e] holds
+// One thread per packed weight element.  transpose 0 (forward): MFMA
+// A-fragment order, dst[((rb*nch + ch)*nks + ks)*64 + lane][e] holds
+// W'[32*rb + lane%32][ch*kc + ks*kstep + (lane/32)*kpl + e], so one wave's
+// fragment load is one contiguous run; transpose 1 (backward): the same for
+// W'^T (rows k, reduction m): dst[((kb*(Mp/kstep) + ms)*64 + lane)][e] holds
 // W'[ms*kstep + (lane/32)*kpl + e][32*kb + lane%32].
 // The first nch threads also write the chunk table: for chunk ch of the K
 // order (tap, group, channel chunk of kc channels) tab[ch] = {offset/mask
@@ -63,25 +90,23 @@ __global__ __launch_bounds__(256) void pack_input_kernel(const T *__restrict__ i
 // g*Cgp + cc*kc}; the sampling kernels read it with scalar loads instead of
 // dividing the chunk index every step.
 template <typename T>
-__global__ __launch_bounds__(256) void pack_weight_kernel(const T *__restrict__ w,
-                                                          T *__restrict__ dst, int4 *__restrict__ tab,
-                                                          int Cout, int C, int KK, int kw, int dh,
-                                                          int dw, int G, int Cg, int Cgp, int kc,
-                                                          int kstep, int kpl, int Mp, int Kp,
-                                                          int transpose) {
-    const long idx = (long)blockIdx.x * 256 + threadIdx.x;
-    const int nch = Kp / kc;
-    if (tab && idx < nch) {
-        const int cpg = Cgp / kc;
+__device__ __forceinline__ void pack_weight_block(const PackParams &p, int blk) {
+    const T *__restrict__ w = (const T *)p.w;
+    T *__restrict__ dst = (T *)p.wp;
+    const long idx = (long)blk * 256 + threadIdx.x;
+    const int nch = p.Kp / p.kc;
+    if (p.tab && idx < nch) {
+        const int cpg = p.Cgp / p.kc;
         const int tg = (int)idx / cpg, cc = (int)idx - tg * cpg;
-        const int tap = tg / G, g = tg - tap * G;
-        const int ki = tap / kw, kj = tap - ki * kw;
-        tab[idx] = make_int4(g * KK + tap, ki * dh, kj * dw, g * Cgp + cc * kc);
+        const int tap = tg / p.G, g = tg - tap * p.G;
+        const int ki = tap / p.kw, kj = tap - ki * p.kw;
+        p.tab[idx] = make_int4(g * p.KK + tap, ki * p.dh, kj * p.dw, g * p.Cgp + cc * p.kc);
     }
-    if (idx >= (long)Mp * Kp) return;
+    if (idx >= (long)p.Mp * p.Kp) return;
     int m, k;
-    if (transpose) {
-        const int nms = Mp / kstep;
+    const int kpl = p.kpl, kstep = p.kstep;
+    if (p.transpose) {
+        const int nms = p.Mp / kstep;
         const int e = (int)(idx % kpl);
         long r = idx / kpl;
         const int lane = (int)(r % 64);
@@ -91,8 +116,7 @@ __global__ __launch_bounds__(256) void pack_weight_kernel(const T *__restrict__ 
         k = kb * 32 + (lane & 31);
         m = ms * kstep + (lane >> 5) * kpl + e;
     } else {
-        // decompose the fragment-order index
-        const int nks = kc / kstep;
+        const int nks = p.kc / kstep;
         const int e = (int)(idx % kpl);
         long r = idx / kpl;
         const int lane = (int)(r % 64);
@@ -102,51 +126,70 @@ __global__ __launch_bounds__(256) void pack_weight_kernel(const T *__restrict__ 
         const int ch = (int)(r % nch);
         const int rb = (int)(r / nch);
         m = rb * 32 + (lane & 31);
-        k = ch * kc + ks * kstep + (lane >> 5) * kpl + e;
+        k = ch * p.kc + ks * kstep + (lane >> 5) * kpl + e;
     }
-    const int gc = G * Cgp;
+    const int gc = p.G * p.Cgp;
     const int tap = k / gc, r = k - tap * gc;
-    const int g = r / Cgp, c = r - g * Cgp;
+    const int g = r / p.Cgp, c = r - g * p.Cgp;
     T v = (T)0.0f;
-    if (m < Cout && c < Cg) v = w[((size_t)m * C + g * Cg + c) * KK + tap];
+    if (m < p.Cout && c < p.Cg) v = w[((size_t)m * p.C + g * p.Cg + c) * p.KK + tap];
     dst[idx] = v;
 }
 
 template <typename T>
-static hipError_t pack_input_t(const Geo &g, const void *input, void *xt, hipStream_t s) {
-    const int HW = g.H * g.W;
-    dim3 grid(ceil_div(HW, 64), g.cs / 32, g.B);
-    pack_input_kernel<T><<<grid, 256, 0, s>>>((const T *)input, (T *)xt, g.C, HW, g.Cg, g.Cgp,
-                                              g.cs);
-    return hipGetLastError();
-}
-
-hipError_t launch_pack_input(const Geo &g, const void *input, void *xt, hipStream_t s) {
-    if (g.B == 0) return hipSuccess;
-    switch (g.dtype) {
-    case DCN2_F16: return pack_input_t<f16>(g, input, xt, s);
-    case DCN2_BF16: return pack_input_t<bf16>(g, input, xt, s);
-    default: return pack_input_t<float>(g, input, xt, s);
-    }
+__global__ __launch_bounds__(256) void pack_kernel(const PackParams p) {
+    const int blk = blockIdx.x;
+    if (blk < p.nin)
+        pack_input_block<T>(p, blk);
+    else
+        pack_weight_block<T>(p, blk - p.nin);
 }
 
 template <typename T>
-static hipError_t pack_weight_t(const Geo &g, const void *w, void *dst, void *tab, bool tr,
-                                hipStream_t s) {
-    const long total = (long)g.Mp * g.Kp;
-    pack_weight_kernel<T><<<(unsigned)((total + 255) / 256), 256, 0, s>>>(
-        (const T *)w, (T *)dst, (int4 *)tab, g.Cout, g.C, g.KK, g.kw, g.dh, g.dw, g.G, g.Cg,
-        g.Cgp, g.KC, g.dtype == DCN2_F32 ? 2 : 16, g.dtype == DCN2_F32 ? 1 : 8, g.Mp, g.Kp,
-        tr ? 1 : 0);
+static hipError_t pack_t(const Geo &g, const void *input, void *xt, const void *weight,
+                         void *wp, void *tab, bool transpose, hipStream_t s) {
+    constexpr int E = 16 / sizeof(T), CT = 128 / sizeof(T);
+    PackParams p;
+    p.in = input;
+    p.w = weight;
+    p.xt = xt;
+    p.wp = wp;
+    p.tab = (int4 *)tab;
+    p.B = g.B;
+    p.C = g.C;
+    p.HW = g.H * g.W;
+    p.Cg = g.Cg;
+    p.Cgp = g.Cgp;
+    p.cs = g.cs;
+    p.pxt = ceil_div(p.HW, 64);
+    p.cht = g.cs / CT;  // cs is a multiple of the chunk KC, and KC == CT
+    p.nin = input ? g.B * p.pxt * p.cht : 0;
+    p.in_vec = (p.HW % E == 0) && (((uintptr_t)input & 15) == 0);
+    p.Cout = g.Cout;
+    p.KK = g.KK;
+    p.kw = g.kw;
+    p.dh = g.dh;
+    p.dw = g.dw;
+    p.G = g.G;
+    p.kc = g.KC;
+    p.kstep = g.dtype == DCN2_F32 ? 2 : 16;
+    p.kpl = g.dtype == DCN2_F32 ? 1 : 8;
+    p.Mp = g.Mp;
+    p.Kp = g.Kp;
+    p.transpose = transpose ? 1 : 0;
+    const long nw = ((long)g.Mp * g.Kp + 255) / 256;
+    const long blocks = p.nin + nw;
+    pack_kernel<T><<<(unsigned)blocks, 256, 0, s>>>(p);
     return hipGetLastError();
 }
 
-hipError_t launch_pack_weight(const Geo &g, const void *weight, void *wp, void *tab,
-                              bool transpose, hipStream_t s) {
+hipError_t launch_pack(const Geo &g, const void *input, void *xt, const void *weight, void *wp,
+                       void *tab, bool transpose, hipStream_t s) {
+    if (g.B == 0) input = nullptr;  // weight packing only
     switch (g.dtype) {
-    case DCN2_F16: return pack_weight_t<f16>(g, weight, wp, tab, transpose, s);
-    case DCN2_BF16: return pack_weight_t<bf16>(g, weight, wp, tab, transpose, s);
-    default: return pack_weight_t<float>(g, weight, wp, tab, transpose, s);
+    case DCN2_F16: return pack_t<f16>(g, input, xt, weight, wp, tab, transpose, s);
+    case DCN2_BF16: return pack_t<bf16>(g, input, xt, weight, wp, tab, transpose, s);
+    default: return pack_t<float>(g, input, xt, weight, wp, tab, transpose, s);
     }
 }
 
