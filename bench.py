@@ -207,7 +207,7 @@ def main():
                       "forward_backward": {k: round(v, 5) for k, v in bstages.items()}},
         "roofline": {
             "bound": "mfma",
-            "kernel": "dcn2_fwd_kernel<f16,4,2,2,true> (fused sampling + 32x32x16 MFMA)",
+            "kernel": "dcn2_fwd_kernel (fused bilinear sampling + 32x32x16 f16 MFMA)",
             "achieved": round(achieved, 2),
             "peak": PEAK_FP16_TFLOPS,
             "unit": "TFLOP/s",
