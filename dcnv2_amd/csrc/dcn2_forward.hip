@@ -36,6 +36,7 @@ struct FwdParams {
     const void *xt, *wp, *tab, *offset, *mask, *bias;
     void *out;
     int H, W, Cout, kh, kw, sh, sw, ph, pw, dh, dw, G, Cgp, Ho, Wo, Kp;
+    int Mp;                     // padded output rows of the packed weight
     int ntiles, mtiles, tiles;  // pixel tiles per image, M tiles, B*ntiles*mtiles
     int out_vec;                // output rows can be written with 16-byte stores
 };
@@ -267,6 +268,494 @@ __global__ __launch_bounds__(512) void dcn2_fwd_kernel(const FwdParams p) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Warp-specialised forward for 2-byte types (f16, bf16).
+//
+// The 8 waves of a workgroup split into two roles that run concurrently on
+// every SIMD (waves w and w+4 share SIMD w % 4):
+//   waves 0-3  MFMA waves: each owns 32*IB output rows x all BN = 128 pixels
+//              of the tile, loads its weight fragments from the fragment-
+//              ordered packed weight and runs the 32x32x16 MFMAs over the LDS
+//              stage of the current chunk;
+//   waves 4-7  sampler waves: the bilinear descriptor of every (pixel, chunk)
+//              is computed by one pair of sampler threads three chunks ahead
+//              and put in an LDS ring; two chunks ahead every sampler lane
+//              reads the descriptors of its four pixels and issues their
+//              corner gathers; one chunk ahead it blends them into the free
+//              LDS stage.
+// One barrier per chunk hands a stage from the samplers to the MFMA waves.
+// The matrix cores and the blend VALU then overlap across waves instead of
+// alternating inside one wave.  The workgroup is persistent: it walks its
+// tiles back to back (tile k+1's sampling pipeline starts while tile k's last
+// chunk is multiplied), with tiles dispatched XCD-aware as in xcd_remap.
+//
+// Gather lane map: 8 consecutive lanes read the 8 16-byte pieces of one
+// corner of one pixel (64 channels x 2 bytes = one 128-byte line), so a wave
+// instruction touches 8 lines.  Measured on MI355X, L2-resident 128-byte
+// lines stream at ~50 B/clk/CU this way against ~30 B/clk/CU with 2 lanes
+// per line: the vector L1 handles about one line per clock per instruction.
+// ---------------------------------------------------------------------------
+
+// Descriptor of one (pixel, chunk) in the LDS ring: the four corner offsets
+// (elements, 0 outside the image) and the four mask-folded corner weights,
+// as packed (w, w) f16 pairs for f16 and as floats for bf16.  Half h (16
+// bytes) holds corners 2h and 2h+1.
+struct RingHalf {
+    int o0, o1;
+    uint32_t w0, w1;
+};
+struct RingDesc {
+    RingHalf h[2];
+};
+
+template <typename T> struct Blend8;
+template <> struct Blend8<f16> {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    static __device__ __forceinline__ uint4 weights(const float (&w)[4]) {
+        uint32_t o[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const _Float16 hw = (_Float16)w[q];
+            o[q] = __builtin_bit_cast(uint32_t, h2{hw, hw});
+        }
+        return make_uint4(o[0], o[1], o[2], o[3]);
+    }
+    // packed f16 FMAs, two channels per instruction, with f16 corner weights
+    // (in [0, 1]); the result is rounded to f16 for the MFMA anyway.
+    static __device__ __forceinline__ uint4 run(const uint4 (&r)[4], uint4 wd) {
+        const h2 wq[4] = {__builtin_bit_cast(h2, wd.x), __builtin_bit_cast(h2, wd.y),
+                          __builtin_bit_cast(h2, wd.z), __builtin_bit_cast(h2, wd.w)};
+        const uint32_t *c0 = reinterpret_cast<const uint32_t *>(&r[0]);
+        const uint32_t *c1 = reinterpret_cast<const uint32_t *>(&r[1]);
+        const uint32_t *c2 = reinterpret_cast<const uint32_t *>(&r[2]);
+        const uint32_t *c3 = reinterpret_cast<const uint32_t *>(&r[3]);
+        uint32_t o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            h2 a = __builtin_bit_cast(h2, c0[e]) * wq[0];
+            a = __builtin_elementwise_fma(__builtin_bit_cast(h2, c1[e]), wq[1], a);
+            a = __builtin_elementwise_fma(__builtin_bit_cast(h2, c2[e]), wq[2], a);
+            a = __builtin_elementwise_fma(__builtin_bit_cast(h2, c3[e]), wq[3], a);
+            o[e] = __builtin_bit_cast(uint32_t, a);
+        }
+        return make_uint4(o[0], o[1], o[2], o[3]);
+    }
+};
+template <> struct Blend8<bf16> {
+    static __device__ __forceinline__ uint4 weights(const float (&w)[4]) {
+        return make_uint4(__float_as_uint(w[0]), __float_as_uint(w[1]), __float_as_uint(w[2]),
+                          __float_as_uint(w[3]));
+    }
+    // fp32 blend (bf16 -> fp32 is a shift), rounded to bf16 once.
+    static __device__ __forceinline__ uint4 run(const uint4 (&r)[4], uint4 wd) {
+        const float w[4] = {__uint_as_float(wd.x), __uint_as_float(wd.y), __uint_as_float(wd.z),
+                            __uint_as_float(wd.w)};
+        float acc[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            float v[8];
+            Unpack<bf16>::run(r[q], v);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[e] = fmaf(w[q], v[e], acc[e]);
+        }
+        return pack16<bf16>(acc);
+    }
+};
+
+// Rows of the LDS bias table of the warp-specialised forward.
+constexpr int kBiasRows = 1024;
+
+template <typename T, int IB, bool MASK>
+__global__ __launch_bounds__(512) void dcn2_fwd_ws_kernel(const FwdParams p) {
+    using M = Mma<T>;
+    using frag = typename M::frag;
+    constexpr int KC = 64, KPL = 8, KSTEP = 16, NKS = 4;
+    constexpr int BN = 128, JB = 4;      // tile pixels; 32-pixel blocks per MFMA wave
+    constexpr int ROWS = 32 * IB;        // output rows per MFMA wave
+    constexpr int LDK = KC + 8;          // stage pitch (elements): 144 B, conflict-free fragments
+    constexpr int LDO = BN + 8;          // epilogue staging pitch (elements)
+    static_assert(sizeof(T) == 2, "2-byte types only");
+
+    __shared__ __attribute__((aligned(16))) T sB[2][BN][LDK];
+    __shared__ __attribute__((aligned(16))) T sO[4][ROWS][LDO];
+    __shared__ RingDesc ring[2][BN];
+    __shared__ float sBias[kBiasRows];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    // Role election: the MFMA waves must sit on four different SIMDs (two
+    // MFMA waves on one SIMD would halve the matrix rate), and the hardware
+    // does not promise which SIMD a wave of the workgroup lands on.  At this
+    // register count a SIMD holds at most two of the eight waves, so every
+    // SIMD holds exactly two: the first to arrive takes the MFMA role and
+    // the other the sampler role; rw (0..3) = SIMD id indexes the role.
+    __shared__ int simd_seen[4];
+    if (tid < 4) simd_seen[tid] = 0;
+    __syncthreads();
+    int rw;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID, 4, 2)" : "=s"(rw));
+    int rank = 0;
+    if (lane == 0) rank = atomicAdd(&simd_seen[rw], 1);
+    const bool mfma_role = __builtin_amdgcn_readfirstlane(__shfl(rank, 0)) == 0;
+    const int N = p.Ho * p.Wo, KK = p.kh * p.kw, cs = p.G * p.Cgp;
+    const int nch = p.Kp / KC, last = nch - 1;
+    const int ntile = p.tiles, G = gridDim.x;
+    // this workgroup's tiles are the dispatch ids blockIdx.x + k*G, k = 0..
+    const int my_tiles = blockIdx.x < ntile ? (ntile - 1 - blockIdx.x) / G + 1 : 0;
+    const int S = my_tiles * nch;  // pipeline steps (chunks) of this workgroup
+    // The chunk table is read through the constant address space: with a
+    // wave-uniform index that makes every read a scalar load, which the
+    // vector-memory counter (and so the corner gathers in flight) never waits on.
+    typedef const __attribute__((address_space(4))) int *ConstTab;
+    const ConstTab tabi = (ConstTab)(uintptr_t)p.tab;
+    auto tab_ent = [&](int ch) __attribute__((always_inline)) {
+        return make_int4(tabi[4 * ch], tabi[4 * ch + 1], tabi[4 * ch + 2], tabi[4 * ch + 3]);
+    };
+
+    // Pipeline cursor: position (k-th tile of this workgroup, chunk ch) of
+    // one pipeline point, advanced by one chunk per step.  Positions past the
+    // last tile stay on the last tile, so look-ahead loads remain in bounds.
+    // Every workgroup walks the chunks of its tiles in the same cyclic order
+    // but from its own starting chunk rot, so the tile ends (and the output
+    // stores they issue) of different workgroups are spread over time instead
+    // of hitting HBM all at once.  j counts the chunks done in the tile.
+    const int rot = blockIdx.x % nch;
+    struct Cursor { int k, j, ch, b, n0, m0; };
+    // Cursor fields are wave-uniform; readfirstlane keeps them in SGPRs.
+    // Otherwise (the role branch is divergent code to the compiler) they
+    // live in VGPRs, the chunk-table reads become vector loads, and waiting
+    // for one of those waits for every corner gather issued before it.
+    auto uni = [](int v) __attribute__((always_inline)) { return __builtin_amdgcn_readfirstlane(v); };
+    auto set_tile = [&](Cursor &c) __attribute__((always_inline)) {
+        const int t = xcd_remap(blockIdx.x + min(c.k, my_tiles - 1) * G, ntile);
+        const int mt = t % p.mtiles, r = t / p.mtiles;
+        c.n0 = uni((r % p.ntiles) * BN);
+        c.b = uni(r / p.ntiles);
+        c.m0 = uni(mt * 4 * ROWS);
+    };
+    auto cursor = [&](int g) __attribute__((always_inline)) {
+        Cursor c;
+        c.k = uni(g / nch);
+        c.j = uni(g - c.k * nch);
+        c.ch = uni(c.j + rot < nch ? c.j + rot : c.j + rot - nch);
+        set_tile(c);
+        return c;
+    };
+    // Advances c by one chunk; on a tile change refreshes the tile fields and
+    // runs on_tile() to refresh the caller's per-tile state.  The empty
+    // volatile asm keeps the (rare) tile change a real branch: if-converted,
+    // its divisions would run every step on the scalar unit.
+    auto advance = [&](Cursor &c, auto &&on_tile) __attribute__((always_inline)) {
+        c.ch = uni(c.ch + 1 == nch ? 0 : c.ch + 1);
+        c.j = uni(c.j + 1);
+        if (c.j == nch) {
+            asm volatile("");
+            c.j = 0;
+            c.k = uni(c.k + 1);
+            set_tile(c);
+            on_tile();
+        }
+    };
+    auto no_tile = [] {};
+
+    if (mfma_role) {
+        // ------------------------------------------------------------ MFMA waves
+        // Two sets of A fragments: the set of chunk g+1 is loaded at the top
+        // of step g, ahead of the MFMAs of chunk g, so it has a whole step to
+        // land.  (Left to itself the scheduler sinks the loads to the end of
+        // the step, which exposes their full latency every step.)
+        frag a[2][IB][NKS];
+        f32x16 acc[IB][JB];
+        const T *bias = (const T *)p.bias;
+        const T *wbase = (const T *)p.wp + (size_t)lane * KPL;
+        // Bias of this wave's rows of every M tile in LDS (fp32, 0 past Cout;
+        // the host guarantees Mp <= kBiasRows), so starting a tile never waits
+        // on a global load queued behind the A loads in flight.  Each wave
+        // writes and reads only its own rows: no barrier needed.
+        for (int m = lane; m < p.Mp; m += 64)
+            if ((m / ROWS) % 4 == rw) sBias[m] = (bias && m < p.Cout) ? to_f32(bias[m]) : 0.0f;
+        // The MFMAs compute the transposed tile D^T[n][m] (the weight
+        // fragment is the B operand, the sampled columns the A operand; both
+        // operands have the same register layout), so lane l holds output
+        // row m = i*32 + l%32 and, in acc[r], pixel n = j*32 + 8*(r/4) +
+        // 4*(l/32) + r%4: four consecutive pixels of one row per r/4.
+        auto init_acc = [&](int m0) __attribute__((always_inline)) {
+#pragma unroll
+            for (int i = 0; i < IB; ++i) {
+                const float bv = sBias[m0 + rw * ROWS + i * 32 + (lane & 31)];
+#pragma unroll
+                for (int j = 0; j < JB; ++j)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) acc[i][j][r] = bv;
+            }
+        };
+        // A fragments at cursor c: rows m0 + rw*ROWS + i*32 + lane%32 of chunk
+        // c.ch; wrow = first fragment of this wave's rows of the next tile's M block
+        const T *wrow;
+        auto set_wrow = [&](const Cursor &c) __attribute__((always_inline)) {
+            wrow = wbase + (size_t)((c.m0 + rw * ROWS) / 32) * nch * NKS * 64 * KPL;
+        };
+        auto load_a = [&](auto set_c, const Cursor &c) __attribute__((always_inline)) {
+            constexpr int SET = decltype(set_c)::value;
+            const T *w0 = wrow + (size_t)c.ch * NKS * 64 * KPL;
+#pragma unroll
+            for (int i = 0; i < IB; ++i)
+#pragma unroll
+                for (int ks = 0; ks < NKS; ++ks)
+                    a[SET][i][ks] = *reinterpret_cast<const frag *>(
+                        w0 + ((size_t)i * nch * NKS + ks) * 64 * KPL);
+        };
+        auto mfma_stage = [&](auto set_c) __attribute__((always_inline)) {
+            constexpr int SET = decltype(set_c)::value;
+            frag bf[2][JB];
+#pragma unroll
+            for (int j = 0; j < JB; ++j)
+                bf[0][j] = *reinterpret_cast<const frag *>(
+                    &sB[SET][j * 32 + (lane & 31)][(lane >> 5) * KPL]);
+#pragma unroll
+            for (int ks = 0; ks < NKS; ++ks) {
+                if (ks + 1 < NKS) {
+#pragma unroll
+                    for (int j = 0; j < JB; ++j)
+                        bf[(ks + 1) & 1][j] = *reinterpret_cast<const frag *>(
+                            &sB[SET][j * 32 + (lane & 31)][(ks + 1) * KSTEP + (lane >> 5) * KPL]);
+                }
+#pragma unroll
+                for (int i = 0; i < IB; ++i)
+#pragma unroll
+                    for (int j = 0; j < JB; ++j)
+                        acc[i][j] = M::mma(bf[ks & 1][j], a[SET][i][ks], acc[i][j]);
+            }
+        };
+        // Output tile of this wave: round to T, stage in LDS, 16-byte row stores.
+        auto store_tile = [&](const Cursor &c) __attribute__((always_inline)) {
+            T *out = (T *)p.out + (size_t)c.b * p.Cout * N;
+            if (p.out_vec) {
+                // four consecutive pixels of a row -> one 8-byte LDS write
+                T(&so)[ROWS][LDO] = sO[rw];
+#pragma unroll
+                for (int i = 0; i < IB; ++i)
+#pragma unroll
+                    for (int j = 0; j < JB; ++j)
+#pragma unroll
+                        for (int rq = 0; rq < 4; ++rq) {
+                            T v4[4];
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) v4[e] = from_f32<T>(acc[i][j][rq * 4 + e]);
+                            *reinterpret_cast<uint2 *>(&so[i * 32 + (lane & 31)][j * 32 + 8 * rq + 4 * (lane >> 5)]) =
+                                __builtin_bit_cast(uint2, v4);
+                        }
+                // a wave instruction covers 64 / SEG whole rows of SEG 16-byte segments
+                constexpr int SEG = BN / 8, RPI = 64 / SEG;
+                const int seg = lane % SEG, r0 = lane / SEG;
+                const int n = c.n0 + seg * 8;
+                T *orow = out + (size_t)(c.m0 + rw * ROWS + r0) * N + n;
+#pragma unroll
+                for (int it = 0; it < ROWS / RPI; ++it) {
+                    const int m = c.m0 + rw * ROWS + it * RPI + r0;
+                    const uint4 v = *reinterpret_cast<const uint4 *>(&so[it * RPI + r0][seg * 8]);
+                    if (m < p.Cout && n < N)  // N % 8 == 0: a segment is all in or all out
+                        *reinterpret_cast<uint4 *>(orow + (size_t)it * RPI * N) = v;
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < IB; ++i) {
+                    const int m = c.m0 + rw * ROWS + i * 32 + (lane & 31);
+                    if (m >= p.Cout) continue;
+#pragma unroll
+                    for (int j = 0; j < JB; ++j)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) {
+                            const int n = c.n0 + j * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                            if (n < N) out[(size_t)m * N + n] = from_f32<T>(acc[i][j][r]);
+                        }
+                }
+            }
+        };
+        Cursor cur = cursor(0), nxt = cursor(1);  // chunk being multiplied, chunk loaded next
+        auto step = [&](auto s_c) __attribute__((always_inline)) {
+            constexpr int S_ = decltype(s_c)::value;
+            load_a(std::integral_constant<int, S_ ^ 1>{}, nxt);
+            __builtin_amdgcn_sched_barrier(0);
+            mfma_stage(std::integral_constant<int, S_>{});
+            if (cur.j == last) {  // tile done: write it, start the next one at its bias
+                store_tile(cur);
+                if (nxt.k < my_tiles) init_acc(nxt.m0);
+            }
+            advance(cur, no_tile);
+            advance(nxt, [&] { set_wrow(nxt); });
+            __syncthreads();
+        };
+        init_acc(cur.m0);
+        set_wrow(cur);
+        load_a(std::integral_constant<int, 0>{}, cur);
+        set_wrow(nxt);
+        // prologue: the samplers fill the descriptor ring and stage 0
+        __syncthreads();
+        __syncthreads();
+        __syncthreads();
+        int g = 0;
+        for (; g + 1 < S; g += 2) {
+            step(std::integral_constant<int, 0>{});
+            step(std::integral_constant<int, 1>{});
+        }
+        if (g < S) step(std::integral_constant<int, 0>{});
+    } else {
+        // --------------------------------------------------------- sampler waves
+        const int st = rw * 64 + lane;                // 0..255
+        const int cg = lane & 7;                      // 16-byte piece (8 channels) of a corner
+        const int pbase = rw * 32 + (lane >> 3);      // slot s covers pixel pbase + 8*s
+        // descriptor work: threads 2p, 2p+1 both evaluate pixel p of the next
+        // descriptor chunk and write half of it each (no divergent branch in
+        // the step, so the compiler's load counting stays exact)
+        const int dpix = st >> 1, dhalf = st & 1;
+        uint4 raw[2][4][4];   // [set][slot][corner]
+        uint4 wts[2][4];      // [set][slot] corner weights
+        // offsets/mask of the next descriptor chunk (raw bits) with the output
+        // position of pixel dpix in the tile they belong to
+        int n_om, by_om, bx_om;
+        T dy_om, dx_om, m_om;
+
+        // Per-tile state of the offset-load point: offset/mask planes of the
+        // image and the output position of pixel dpix.
+        const T *offb, *mskb;
+        int n_t, nn_t, by_t, bx_t;
+        auto set_om_tile = [&](const Cursor &c) __attribute__((always_inline)) {
+            offb = (const T *)p.offset + (size_t)c.b * p.G * KK * 2 * N;
+            mskb = MASK ? (const T *)p.mask + (size_t)c.b * p.G * KK * N : nullptr;
+            n_t = c.n0 + dpix;
+            nn_t = n_t < N ? n_t : 0;
+            const int oy = nn_t / p.Wo, ox = nn_t - oy * p.Wo;
+            by_t = oy * p.sh - p.ph;
+            bx_t = ox * p.sw - p.pw;
+        };
+        // Per-tile state of the gather point: a buffer resource over the
+        // image's channels-last input (byte offsets are 32-bit, and a read
+        // past the image returns 0).
+        const uint32_t img_bytes = (uint32_t)((size_t)p.H * p.W * cs * sizeof(T));
+        __amdgpu_buffer_rsrc_t xrs;
+        auto set_x_tile = [&](const Cursor &c) __attribute__((always_inline)) {
+            const T *xb = (const T *)p.xt + (size_t)c.b * p.H * p.W * cs;
+            xrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<T *>(xb), (short)0, (int)img_bytes,
+                                                    0x00020000);
+        };
+
+        // offset/mask bits of pixel dpix at cursor c (kept raw until used)
+        auto load_om = [&](const Cursor &c) __attribute__((always_inline)) {
+            const int plane = tabi[4 * c.ch];
+            n_om = n_t;
+            by_om = by_t;
+            bx_om = bx_t;
+            const size_t ob = (size_t)plane * 2 * N + nn_t;
+            dy_om = offb[ob];
+            dx_om = offb[ob + N];
+            if constexpr (MASK) m_om = mskb[(size_t)plane * N + nn_t];
+        };
+        // descriptor of pixel dpix at cursor c -> ring slot R (this thread's
+        // half); corner offsets in bytes
+        auto put_desc = [&](int R, const Cursor &c) __attribute__((always_inline)) {
+            const ChunkEnt e = tab_ent(c.ch);
+            const float y = (float)(by_om + e.y) + to_f32(dy_om);
+            const float x = (float)(bx_om + e.z) + to_f32(dx_om);
+            float mv = 1.0f;
+            if constexpr (MASK) mv = to_f32(m_om);
+            mv = n_om < N ? mv : 0.0f;  // pixels past N sample 0
+            const Corners cr = make_corners(sample_pos(y, x, p.H, p.W), mv, p.W, cs);
+            const uint4 wq = Blend8<T>::weights(cr.w);
+            RingHalf hd;
+            hd.o0 = (dhalf ? cr.off[2] : cr.off[0]) * (int)sizeof(T);
+            hd.o1 = (dhalf ? cr.off[3] : cr.off[1]) * (int)sizeof(T);
+            hd.w0 = dhalf ? wq.z : wq.x;
+            hd.w1 = dhalf ? wq.w : wq.y;
+            ring[R][dpix].h[dhalf] = hd;
+        };
+        // corner gathers of the four slots at cursor c (descriptors in ring slot R) -> set SET
+        typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+        auto gather = [&](int off, int soff) __attribute__((always_inline)) {
+            const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(xrs, off + cg * 16, soff, 0);
+            return make_uint4(v.x, v.y, v.z, v.w);
+        };
+        auto issue = [&](auto set_c, int R, const Cursor &c) __attribute__((always_inline)) {
+            constexpr int SET = decltype(set_c)::value;
+            const int soff = tabi[4 * c.ch + 3] * (int)sizeof(T);  // chunk's first channel
+#pragma unroll
+            for (int sl = 0; sl < 4; ++sl) {
+                const RingDesc d = ring[R][pbase + 8 * sl];
+                wts[SET][sl] = make_uint4(d.h[0].w0, d.h[0].w1, d.h[1].w0, d.h[1].w1);
+                raw[SET][sl][0] = gather(d.h[0].o0, soff);
+                raw[SET][sl][1] = gather(d.h[0].o1, soff);
+                raw[SET][sl][2] = gather(d.h[1].o0, soff);
+                raw[SET][sl][3] = gather(d.h[1].o1, soff);
+            }
+        };
+        auto blend_store = [&](auto set_c) __attribute__((always_inline)) {
+            constexpr int SET = decltype(set_c)::value;
+#pragma unroll
+            for (int sl = 0; sl < 4; ++sl)
+                *reinterpret_cast<uint4 *>(&sB[SET][pbase + 8 * sl][cg * 8]) =
+                    Blend8<T>::run(raw[SET][sl], wts[SET][sl]);
+        };
+        // Chunk c uses ring slot, gather set and LDS stage c & 1.  Step g:
+        //   gathers of g+2 (ring (g+2)&1) -> set g&1;
+        //   descriptors of g+3 -> ring (g+3)&1, then the offsets of g+4;
+        //   blend of g+1 (set (g+1)&1) -> stage (g+1)&1;
+        // with the gathers interleaved into the VALU work so that the vector
+        // memory pipe is fed through the whole step.
+        Cursor ci = cursor(2), cd = cursor(3), co = cursor(4);  // issue, descriptor, offset points
+        auto step = [&](auto s_c) __attribute__((always_inline)) {
+            constexpr int S_ = decltype(s_c)::value;
+            issue(std::integral_constant<int, S_>{}, S_, ci);
+            put_desc(S_ ^ 1, cd);
+            load_om(co);
+            blend_store(std::integral_constant<int, S_ ^ 1>{});
+            __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);  // ring reads
+#pragma unroll
+            for (int q = 0; q < 5; ++q) {
+                __builtin_amdgcn_sched_group_barrier(0x020, 4, 0);  // gathers / offset loads
+                __builtin_amdgcn_sched_group_barrier(0x002, 20, 0);  // VALU
+            }
+            advance(ci, [&] { set_x_tile(ci); });
+            advance(cd, no_tile);
+            advance(co, [&] { set_om_tile(co); });
+            __syncthreads();
+        };
+        // (S >= 1: the grid never exceeds the tile count)
+        // ring <- descriptors of chunks 0 and 1; offsets of chunk 2
+        {
+            Cursor c0 = cursor(0), c1 = cursor(1), c2 = cursor(2), c3 = cursor(3);
+            set_om_tile(c0);
+            load_om(c0);
+            put_desc(0, c0);
+            set_om_tile(c1);
+            load_om(c1);
+            put_desc(1, c1);
+            set_om_tile(c2);
+            load_om(c2);
+            __syncthreads();
+            set_x_tile(c0);
+            issue(std::integral_constant<int, 0>{}, 0, c0);
+            __syncthreads();  // ring slot 0 is read: chunk 2 may replace chunk 0
+            put_desc(0, c2);
+            set_om_tile(c3);
+            load_om(c3);
+            __builtin_amdgcn_sched_barrier(0);
+            set_x_tile(c1);
+            issue(std::integral_constant<int, 1>{}, 1, c1);
+            blend_store(std::integral_constant<int, 0>{});
+            __syncthreads();
+            set_x_tile(ci);
+            set_om_tile(co);
+        }
+        int g = 0;
+        for (; g + 1 < S; g += 2) {
+            step(std::integral_constant<int, 0>{});
+            step(std::integral_constant<int, 1>{});
+        }
+        if (g < S) step(std::integral_constant<int, 0>{});
+    }
+}
+
 template <typename T, int WM, int WN, int IB, int JB>
 static hipError_t launch_fwd_t(const Geo &g, const FwdParams &p0, hipStream_t s) {
     FwdParams p = p0;
@@ -281,12 +770,63 @@ static hipError_t launch_fwd_t(const Geo &g, const FwdParams &p0, hipStream_t s)
     return hipGetLastError();
 }
 
-// Block tile 256x128 (8 waves of 64x64) when Cout > 128, else 128x128 (8
-// waves of 64x32); both sample 128 pixels, one slot per thread.
+// Warp-specialised kernel for 2-byte types: persistent grid of one
+// workgroup per CU (at most one tile per workgroup more than the average).
+template <typename T, int IB>
+static hipError_t launch_fwd_ws(const Geo &g, const FwdParams &p0, hipStream_t s) {
+    FwdParams p = p0;
+    p.ntiles = ceil_div(g.N, 128);
+    p.mtiles = g.Mp / (128 * IB);
+    p.tiles = g.B * p.ntiles * p.mtiles;
+    p.out_vec = (g.N % 8 == 0) && (((uintptr_t)p.out & 15) == 0);
+    int dev = 0, ncu = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        ncu <= 0)
+        ncu = 256;
+    const int grid = p.tiles < ncu ? p.tiles : ncu;
+    if (p.mask)
+        dcn2_fwd_ws_kernel<T, IB, true><<<grid, 512, 0, s>>>(p);
+    else
+        dcn2_fwd_ws_kernel<T, IB, false><<<grid, 512, 0, s>>>(p);
+    return hipGetLastError();
+}
+
+// The role election of dcn2_fwd_ws_kernel needs every SIMD to hold at most
+// two waves of a workgroup, i.e. more than 512/3 VGPRs per wave.
+template <typename T, int IB>
+static bool ws_two_waves_per_simd() {
+    static const bool ok = [] {
+        hipFuncAttributes a;
+        if (hipFuncGetAttributes(&a, reinterpret_cast<const void *>(&dcn2_fwd_ws_kernel<T, IB, true>)) !=
+                hipSuccess || a.numRegs <= 512 / 3)
+            return false;
+        if (hipFuncGetAttributes(&a, reinterpret_cast<const void *>(&dcn2_fwd_ws_kernel<T, IB, false>)) !=
+                hipSuccess || a.numRegs <= 512 / 3)
+            return false;
+        return true;
+    }();
+    return ok;
+}
+
+// fp32 (and 2-byte types with more than kBiasRows padded output rows): block
+// tile 256x128 (8 waves of 32x128) when Cout > 128, else 128x128 (8 waves of
+// 64x32); both sample 128 pixels, one slot per thread.
 template <typename T>
 static hipError_t launch_fwd_dt(const Geo &g, const FwdParams &p, hipStream_t s) {
-    if (g.BM == 256) return launch_fwd_t<T, 8, 1, 1, 4>(g, p, s);
-    return launch_fwd_t<T, 2, 4, 2, 1>(g, p, s);
+    if constexpr (sizeof(T) == 2) {
+        if (g.Mp <= kBiasRows) {
+            if (g.BM == 256 && ws_two_waves_per_simd<T, 2>()) return launch_fwd_ws<T, 2>(g, p, s);
+            if (g.BM == 128 && ws_two_waves_per_simd<T, 1>()) return launch_fwd_ws<T, 1>(g, p, s);
+        }
+        // more than kBiasRows output rows (or a register count that would let
+        // three waves share a SIMD): the non-specialised kernel
+        if (g.BM == 256) return launch_fwd_t<T, 8, 1, 1, 4>(g, p, s);
+        return launch_fwd_t<T, 2, 4, 2, 1>(g, p, s);
+    } else {
+        if (g.BM == 256) return launch_fwd_t<T, 8, 1, 1, 4>(g, p, s);
+        return launch_fwd_t<T, 2, 4, 2, 1>(g, p, s);
+    }
 }
 
 hipError_t launch_forward(const Geo &g, const void *xt, const void *wp, const void *tab,
@@ -317,6 +857,7 @@ hipError_t launch_forward(const Geo &g, const void *xt, const void *wp, const vo
     p.Ho = g.Ho;
     p.Wo = g.Wo;
     p.Kp = g.Kp;
+    p.Mp = g.Mp;
     switch (g.dtype) {
     case DCN2_F16: return launch_fwd_dt<f16>(g, p, s);
     case DCN2_BF16: return launch_fwd_dt<bf16>(g, p, s);
