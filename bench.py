@@ -107,7 +107,7 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=500)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--mode", choices=("full", "fwd"), default="full")
@@ -174,7 +174,7 @@ def main():
         return _C.dcn_v2_backward(*b_args, t2["grad_output"], *geo)
 
     fb_steps = max(5, args.steps // 4)
-    for _ in range(max(2, args.warmup // 2)):
+    for _ in range(max(2, min(50, args.warmup // 4))):
         fwd_bwd()
     fb_ms = _events_ms(fwd_bwd, fb_steps, torch)
     _C.profile_enable(True)
