@@ -125,6 +125,8 @@ BwdWorkspace bwd_workspace(const Geo &g) {
     o += align256((size_t)gg.nbuckets * gg.cap * 16);
     w.cnt = o;
     o += align256((size_t)gg.nbuckets * sizeof(int) + 16);
+    w.sidx = o;
+    o += align256((size_t)g.B * g.G * g.KK * g.N * sizeof(int));
     w.total = o;
     return w;
 }
@@ -219,7 +221,8 @@ int dcn2_backward(const dcn2_desc *d, const void *input, const void *weight, con
                                         grad_input, grad_offset, grad_mask, grad_weight,
                                         grad_bias, (float *)(base + ws.gi_acc),
                                         (float *)(base + ws.gw_acc), (float *)(base + ws.gb_acc),
-                                        base + ws.cgm, base + ws.rec, (int *)(base + ws.cnt), s),
+                                        base + ws.cgm, base + ws.rec, (int *)(base + ws.cnt),
+                                        (int *)(base + ws.sidx), s),
                         "backward");
 }
 

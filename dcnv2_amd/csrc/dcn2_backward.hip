@@ -41,6 +41,7 @@ struct BwdParams {
     void *cgm;          // [nbuckets*cap][Cgp] masked column gradient rows, call dtype
     int4 *rec;          // [nbuckets][cap] sample records
     int *cnt;           // [nbuckets] records appended per bucket
+    int *sidx;          // [B][G*KK][N] bucket-slot row of each sample; -1 no corner, -2 bucket full
     int ntx, nty, cap;  // cell tiles per row / column, bucket capacity
 };
 
@@ -98,9 +99,55 @@ __device__ __forceinline__ float shfl_xor_f(float v, int mask) {
 }
 
 // ---------------------------------------------------------------------------
+// Bucket pre-pass of the grad_input hand-off: one thread per sample (image,
+// offset plane g*KK + tap, output pixel).  Appends the record of every sample
+// with a corner inside the image to the bucket of its cell tile (wavefront-
+// aggregated atomics) and writes the sample's bucket-slot row to sidx, so the
+// column-gradient kernel only reads one int per sample instead of waiting on
+// an atomic with return in its per-chunk critical path.  The sample position
+// is computed exactly as the column-gradient kernel computes it.
+__global__ __launch_bounds__(256) void dcn2_bucket_kernel(const BwdParams p, const void *offset_v,
+                                                          int esz_is_f32, int is_bf16) {
+    const int N = p.Ho * p.Wo, KK = p.kh * p.kw;
+    const int n = blockIdx.x * 256 + threadIdx.x;
+    const int plane = blockIdx.y, b = blockIdx.z;
+    const int g = plane / KK, tap = plane - g * KK;
+    const int ki = tap / p.kw, kj = tap - ki * p.kw;
+    const bool live = n < N;
+    const int nn = live ? n : 0;
+    const int oy = nn / p.Wo, ox = nn - oy * p.Wo;
+    const size_t ob = ((size_t)b * p.G * KK + plane) * 2 * N + nn;
+    float dy, dx;
+    if (esz_is_f32) {
+        dy = ((const float *)offset_v)[ob];
+        dx = ((const float *)offset_v)[ob + N];
+    } else if (is_bf16) {
+        dy = to_f32(((const bf16 *)offset_v)[ob]);
+        dx = to_f32(((const bf16 *)offset_v)[ob + N]);
+    } else {
+        dy = to_f32(((const f16 *)offset_v)[ob]);
+        dx = to_f32(((const f16 *)offset_v)[ob + N]);
+    }
+    const float y = (float)(oy * p.sh - p.ph + ki * p.dh) + dy;
+    const float x = (float)(ox * p.sw - p.pw + kj * p.dw) + dx;
+    const SamplePos sp = sample_pos(y, x, p.H, p.W);
+    const bool any = live && (sp.vy0 || sp.vy1) && (sp.vx0 || sp.vx1);
+    const int cy = sp.y0 + 1, cx = sp.x0 + 1;
+    const int key = ((b * p.G + g) * p.nty + cy / kCellTile) * p.ntx + cx / kCellTile;
+    const int slot = bucket_append(any, key, p.cnt, p.cap);
+    const int row = key * p.cap + slot;
+    if (slot >= 0)
+        p.rec[row] = make_int4(row, (sp.y0 & 0xffff) | (int)((unsigned)sp.x0 << 16),
+                               __float_as_int(sp.ly), __float_as_int(sp.lx));
+    if (live) p.sidx[((size_t)b * p.G * KK + plane) * N + n] = !any ? -1 : (slot >= 0 ? row : -2);
+}
+
+// ---------------------------------------------------------------------------
 // Column-gradient kernel: grad_offset, grad_mask and grad_input.
 // 512 threads; BN = 128 output pixels of one image per block.
-template <typename T, int MCH>
+// ALDS: the W'^T fragments of a chunk (Mp*128 bytes, Mp <= 256) are staged in
+// LDS one chunk ahead; otherwise every wave reads its fragments from memory.
+template <typename T, int MCH, bool ALDS>
 __global__ __launch_bounds__(512) void dcn2_colgrad_kernel(const BwdParams p) {
     using M = Mma<T>;
     using frag = typename M::frag;
@@ -119,6 +166,8 @@ __global__ __launch_bounds__(512) void dcn2_colgrad_kernel(const BwdParams p) {
 
     __shared__ __attribute__((aligned(16))) float sCG[WPB][BN][LDC];
     __shared__ Desc sD[BN];
+    constexpr int kAVec = 2048;  // 16-byte vectors of one staged chunk (Mp = 256)
+    __shared__ __attribute__((aligned(16))) uint4 sA[ALDS ? 2 : 1][ALDS ? kAVec : 1];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int blk = wave % NB, wr = wave / NB;
@@ -162,22 +211,76 @@ __global__ __launch_bounds__(512) void dcn2_colgrad_kernel(const BwdParams p) {
     }
     float racc[3] = {0.0f, 0.0f, 0.0f};  // grad_mask, grad_off_y, grad_off_x (lq == 0)
     int gmode = 0, gsidx = 0;             // grad_input mode of (pr, tap, g), see Desc
+    const int *__restrict__ sidx = p.sidx + (size_t)b * p.G * KK * N;
+
+    // W'^T staging: chunk ch's fragments are Mp*8 consecutive 16-byte vectors
+    // (pack_weight_kernel layout 1 is k-block major); each thread moves up to
+    // four of them, loaded at the start of chunk ch-1 and written to the free
+    // LDS buffer at its end.
+    const int avec = p.Mp * 8;
+    const uint4 *__restrict__ wtv = (const uint4 *)p.wt;
+    uint4 apf[4];
+    auto a_prefetch = [&](int c) __attribute__((always_inline)) {
+        if constexpr (ALDS) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int i = tid + q * 512;
+                if (i < avec) apf[q] = wtv[(size_t)c * avec + i];
+            }
+        }
+    };
+    auto a_commit = [&](int buf) __attribute__((always_inline)) {
+        if constexpr (ALDS) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int i = tid + q * 512;
+                if (i < avec) sA[buf][i] = apf[q];
+            }
+        }
+    };
+
+    // Offsets, mask and bucket row of (pr, chunk) are loaded one chunk ahead.
+    struct OM {
+        T dy, dx, m;
+        int sx;
+    };
+    auto load_om = [&](int c, OM &o) __attribute__((always_inline)) {
+        const int tg = c / cpg, tap = tg / p.G, g = tg - tap * p.G;
+        const int plane = g * KK + tap;
+        const int nn = nr < N ? nr : 0;
+        const size_t ob = (size_t)plane * 2 * N + nn;
+        o.dy = offs[ob];
+        o.dx = offs[ob + N];
+        o.m = msk ? msk[(size_t)plane * N + nn] : (T)1.0f;
+        o.sx = sidx[(size_t)plane * N + nn];
+    };
+    OM om_cur, om_nxt;
+    load_om(0, om_cur);
+    a_prefetch(0);
+    a_commit(0);
+    __syncthreads();
 
     for (int ch = 0; ch < nch; ++ch) {
         const int tg = ch / cpg, cc = ch - tg * cpg;
         const int tap = tg / p.G, g = tg - tap * p.G;
         const int ki = tap / p.kw, kj = tap - ki * p.kw;
 
+        // next chunk's W'^T and offsets first: the MFMA below reads LDS only,
+        // and the corner gathers issued after these loads are what the
+        // reduction waits for
+        if (ch + 1 < nch) {
+            a_prefetch(ch + 1);
+            load_om(ch + 1, om_nxt);
+        }
         // Sampling position of (pr, tap, g) and the corner gathers of this
         // lane's channels; issued before the MFMA so their latency overlaps it.
         SamplePos sp;
         float mv = 0.0f;
-        bool live = nr < N;
+        const bool live = nr < N;
         if (live) {
-            const size_t ob = ((size_t)g * KK + tap) * 2 * N + nr;
-            const float y = (float)(oyr * p.sh - p.ph + ki * p.dh) + to_f32(offs[ob]);
-            const float x = (float)(oxr * p.sw - p.pw + kj * p.dw) + to_f32(offs[ob + N]);
-            mv = msk ? to_f32(msk[((size_t)g * KK + tap) * N + nr]) : 1.0f;
+            const float y = (float)(oyr * p.sh - p.ph + ki * p.dh) + to_f32(om_cur.dy);
+            const float x = (float)(oxr * p.sw - p.pw + kj * p.dw) + to_f32(om_cur.dx);
+            mv = to_f32(om_cur.m);
             sp = sample_pos(y, x, p.H, p.W);
         } else {
             sp = sample_pos(-2.0f, -2.0f, p.H, p.W);
@@ -193,6 +296,10 @@ __global__ __launch_bounds__(512) void dcn2_colgrad_kernel(const BwdParams p) {
                 raw[q][1] = src[1];
             }
         }
+        if (cc == 0) {
+            gmode = om_cur.sx == -1 ? 0 : (om_cur.sx >= 0 ? 1 : 2);
+            gsidx = om_cur.sx;
+        }
 
         // Column gradient of this chunk: block (kb, nb), M share wr.
         f32x16 acc;
@@ -202,12 +309,14 @@ __global__ __launch_bounds__(512) void dcn2_colgrad_kernel(const BwdParams p) {
         // fragment (row block ch*KC/32 + kb, step ms) is one contiguous run.
         const T *wrow = wt + ((size_t)(ch * KC / 32 + kb) * (p.Mp / KSTEP) + wr * (MPW / KSTEP)) *
                                  64 * KPL + lane * KPL;
+        const T *arow = reinterpret_cast<const T *>(&sA[0][0]) + (size_t)(ch & 1) * kAVec * (16 / sizeof(T)) +
+                        ((size_t)kb * (p.Mp / KSTEP) + wr * (MPW / KSTEP)) * 64 * KPL + lane * KPL;
         for (int mc = 0; mc < nmc; ++mc) {
             if (nmc > 1) load_go(mc);
 #pragma unroll
             for (int s = 0; s < NMS; ++s) {
-                const frag a = *reinterpret_cast<const frag *>(
-                    wrow + (size_t)(mc * (MCH / KSTEP) + s) * 64 * KPL);
+                const size_t fo = (size_t)(mc * (MCH / KSTEP) + s) * 64 * KPL;
+                const frag a = *reinterpret_cast<const frag *>((ALDS ? arow : wrow) + fo);
                 acc = M::mma(a, gfr[s], acc);
             }
         }
@@ -219,22 +328,6 @@ __global__ __launch_bounds__(512) void dcn2_colgrad_kernel(const BwdParams p) {
                 *reinterpret_cast<f32x4 *>(&sCG[wr][nl][kl]) =
                     f32x4{acc[4 * j], acc[4 * j + 1], acc[4 * j + 2], acc[4 * j + 3]};
             }
-        }
-        // grad_input bookkeeping, once per (tap, group): append the sample to
-        // the bucket of its cell tile.  The slot decision holds for all
-        // channel chunks of the group.
-        if (cc == 0) {
-            const bool any = live && (sp.vy0 || sp.vy1) && (sp.vx0 || sp.vx1);
-            const int cy = sp.y0 + 1, cx = sp.x0 + 1;
-            const int key = ((b * p.G + g) * p.nty + cy / kCellTile) * p.ntx + cx / kCellTile;
-            const int slot = bucket_append(any && lq == 0, key, p.cnt, p.cap);
-            const int row = key * p.cap + slot;  // bucket-slot row of the column gradient
-            if (slot >= 0) {
-                p.rec[row] = make_int4(row, (sp.y0 & 0xffff) | (int)((unsigned)sp.x0 << 16),
-                                       __float_as_int(sp.ly), __float_as_int(sp.lx));
-            }
-            gmode = !any ? 0 : (slot >= 0 ? 1 : 2);
-            gsidx = row;
         }
         if (lq == 0) {
             Desc d;
@@ -328,6 +421,10 @@ __global__ __launch_bounds__(512) void dcn2_colgrad_kernel(const BwdParams p) {
                         if (d.w[q] != 0.0f) unsafeAtomicAdd(gib + d.off[q], v * d.w[q]);
                 }
             }
+        }
+        if (ch + 1 < nch) {
+            a_commit((ch + 1) & 1);
+            om_cur = om_nxt;
         }
         __syncthreads();
     }
@@ -804,15 +901,24 @@ static hipError_t backward_t(const Geo &g, const BwdParams &p0, void *grad_input
         // 2. column gradient: grad_offset, grad_mask, grad_input accumulation
         prof_begin(DCN2_STAGE_BWD_COLGRAD, s);
         {
+            dim3 bgrid(ceil_div(g.N, 256), g.G * g.KK, g.B);
+            dcn2_bucket_kernel<<<bgrid, 256, 0, s>>>(p, p.offset, sizeof(T) == 4,
+                                                     std::is_same<T, bf16>::value);
+            if ((e = hipGetLastError()) != hipSuccess) return e;
             dim3 grid(p.tiles_per_img, g.B);
+            const bool alds = g.Mp <= 256;
             // fp32 keeps the 128-wide M chunk: 256 would hold 128 gO registers.
             if constexpr (sizeof(T) == 2) {
-                if (g.Mp % 256 == 0)
-                    dcn2_colgrad_kernel<T, 256><<<grid, 512, 0, s>>>(p);
-                else
-                    dcn2_colgrad_kernel<T, 128><<<grid, 512, 0, s>>>(p);
+                if (g.Mp % 256 == 0) {
+                    if (alds) dcn2_colgrad_kernel<T, 256, true><<<grid, 512, 0, s>>>(p);
+                    else dcn2_colgrad_kernel<T, 256, false><<<grid, 512, 0, s>>>(p);
+                } else {
+                    if (alds) dcn2_colgrad_kernel<T, 128, true><<<grid, 512, 0, s>>>(p);
+                    else dcn2_colgrad_kernel<T, 128, false><<<grid, 512, 0, s>>>(p);
+                }
             } else {
-                dcn2_colgrad_kernel<T, 128><<<grid, 512, 0, s>>>(p);
+                if (alds) dcn2_colgrad_kernel<T, 128, true><<<grid, 512, 0, s>>>(p);
+                else dcn2_colgrad_kernel<T, 128, false><<<grid, 512, 0, s>>>(p);
             }
             if ((e = hipGetLastError()) != hipSuccess) return e;
         }
@@ -888,7 +994,7 @@ hipError_t launch_backward(const Geo &g, const void *xt, const void *wt, const v
                            const void *mask, const void *grad_out, void *grad_input,
                            void *grad_offset, void *grad_mask, void *grad_weight, void *grad_bias,
                            float *gi_acc, float *gw_acc, float *gb_acc, void *cgm, void *rec,
-                           int *cnt, hipStream_t s) {
+                           int *cnt, int *sidx, hipStream_t s) {
     BwdParams p;
     p.xt = xt;
     p.wt = wt;
@@ -927,6 +1033,7 @@ hipError_t launch_backward(const Geo &g, const void *xt, const void *wt, const v
     p.cgm = cgm;
     p.rec = (int4 *)rec;
     p.cnt = cnt;
+    p.sidx = sidx;
     p.ntx = gg.ntx;
     p.nty = gg.nty;
     p.cap = gg.cap;

@@ -31,7 +31,7 @@ struct FwdWorkspace {
 FwdWorkspace fwd_workspace(const Geo &g);
 
 struct BwdWorkspace {
-    size_t xt, wt, tab, gi_acc, gw_acc, gb_acc, cgm, rec, cnt, total;
+    size_t xt, wt, tab, gi_acc, gw_acc, gb_acc, cgm, rec, cnt, sidx, total;
 };
 BwdWorkspace bwd_workspace(const Geo &g);
 
@@ -58,6 +58,6 @@ hipError_t launch_backward(const Geo &g, const void *xt, const void *wt, const v
                            const void *mask, const void *grad_out, void *grad_input,
                            void *grad_offset, void *grad_mask, void *grad_weight, void *grad_bias,
                            float *gi_acc, float *gw_acc, float *gb_acc, void *cgm, void *rec,
-                           int *cnt, hipStream_t s);
+                           int *cnt, int *sidx, hipStream_t s);
 
 }  // namespace dcn2
