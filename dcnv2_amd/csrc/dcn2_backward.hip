@@ -160,7 +160,6 @@ __global__ __launch_bounds__(512) void dcn2_colgrad_kernel(const BwdParams p) {
     constexpr int LDC = KC + 4;                // pitch (floats) of the column gradient
     constexpr int QPP = 512 / BN;              // lanes per pixel in the reduction phase
     constexpr int CPL = KC / QPP;              // channels per lane there
-    constexpr int PPW = 64 / KC;               // pixels per wave step in the scatter
     constexpr int E = Unpack<T>::E;
     static_assert(CPL * sizeof(T) == 32, "reduction lane covers 32 bytes per corner");
 
@@ -397,28 +396,45 @@ __global__ __launch_bounds__(512) void dcn2_colgrad_kernel(const BwdParams p) {
             }
         }
 
-        // grad_input: lane = channel.  Bucketed samples store their masked
-        // column-gradient row (one contiguous run per wave instruction) for
-        // the gather kernel; samples of a full bucket add to grad_input here.
+        // grad_input: 8 lanes per pixel, 16 bytes (EPL channels) per lane.
+        // A bucketed sample stores its masked column-gradient row (8 rows of
+        // 16-byte pieces per wave instruction) for the gather kernel; a sample
+        // of a full bucket adds to grad_input here with fp32 atomics.
         {
-            const int c = lane % KC, sub = lane / KC;
-            const bool cvalid = cc * KC + c < p.Cg;
-            float *gib = gi + g * p.Cgp + cc * KC + c;
-            T *cgm = (T *)p.cgm + cc * KC + c;
-            for (int it = 0; it < BN / (8 * PPW); ++it) {
-                const int pl = (it * 8 + wave) * PPW + sub;
+            constexpr int EPL = 16 / sizeof(T), LPP = KC / EPL, PPI = 64 / LPP;
+            static_assert(LPP == 8, "8 lanes cover one chunk row");
+            const int co = lane % LPP, r = lane / LPP;
+#pragma unroll
+            for (int it = 0; it < BN / (8 * PPI); ++it) {
+                const int pl = (it * 8 + wave) * PPI + r;
                 if (n0 + pl >= N) continue;
                 const Desc d = sD[pl];
                 if (d.mode == 0) continue;
-                float v = sCG[0][pl][c];
+                float v[EPL];
 #pragma unroll
-                for (int w2 = 1; w2 < WPB; ++w2) v += sCG[w2][pl][c];
+                for (int e4 = 0; e4 < EPL / 4; ++e4) {
+                    f32x4 x = *reinterpret_cast<const f32x4 *>(&sCG[0][pl][co * EPL + 4 * e4]);
+#pragma unroll
+                    for (int w2 = 1; w2 < WPB; ++w2)
+                        x += *reinterpret_cast<const f32x4 *>(&sCG[w2][pl][co * EPL + 4 * e4]);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) v[4 * e4 + e] = x[e];
+                }
                 if (d.mode == 1) {
-                    cgm[(size_t)d.sidx * p.Cgp] = from_f32<T>(v * d.m);
-                } else if (cvalid) {
+                    float mv8[EPL];
 #pragma unroll
-                    for (int q = 0; q < 4; ++q)
-                        if (d.w[q] != 0.0f) unsafeAtomicAdd(gib + d.off[q], v * d.w[q]);
+                    for (int e = 0; e < EPL; ++e) mv8[e] = v[e] * d.m;
+                    *reinterpret_cast<uint4 *>((T *)p.cgm + (size_t)d.sidx * p.Cgp + cc * KC + co * EPL) =
+                        pack16<T>(mv8);
+                } else {
+                    float *gib = gi + g * p.Cgp + cc * KC + co * EPL;
+#pragma unroll
+                    for (int e = 0; e < EPL; ++e) {
+                        if (cc * KC + co * EPL + e >= p.Cg) continue;
+#pragma unroll
+                        for (int q = 0; q < 4; ++q)
+                            if (d.w[q] != 0.0f) unsafeAtomicAdd(gib + d.off[q] + e, v[e] * d.w[q]);
+                    }
                 }
             }
         }
