@@ -99,19 +99,33 @@ __device__ __forceinline__ float shfl_xor_f(float v, int mask) {
 }
 
 // ---------------------------------------------------------------------------
-// Bucket pre-pass of the grad_input hand-off: one thread per sample (image,
-// offset plane g*KK + tap, output pixel).  Appends the record of every sample
-// with a corner inside the image to the bucket of its cell tile (wavefront-
-// aggregated atomics) and writes the sample's bucket-slot row to sidx, so the
-// column-gradient kernel only reads one int per sample instead of waiting on
-// an atomic with return in its per-chunk critical path.  The sample position
+// Bucket pre-pass of the grad_input hand-off.  For every sample (image,
+// offset plane g*KK + tap, output pixel) with a corner inside the image it
+// appends the record to the bucket of its cell tile and writes the sample's
+// bucket-slot row to sidx (-1: no corner inside, -2: bucket full), so the
+// column-gradient kernel only reads one int per sample.  The sample position
 // is computed exactly as the column-gradient kernel computes it.
-__global__ __launch_bounds__(256) void dcn2_bucket_kernel(const BwdParams p, const void *offset_v,
-                                                          int esz_is_f32, int is_bf16) {
+//
+// A workgroup takes kBucketSPT*256 consecutive pixels of one offset plane and
+// counts its samples per cell tile in LDS (wavefront-aggregated LDS atomics
+// give each sample its rank inside the workgroup); then one global atomic per
+// (workgroup, cell tile) claims a range of the bucket.  Claiming slots with
+// one global atomic per wave instead serialises thousands of atomics on each
+// bucket counter.
+constexpr int kBucketTab = 16384;  // cell tiles of one image the LDS table holds
+constexpr int kBucketSPT = 16;     // samples per thread
+
+struct BucketSample {
+    SamplePos sp;
+    bool any;
+    int tkey;  // cell tile inside the image: (cy / kCellTile) * ntx + cx / kCellTile
+};
+
+__device__ __forceinline__ BucketSample bucket_sample(const BwdParams &p, const void *offset_v,
+                                                      int esz_is_f32, int is_bf16, int b,
+                                                      int plane, int n) {
     const int N = p.Ho * p.Wo, KK = p.kh * p.kw;
-    const int n = blockIdx.x * 256 + threadIdx.x;
-    const int plane = blockIdx.y, b = blockIdx.z;
-    const int g = plane / KK, tap = plane - g * KK;
+    const int tap = plane % KK;
     const int ki = tap / p.kw, kj = tap - ki * p.kw;
     const bool live = n < N;
     const int nn = live ? n : 0;
@@ -130,16 +144,92 @@ __global__ __launch_bounds__(256) void dcn2_bucket_kernel(const BwdParams p, con
     }
     const float y = (float)(oy * p.sh - p.ph + ki * p.dh) + dy;
     const float x = (float)(ox * p.sw - p.pw + kj * p.dw) + dx;
-    const SamplePos sp = sample_pos(y, x, p.H, p.W);
-    const bool any = live && (sp.vy0 || sp.vy1) && (sp.vx0 || sp.vx1);
-    const int cy = sp.y0 + 1, cx = sp.x0 + 1;
-    const int key = ((b * p.G + g) * p.nty + cy / kCellTile) * p.ntx + cx / kCellTile;
-    const int slot = bucket_append(any, key, p.cnt, p.cap);
+    BucketSample r;
+    r.sp = sample_pos(y, x, p.H, p.W);
+    r.any = live && (r.sp.vy0 || r.sp.vy1) && (r.sp.vx0 || r.sp.vx1);
+    r.tkey = ((r.sp.y0 + 1) / kCellTile) * p.ntx + (r.sp.x0 + 1) / kCellTile;
+    return r;
+}
+
+// Rank of this lane among the wave's lanes with the same key, plus the value
+// of counter[key] before the wave's additions (one LDS atomic per distinct key).
+__device__ __forceinline__ int wave_rank_lds(bool want, int key, int *counter) {
+    const int lane = threadIdx.x & 63;
+    unsigned long long active = __ballot(want);
+    int r = -1;
+    while (active) {
+        const int leader = __ffsll((long long)active) - 1;
+        const int lkey = __shfl(key, leader, 64);
+        const unsigned long long same = __ballot(want && key == lkey) & active;
+        int base = 0;
+        if (lane == leader) base = atomicAdd(counter + lkey, __popcll(same));
+        base = __shfl(base, leader, 64);
+        if ((same >> lane) & 1ull) r = base + __popcll(same & ((1ull << lane) - 1ull));
+        active &= ~same;
+    }
+    return r;
+}
+
+__global__ __launch_bounds__(256) void dcn2_bucket_kernel(const BwdParams p, const void *offset_v,
+                                                          int esz_is_f32, int is_bf16) {
+    __shared__ int tab[kBucketTab];
+    const int N = p.Ho * p.Wo, KK = p.kh * p.kw;
+    const int tid = threadIdx.x, ntile = p.nty * p.ntx;
+    const int plane = blockIdx.y, b = blockIdx.z, g = plane / KK;
+    const int n_base = blockIdx.x * 256 * kBucketSPT;
+    for (int i = tid; i < ntile; i += 256) tab[i] = 0;
+    __syncthreads();
+    int rank[kBucketSPT];
+#pragma unroll
+    for (int k = 0; k < kBucketSPT; ++k) {
+        const BucketSample bs =
+            bucket_sample(p, offset_v, esz_is_f32, is_bf16, b, plane, n_base + k * 256 + tid);
+        rank[k] = wave_rank_lds(bs.any, bs.tkey, tab);
+    }
+    __syncthreads();
+    int *cnt = p.cnt + (size_t)(b * p.G + g) * ntile;
+    for (int i = tid; i < ntile; i += 256) {
+        const int c = tab[i];
+        if (c) tab[i] = atomicAdd(cnt + i, c);  // first slot of this workgroup's range
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < kBucketSPT; ++k) {
+        const int n = n_base + k * 256 + tid;
+        if (n >= N) continue;
+        int sx = -1;
+        if (rank[k] >= 0) {
+            const BucketSample bs = bucket_sample(p, offset_v, esz_is_f32, is_bf16, b, plane, n);
+            const int key = (b * p.G + g) * ntile + bs.tkey;
+            const int slot = tab[bs.tkey] + rank[k];
+            if (slot < p.cap) {
+                sx = key * p.cap + slot;
+                p.rec[sx] = make_int4(sx, (bs.sp.y0 & 0xffff) | (int)((unsigned)bs.sp.x0 << 16),
+                                      __float_as_int(bs.sp.ly), __float_as_int(bs.sp.lx));
+            } else {
+                sx = -2;
+            }
+        }
+        p.sidx[((size_t)b * p.G * KK + plane) * N + n] = sx;
+    }
+}
+
+// The same with one global atomic per (wave, bucket), for images with more
+// cell tiles than kBucketTab.
+__global__ __launch_bounds__(256) void dcn2_bucket_global_kernel(const BwdParams p,
+                                                                 const void *offset_v,
+                                                                 int esz_is_f32, int is_bf16) {
+    const int N = p.Ho * p.Wo, KK = p.kh * p.kw;
+    const int n = blockIdx.x * 256 + threadIdx.x;
+    const int plane = blockIdx.y, b = blockIdx.z, g = plane / KK;
+    const BucketSample bs = bucket_sample(p, offset_v, esz_is_f32, is_bf16, b, plane, n);
+    const int key = (b * p.G + g) * p.nty * p.ntx + bs.tkey;
+    const int slot = bucket_append(bs.any, key, p.cnt, p.cap);
     const int row = key * p.cap + slot;
     if (slot >= 0)
-        p.rec[row] = make_int4(row, (sp.y0 & 0xffff) | (int)((unsigned)sp.x0 << 16),
-                               __float_as_int(sp.ly), __float_as_int(sp.lx));
-    if (live) p.sidx[((size_t)b * p.G * KK + plane) * N + n] = !any ? -1 : (slot >= 0 ? row : -2);
+        p.rec[row] = make_int4(row, (bs.sp.y0 & 0xffff) | (int)((unsigned)bs.sp.x0 << 16),
+                               __float_as_int(bs.sp.ly), __float_as_int(bs.sp.lx));
+    if (n < N) p.sidx[((size_t)b * p.G * KK + plane) * N + n] = !bs.any ? -1 : (slot >= 0 ? row : -2);
 }
 
 // ---------------------------------------------------------------------------
@@ -917,9 +1007,15 @@ static hipError_t backward_t(const Geo &g, const BwdParams &p0, void *grad_input
         // 2. column gradient: grad_offset, grad_mask, grad_input accumulation
         prof_begin(DCN2_STAGE_BWD_COLGRAD, s);
         {
-            dim3 bgrid(ceil_div(g.N, 256), g.G * g.KK, g.B);
-            dcn2_bucket_kernel<<<bgrid, 256, 0, s>>>(p, p.offset, sizeof(T) == 4,
-                                                     std::is_same<T, bf16>::value);
+            if ((long)p.nty * p.ntx <= kBucketTab) {
+                dim3 bgrid(ceil_div(g.N, 256 * kBucketSPT), g.G * g.KK, g.B);
+                dcn2_bucket_kernel<<<bgrid, 256, 0, s>>>(p, p.offset, sizeof(T) == 4,
+                                                         std::is_same<T, bf16>::value);
+            } else {
+                dim3 bgrid(ceil_div(g.N, 256), g.G * g.KK, g.B);
+                dcn2_bucket_global_kernel<<<bgrid, 256, 0, s>>>(p, p.offset, sizeof(T) == 4,
+                                                                std::is_same<T, bf16>::value);
+            }
             if ((e = hipGetLastError()) != hipSuccess) return e;
             dim3 grid(p.tiles_per_img, g.B);
             const bool alds = g.Mp <= 256;
