@@ -107,8 +107,8 @@ __device__ __forceinline__ float shfl_xor_f(float v, int mask) {
 // is computed exactly as the column-gradient kernel computes it.
 //
 // A workgroup takes kBucketSPT*256 consecutive pixels of one offset plane and
-// counts its samples per cell tile in LDS (wavefront-aggregated LDS atomics
-// give each sample its rank inside the workgroup); then one global atomic per
+// counts its samples per cell tile in LDS (the LDS atomic's return value is
+// the sample's rank inside the workgroup); then one global atomic per
 // (workgroup, cell tile) claims a range of the bucket.  Claiming slots with
 // one global atomic per wave instead serialises thousands of atomics on each
 // bucket counter.
@@ -151,25 +151,6 @@ __device__ __forceinline__ BucketSample bucket_sample(const BwdParams &p, const 
     return r;
 }
 
-// Rank of this lane among the wave's lanes with the same key, plus the value
-// of counter[key] before the wave's additions (one LDS atomic per distinct key).
-__device__ __forceinline__ int wave_rank_lds(bool want, int key, int *counter) {
-    const int lane = threadIdx.x & 63;
-    unsigned long long active = __ballot(want);
-    int r = -1;
-    while (active) {
-        const int leader = __ffsll((long long)active) - 1;
-        const int lkey = __shfl(key, leader, 64);
-        const unsigned long long same = __ballot(want && key == lkey) & active;
-        int base = 0;
-        if (lane == leader) base = atomicAdd(counter + lkey, __popcll(same));
-        base = __shfl(base, leader, 64);
-        if ((same >> lane) & 1ull) r = base + __popcll(same & ((1ull << lane) - 1ull));
-        active &= ~same;
-    }
-    return r;
-}
-
 __global__ __launch_bounds__(256) void dcn2_bucket_kernel(const BwdParams p, const void *offset_v,
                                                           int esz_is_f32, int is_bf16) {
     __shared__ int tab[kBucketTab];
@@ -184,7 +165,7 @@ __global__ __launch_bounds__(256) void dcn2_bucket_kernel(const BwdParams p, con
     for (int k = 0; k < kBucketSPT; ++k) {
         const BucketSample bs =
             bucket_sample(p, offset_v, esz_is_f32, is_bf16, b, plane, n_base + k * 256 + tid);
-        rank[k] = wave_rank_lds(bs.any, bs.tkey, tab);
+        rank[k] = bs.any ? atomicAdd(tab + bs.tkey, 1) : -1;
     }
     __syncthreads();
     int *cnt = p.cnt + (size_t)(b * p.G + g) * ntile;
