@@ -538,7 +538,12 @@ template <> struct GwLayout<bf16> {
 
 __device__ __forceinline__ int gw_swz(int k) { return ((k & 15) ^ (k >> 3)) & 15; }
 
-template <typename T, int MB, bool MASK>
+// VEC (2-byte types, N % 8 == 0, 16-byte aligned gO): gO fragments come from
+// buffer loads (rows past Cout read 0, pixels past N are zeroed with a select)
+// and every pipeline stage runs unconditionally on a clamped tile index, so
+// the loop has no divergent branches around its loads and the compiler's
+// load counting stays exact.  Otherwise a guarded element-wise path is used.
+template <typename T, int MB, bool MASK, bool VEC>
 __global__ __launch_bounds__(512) void dcn2_gradw_kernel(const BwdParams p) {
     using M = Mma<T>;
     using frag = typename M::frag;
@@ -631,17 +636,29 @@ __global__ __launch_bounds__(512) void dcn2_gradw_kernel(const BwdParams p) {
     float bsum = 0.0f;
 
     const bool aligned = p.go_vec != 0;
+    const uint32_t go_bytes = (uint32_t)((size_t)p.Cout * N * sizeof(T));
     auto load_a = [&](frag &a, int t, int ks) __attribute__((always_inline)) {
         const int b = t / p.tiles_per_img, n0 = (t - b * p.tiles_per_img) * BN;
         const int n = n0 + ks * KSTEP + (lane >> 5) * KPL;
-        const T *row = (const T *)p.gout + ((size_t)b * p.Cout + mrow) * N;
-        if (mrow < p.Cout && aligned && n + KPL <= N && KPL == 8) {
-            a = *reinterpret_cast<const frag *>(row + n);
+        if constexpr (VEC && KPL == 8) {
+            typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+            const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<T *>((const T *)p.gout + (size_t)b * p.Cout * N), (short)0,
+                (int)go_bytes, 0x00020000);
+            u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(
+                rs, (int)(((unsigned)mrow * (unsigned)N + (unsigned)n) * sizeof(T)), 0, 0);
+            if (n >= N) v = u32x4{0u, 0u, 0u, 0u};
+            a = __builtin_bit_cast(frag, v);
         } else {
+            const T *row = (const T *)p.gout + ((size_t)b * p.Cout + mrow) * N;
+            if (mrow < p.Cout && aligned && n + KPL <= N && KPL == 8) {
+                a = *reinterpret_cast<const frag *>(row + n);
+            } else {
 #pragma unroll
-            for (int e = 0; e < KPL; ++e) {
-                const T v = (mrow < p.Cout && n + e < N) ? row[n + e] : (T)0.0f;
-                FragSet<T, KPL>::set(a, e, v);
+                for (int e = 0; e < KPL; ++e) {
+                    const T v = (mrow < p.Cout && n + e < N) ? row[n + e] : (T)0.0f;
+                    FragSet<T, KPL>::set(a, e, v);
+                }
             }
         }
     };
@@ -690,30 +707,52 @@ __global__ __launch_bounds__(512) void dcn2_gradw_kernel(const BwdParams p) {
     };
 
     // One step for tile t (the it-th of this work item, set S = it % 2).
+    const int t_last = t_end - 1;
     auto step = [&](auto s_c, int t) __attribute__((always_inline)) {
         constexpr int S = decltype(s_c)::value;
         constexpr int O = S ^ 1;
-        if (t + 3 < t_end) load_om_tile(t + 3, om[O]);
-        if (t + 1 < t_end && active) load_a_tile(a_nxt, t + 1);
-        if (t + 2 < t_end) issue_tile(std::integral_constant<int, S>{}, t + 2, om[S]);
-        mfma_tile(t, S);
-        if (t + 1 < t_end) {
+        if constexpr (VEC) {
+            load_om_tile(min(t + 3, t_last), om[O]);
+            if (active) load_a_tile(a_nxt, min(t + 1, t_last));
+            issue_tile(std::integral_constant<int, S>{}, min(t + 2, t_last), om[S]);
+            mfma_tile(t, S);
             store_stage(std::integral_constant<int, O>{}, O);
             if constexpr (PREA) {
 #pragma unroll
                 for (int ks = 0; ks < NKS; ++ks) a_cur[ks] = a_nxt[ks];
+            }
+        } else {
+            if (t + 3 < t_end) load_om_tile(t + 3, om[O]);
+            if (t + 1 < t_end && active) load_a_tile(a_nxt, t + 1);
+            if (t + 2 < t_end) issue_tile(std::integral_constant<int, S>{}, t + 2, om[S]);
+            mfma_tile(t, S);
+            if (t + 1 < t_end) {
+                store_stage(std::integral_constant<int, O>{}, O);
+                if constexpr (PREA) {
+#pragma unroll
+                    for (int ks = 0; ks < NKS; ++ks) a_cur[ks] = a_nxt[ks];
+                }
             }
         }
         __syncthreads();
     };
 
     if (t_begin < t_end) {
-        load_om_tile(t_begin, om[0]);
-        if (t_begin + 1 < t_end) load_om_tile(t_begin + 1, om[1]);
-        if (active) load_a_tile(a_cur, t_begin);
-        issue_tile(std::integral_constant<int, 0>{}, t_begin, om[0]);
-        if (t_begin + 2 < t_end) load_om_tile(t_begin + 2, om[0]);
-        if (t_begin + 1 < t_end) issue_tile(std::integral_constant<int, 1>{}, t_begin + 1, om[1]);
+        if constexpr (VEC) {
+            load_om_tile(t_begin, om[0]);
+            load_om_tile(min(t_begin + 1, t_last), om[1]);
+            if (active) load_a_tile(a_cur, t_begin);
+            issue_tile(std::integral_constant<int, 0>{}, t_begin, om[0]);
+            load_om_tile(min(t_begin + 2, t_last), om[0]);
+            issue_tile(std::integral_constant<int, 1>{}, min(t_begin + 1, t_last), om[1]);
+        } else {
+            load_om_tile(t_begin, om[0]);
+            if (t_begin + 1 < t_end) load_om_tile(t_begin + 1, om[1]);
+            if (active) load_a_tile(a_cur, t_begin);
+            issue_tile(std::integral_constant<int, 0>{}, t_begin, om[0]);
+            if (t_begin + 2 < t_end) load_om_tile(t_begin + 2, om[0]);
+            if (t_begin + 1 < t_end) issue_tile(std::integral_constant<int, 1>{}, t_begin + 1, om[1]);
+        }
         store_stage(std::integral_constant<int, 0>{}, 0);
     }
     __syncthreads();
@@ -1031,17 +1070,16 @@ static hipError_t backward_t(const Geo &g, const BwdParams &p0, void *grad_input
             S = std::max(1, std::min(S, T_total));
             p.splits = S;
             const int grid = S * nch * nmc;
+            const bool vec = sizeof(T) == 2 && p.go_vec;
+#define DCN2_GRADW(MBV, MK, VC) dcn2_gradw_kernel<T, MBV, MK, VC><<<grid, 512, 0, s>>>(p)
             if (mb == 8) {
-                if (p.mask)
-                    dcn2_gradw_kernel<T, 8, true><<<grid, 512, 0, s>>>(p);
-                else
-                    dcn2_gradw_kernel<T, 8, false><<<grid, 512, 0, s>>>(p);
+                if (p.mask) { if (vec) DCN2_GRADW(8, true, true); else DCN2_GRADW(8, true, false); }
+                else { if (vec) DCN2_GRADW(8, false, true); else DCN2_GRADW(8, false, false); }
             } else {
-                if (p.mask)
-                    dcn2_gradw_kernel<T, 4, true><<<grid, 512, 0, s>>>(p);
-                else
-                    dcn2_gradw_kernel<T, 4, false><<<grid, 512, 0, s>>>(p);
+                if (p.mask) { if (vec) DCN2_GRADW(4, true, true); else DCN2_GRADW(4, true, false); }
+                else { if (vec) DCN2_GRADW(4, false, true); else DCN2_GRADW(4, false, false); }
             }
+#undef DCN2_GRADW
             if ((e = hipGetLastError()) != hipSuccess) return e;
         }
         prof_end(DCN2_STAGE_BWD_GRADW, s);
