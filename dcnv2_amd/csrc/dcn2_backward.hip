@@ -1066,7 +1066,15 @@ static hipError_t backward_t(const Geo &g, const BwdParams &p0, void *grad_input
             const int mb = (g.Mp % 256 == 0) ? 8 : 4;
             const int nmc = g.Mp / (32 * mb);
             const int T_total = g.B * p.tiles_per_img;
-            int S = 1024 / (nch * nmc);
+            // One workgroup per CU: each (K chunk, M chunk) pair gets CUs/(nch*nmc)
+            // contiguous pixel-tile ranges, so the partial grad_weight tiles a
+            // workgroup adds with fp32 atomics are few (one set per range).
+            int dev = 0, ncu = 0;
+            if (hipGetDevice(&dev) != hipSuccess ||
+                hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+                ncu <= 0)
+                ncu = 256;
+            int S = ncu / (nch * nmc);
             S = std::max(1, std::min(S, T_total));
             p.splits = S;
             const int grid = S * nch * nmc;
