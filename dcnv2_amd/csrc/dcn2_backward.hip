@@ -865,30 +865,34 @@ __global__ __launch_bounds__(512) void dcn2_gi_gather_kernel(const BwdParams p) 
     }
     __syncthreads();
 
-    // 2. pull every pixel of the window.  A wave takes one pixel at a time;
-    //    its lanes are (record rs, channel group co): lane (rs, co) loads 16
-    //    bytes (EPL channels) of the row of record rs, so one load instruction
-    //    fetches RPB whole rows, and the RPB partial sums of a channel group
-    //    are reduced across lanes at the end of the pixel.
+    // 2. pull every pixel of the window.  A wave takes PPW pixels at a time;
+    //    lane (pixel slot ps, channel group co) sums the 16-byte slices (EPL
+    //    channels) of all rows of its pixel's records, UNR rows in flight, so
+    //    one load instruction reads PPW whole rows and the pixels' dependency
+    //    chains (LDS record lookup -> row load -> FMA) overlap.  Pixel
+    //    (py, px) is corner 00 of cell (py, px), 01 of (py, px-1), 10 of
+    //    (py-1, px) and 11 of (py-1, px-1).
     constexpr int EPL = 16 / sizeof(T);  // channels per lane per row
     constexpr int LPR = KC / EPL;        // lanes per row (8)
-    constexpr int RPB = 64 / LPR;        // rows per load instruction (8)
+    constexpr int PPW = 64 / LPR;        // pixels per wave pass (8)
+    constexpr int UNR = 4;
     static_assert(LPR == 8, "a 16-byte lane slice of a KC-channel row");
-    const int co = lane % LPR, rs = lane / LPR;
+    const int co = lane % LPR, ps = lane / LPR;
     for (int cc = 0; cc < cpg; ++cc) {
         const T *__restrict__ rows = (const T *)p.cgm + ((size_t)bucket * p.cap) * p.Cgp +
                                      cc * KC + co * EPL;
-        for (int pl = wave; pl < TW * TW; pl += 8) {
+        for (int pl0 = wave * PPW; pl0 < TW * TW; pl0 += 8 * PPW) {
+            const int pl = pl0 + ps;
             const int py = pl / TW, px = pl - py * TW;
             const int Y = oy + py, X = ox + px;
-            if (Y < 0 || Y >= p.H || X < 0 || X >= p.W) continue;
+            const bool live = pl < TW * TW && Y >= 0 && Y < p.H && X >= 0 && X < p.W;
             // record ranges of the four cells whose corner q is this pixel
             int beg[4], len[4];
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const int cy = py - (q >> 1), cx = px - (q & 1);
-                const bool in = cy >= 0 && cy < TS && cx >= 0 && cx < TS;
-                const int cell = cy * TS + cx;
+                const bool in = live && cy >= 0 && cy < TS && cx >= 0 && cx < TS;
+                const int cell = in ? cy * TS + cx : 0;
                 beg[q] = in ? cstart[cell] : 0;
                 len[q] = in ? cstart[cell + 1] - beg[q] : 0;
             }
@@ -896,13 +900,12 @@ __global__ __launch_bounds__(512) void dcn2_gi_gather_kernel(const BwdParams p) 
             float sum[EPL];
 #pragma unroll
             for (int e = 0; e < EPL; ++e) sum[e] = 0.0f;
-            constexpr int UNR = 2;
-            for (int j0 = 0; j0 < tot; j0 += RPB * UNR) {
+            for (int j0 = 0; j0 < tot; j0 += UNR) {
                 uint4 raw[UNR];
                 float wgt[UNR];
 #pragma unroll
                 for (int u = 0; u < UNR; ++u) {
-                    const int j = j0 + u * RPB + rs;
+                    const int j = j0 + u;
                     const int q = (j >= e1) + (j >= e2) + (j >= e3);
                     const int pos = (q == 0 ? beg[0] + j : q == 1 ? beg[1] + j - e1
                                     : q == 2 ? beg[2] + j - e2 : beg[3] + j - e3);
@@ -913,8 +916,7 @@ __global__ __launch_bounds__(512) void dcn2_gi_gather_kernel(const BwdParams p) 
                         const float wy = (q & 2) ? f.x : 1.0f - f.x;
                         const float wx = (q & 1) ? f.y : 1.0f - f.y;
                         wgt[u] = wy * wx;
-                        raw[u] = *reinterpret_cast<const uint4 *>(rows +
-                                                                  (size_t)sslot[pos] * p.Cgp);
+                        raw[u] = *reinterpret_cast<const uint4 *>(rows + (size_t)sslot[pos] * p.Cgp);
                     }
                 }
 #pragma unroll
@@ -926,12 +928,6 @@ __global__ __launch_bounds__(512) void dcn2_gi_gather_kernel(const BwdParams p) 
                 }
             }
             if (tot == 0) continue;
-#pragma unroll
-            for (int e = 0; e < EPL; ++e) {
-#pragma unroll
-                for (int d = LPR; d < 64; d <<= 1) sum[e] += __shfl_xor(sum[e], d, 64);
-            }
-            if (rs != 0) continue;
             float *dst = gi + ((size_t)Y * p.W + X) * cs + cc * KC + co * EPL;
             const int cvalid = min(EPL, p.Cg - (cc * KC + co * EPL));
             if (py >= 1 && py <= TS - 1 && px >= 1 && px <= TS - 1) {
