@@ -20,6 +20,7 @@
 //     grad_bias from the same gO fragments.
 //  finalize kernels: fp32 accumulators -> caller dtype and layout.
 #include <algorithm>
+#include <cstddef>
 #include <type_traits>
 
 #include "dcn2_common.h"
@@ -58,10 +59,19 @@ struct Desc {
     int off[4];
     float w[4];  // masked bilinear weight of each corner, 0 outside the image
     int sidx;    // row of the masked column gradient: bucket*cap + slot
-    float m;     // mask value
     int mode;
-    int pad;
+    int pad0, pad1;
+    // the last 16 bytes (DescFrac) are what the corner-sum reduction reads
+    float m;     // mask value
+    int valid;   // bit q: corner q inside the image
+    float ly, lx;  // bilinear fractions
 };
+struct DescFrac {
+    float m;
+    int valid;
+    float ly, lx;
+};
+static_assert(sizeof(Desc) == 64 && offsetof(Desc, m) % 16 == 0, "Desc is four 16-byte pieces");
 
 // Appends this lane's record to bucket `key` when `want`; wavefront-aggregated:
 // one atomic per distinct bucket among the wave's lanes.  Returns the slot or
@@ -213,12 +223,34 @@ __global__ __launch_bounds__(256) void dcn2_bucket_global_kernel(const BwdParams
     if (n < N) p.sidx[((size_t)b * p.G * KK + plane) * N + n] = !bs.any ? -1 : (slot >= 0 ? row : -2);
 }
 
+// Sink of the stores the column-gradient kernel issues with nothing to store
+// (its contents are never read; each device holds its own copy).  Waves of
+// different workgroups use different 1 KiB pieces, so that such stores do
+// not all queue on one cache line.
+constexpr int kTrashBytes = 64 * 1024;
+__device__ __attribute__((aligned(16))) unsigned char dcn2_trash[kTrashBytes];
+
 // ---------------------------------------------------------------------------
 // Column-gradient kernel: grad_offset, grad_mask and grad_input.
 // 512 threads; BN = 128 output pixels of one image per block.
 // ALDS: the W'^T fragments of a chunk (Mp*128 bytes, Mp <= 256) are staged in
-// LDS one chunk ahead; otherwise every wave reads its fragments from memory.
-template <typename T, int MCH, bool ALDS>
+// LDS two chunks ahead; otherwise every wave reads its fragments from memory.
+//
+// The K chunks run as a software pipeline with one barrier per step.  Step c:
+//   reduces chunk c (gathered and multiplied one step earlier) to
+//   grad_offset / grad_mask,
+//   loads W'^T and the offsets of chunk c+2,
+//   issues the corner gathers of chunk c+1 and stores its descriptors,
+//   computes the column gradient of chunk c+1 on the matrix cores,
+//   hands chunk c's column gradient to grad_input,
+// so a gather lands while the next MFMA and hand-off run, and the
+// vector-memory traffic of one chunk overlaps the matrix work of the next
+// instead of alternating with it.  The column-gradient stage and the
+// descriptors are double-buffered by chunk parity.  The stores of a step do
+// not depend on the data (a row with nothing to store goes to dcn2_trash),
+// so the compiler's in-order count of outstanding memory operations stays
+// exact and a gather is waited for without waiting for later stores.
+template <typename T, int MCH, bool ALDS, bool ONEM>
 __global__ __launch_bounds__(512) void dcn2_colgrad_kernel(const BwdParams p) {
     using M = Mma<T>;
     using frag = typename M::frag;
@@ -234,10 +266,20 @@ __global__ __launch_bounds__(512) void dcn2_colgrad_kernel(const BwdParams p) {
     constexpr int E = Unpack<T>::E;
     static_assert(CPL * sizeof(T) == 32, "reduction lane covers 32 bytes per corner");
 
-    __shared__ __attribute__((aligned(16))) float sCG[WPB][BN][LDC];
-    __shared__ Desc sD[BN];
+    // LDS, carved from one array so that nothing is padded:
+    //   sCG[2][WPB][BN][LDC] floats  column gradient of a chunk pair
+    //   sD[2][BN]                    descriptors of a chunk pair
+    //   sA[2][kAVec] uint4           staged W'^T of two chunks (ALDS only)
     constexpr int kAVec = 2048;  // 16-byte vectors of one staged chunk (Mp = 256)
-    __shared__ __attribute__((aligned(16))) uint4 sA[ALDS ? 2 : 1][ALDS ? kAVec : 1];
+    constexpr size_t kCGBytes = sizeof(float) * WPB * BN * LDC;
+    constexpr size_t kDBytes = sizeof(Desc) * BN;
+    constexpr size_t kABytes = ALDS ? sizeof(uint4) * kAVec : 0;
+    static_assert(kCGBytes % 16 == 0 && kDBytes % 16 == 0, "16-byte aligned carving");
+    __shared__ __attribute__((aligned(16))) char smem[2 * (kCGBytes + kDBytes + kABytes)];
+    typedef float CGStage[WPB][BN][LDC];
+    CGStage *const sCG = reinterpret_cast<CGStage *>(smem);
+    Desc(*const sD)[BN] = reinterpret_cast<Desc(*)[BN]>(smem + 2 * kCGBytes);
+    uint4(*const sA)[kAVec] = reinterpret_cast<uint4(*)[kAVec]>(smem + 2 * (kCGBytes + kDBytes));
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int blk = wave % NB, wr = wave / NB;
@@ -269,47 +311,49 @@ __global__ __launch_bounds__(512) void dcn2_colgrad_kernel(const BwdParams p) {
             }
         }
     };
-    if (nmc == 1) load_go(0);
 
     // Reduction-phase identity: pixel pr, channel quarter lq.
     const int pr = tid / QPP, lq = tid - pr * QPP;
     const int nr = n0 + pr;
+    const bool live = nr < N;
     int oyr = 0, oxr = 0;
-    if (nr < N) {
+    if (live) {
         oyr = nr / p.Wo;
         oxr = nr - oyr * p.Wo;
     }
-    float racc[3] = {0.0f, 0.0f, 0.0f};  // grad_mask, grad_off_y, grad_off_x (lq == 0)
+    float racc[3] = {0.0f, 0.0f, 0.0f};  // grad_mask, grad_off_y, grad_off_x of (pr, tap, g)
     int gmode = 0, gsidx = 0;             // grad_input mode of (pr, tap, g), see Desc
     const int *__restrict__ sidx = p.sidx + (size_t)b * p.G * KK * N;
 
-    // W'^T staging: chunk ch's fragments are Mp*8 consecutive 16-byte vectors
-    // (pack_weight_kernel layout 1 is k-block major); each thread moves up to
-    // four of them, loaded at the start of chunk ch-1 and written to the free
-    // LDS buffer at its end.
+    // W'^T staging: chunk c's fragments are Mp*8 consecutive 16-byte vectors
+    // (pack_weight_kernel layout 1 is k-block major); each thread moves four
+    // of them, loaded at the start of step c-2 and written to the LDS buffer
+    // of chunk c's parity at its end.  Vectors past Mp*8 (Mp < 256) re-read
+    // the last one and land in the unused tail of the buffer, so neither the
+    // loads nor the writes sit in a branch (the compiler would otherwise fuse
+    // each load with its write and wait for it on the spot).
     const int avec = p.Mp * 8;
     const uint4 *__restrict__ wtv = (const uint4 *)p.wt;
-    uint4 apf[4];
+    uint4 apf0, apf1, apf2, apf3;  // (named registers: as an array it was put in scratch)
     auto a_prefetch = [&](int c) __attribute__((always_inline)) {
         if constexpr (ALDS) {
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int i = tid + q * 512;
-                if (i < avec) apf[q] = wtv[(size_t)c * avec + i];
-            }
+            const uint4 *src = wtv + (size_t)c * avec;
+            apf0 = src[min(tid, avec - 1)];
+            apf1 = src[min(tid + 512, avec - 1)];
+            apf2 = src[min(tid + 1024, avec - 1)];
+            apf3 = src[min(tid + 1536, avec - 1)];
         }
     };
     auto a_commit = [&](int buf) __attribute__((always_inline)) {
         if constexpr (ALDS) {
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int i = tid + q * 512;
-                if (i < avec) sA[buf][i] = apf[q];
-            }
+            sA[buf][tid] = apf0;
+            sA[buf][tid + 512] = apf1;
+            sA[buf][tid + 1024] = apf2;
+            sA[buf][tid + 1536] = apf3;
         }
     };
 
-    // Offsets, mask and bucket row of (pr, chunk) are loaded one chunk ahead.
+    // Offsets, mask and bucket row of (pr, chunk), loaded two steps ahead.
     struct OM {
         T dy, dx, m;
         int sx;
@@ -317,87 +361,58 @@ __global__ __launch_bounds__(512) void dcn2_colgrad_kernel(const BwdParams p) {
     auto load_om = [&](int c, OM &o) __attribute__((always_inline)) {
         const int tg = c / cpg, tap = tg / p.G, g = tg - tap * p.G;
         const int plane = g * KK + tap;
-        const int nn = nr < N ? nr : 0;
+        const int nn = live ? nr : 0;
         const size_t ob = (size_t)plane * 2 * N + nn;
         o.dy = offs[ob];
         o.dx = offs[ob + N];
         o.m = msk ? msk[(size_t)plane * N + nn] : (T)1.0f;
         o.sx = sidx[(size_t)plane * N + nn];
     };
-    OM om_cur, om_nxt;
-    load_om(0, om_cur);
-    a_prefetch(0);
-    a_commit(0);
-    __syncthreads();
+    struct ChunkId {
+        int cc, tap, g;
+    };
+    auto chunk_id = [&](int c) __attribute__((always_inline)) {
+        ChunkId r;
+        const int tg = c / cpg;
+        r.cc = c - tg * cpg;
+        r.tap = tg / p.G;
+        r.g = tg - r.tap * p.G;
+        return r;
+    };
 
-    for (int ch = 0; ch < nch; ++ch) {
-        const int tg = ch / cpg, cc = ch - tg * cpg;
-        const int tap = tg / p.G, g = tg - tap * p.G;
-        const int ki = tap / p.kw, kj = tap - ki * p.kw;
+    // This thread's corner gathers of the chunk sampled last.
+    uint4 raw[4][2];
+    // this lane's 16 bytes of dcn2_trash
+    uint4 *const trash_v = reinterpret_cast<uint4 *>(dcn2_trash) +
+                           ((blockIdx.x * 8 + wave) % (kTrashBytes / 1024)) * 64 + lane;
+    T *const trash_t = reinterpret_cast<T *>(trash_v);
 
-        // next chunk's W'^T and offsets first: the MFMA below reads LDS only,
-        // and the corner gathers issued after these loads are what the
-        // reduction waits for
-        if (ch + 1 < nch) {
-            a_prefetch(ch + 1);
-            load_om(ch + 1, om_nxt);
-        }
-        // Sampling position of (pr, tap, g) and the corner gathers of this
-        // lane's channels; issued before the MFMA so their latency overlaps it.
+    // Sampling of chunk c (offsets o): corner gathers, and the descriptor of
+    // pixel pr into sD[X].
+    auto sample = [&](int X, int c, const OM &o) __attribute__((always_inline)) {
+        const ChunkId id = chunk_id(c);
+        const int ki = id.tap / p.kw, kj = id.tap - ki * p.kw;
         SamplePos sp;
         float mv = 0.0f;
-        const bool live = nr < N;
         if (live) {
-            const float y = (float)(oyr * p.sh - p.ph + ki * p.dh) + to_f32(om_cur.dy);
-            const float x = (float)(oxr * p.sw - p.pw + kj * p.dw) + to_f32(om_cur.dx);
-            mv = to_f32(om_cur.m);
+            const float y = (float)(oyr * p.sh - p.ph + ki * p.dh) + to_f32(o.dy);
+            const float x = (float)(oxr * p.sw - p.pw + kj * p.dw) + to_f32(o.dx);
+            mv = to_f32(o.m);
             sp = sample_pos(y, x, p.H, p.W);
         } else {
             sp = sample_pos(-2.0f, -2.0f, p.H, p.W);
         }
         const Corners cr = make_corners(sp, mv, p.W, cs);
-        uint4 raw[4][2];
-        {
-            const int cbase = g * p.Cgp + cc * KC + lq * CPL;
+        const int cbase = id.g * p.Cgp + id.cc * KC + lq * CPL;
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const uint4 *src = reinterpret_cast<const uint4 *>(xt + cr.off[q] + cbase);
-                raw[q][0] = src[0];
-                raw[q][1] = src[1];
-            }
+        for (int q = 0; q < 4; ++q) {
+            const uint4 *src = reinterpret_cast<const uint4 *>(xt + cr.off[q] + cbase);
+            raw[q][0] = src[0];
+            raw[q][1] = src[1];
         }
-        if (cc == 0) {
-            gmode = om_cur.sx == -1 ? 0 : (om_cur.sx >= 0 ? 1 : 2);
-            gsidx = om_cur.sx;
-        }
-
-        // Column gradient of this chunk: block (kb, nb), M share wr.
-        f32x16 acc;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
-        // A = W'^T in fragment order (pack_weight_kernel layout 1): the
-        // fragment (row block ch*KC/32 + kb, step ms) is one contiguous run.
-        const T *wrow = wt + ((size_t)(ch * KC / 32 + kb) * (p.Mp / KSTEP) + wr * (MPW / KSTEP)) *
-                                 64 * KPL + lane * KPL;
-        const T *arow = reinterpret_cast<const T *>(&sA[0][0]) + (size_t)(ch & 1) * kAVec * (16 / sizeof(T)) +
-                        ((size_t)kb * (p.Mp / KSTEP) + wr * (MPW / KSTEP)) * 64 * KPL + lane * KPL;
-        for (int mc = 0; mc < nmc; ++mc) {
-            if (nmc > 1) load_go(mc);
-#pragma unroll
-            for (int s = 0; s < NMS; ++s) {
-                const size_t fo = (size_t)(mc * (MCH / KSTEP) + s) * 64 * KPL;
-                const frag a = *reinterpret_cast<const frag *>((ALDS ? arow : wrow) + fo);
-                acc = M::mma(a, gfr[s], acc);
-            }
-        }
-        {
-            const int nl = nb * 32 + (lane & 31);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int kl = kb * 32 + 8 * j + 4 * (lane >> 5);
-                *reinterpret_cast<f32x4 *>(&sCG[wr][nl][kl]) =
-                    f32x4{acc[4 * j], acc[4 * j + 1], acc[4 * j + 2], acc[4 * j + 3]};
-            }
+        if (id.cc == 0) {
+            gmode = o.sx == -1 ? 0 : (o.sx >= 0 ? 1 : 2);
+            gsidx = o.sx;
         }
         if (lq == 0) {
             Desc d;
@@ -407,114 +422,190 @@ __global__ __launch_bounds__(512) void dcn2_colgrad_kernel(const BwdParams p) {
                 d.w[q] = cr.w[q];
             }
             d.sidx = gsidx;
-            d.m = mv;
             d.mode = gmode;
-            d.pad = 0;
-            sD[pr] = d;
+            d.pad0 = d.pad1 = 0;
+            d.m = mv;
+            d.valid = (sp.vy0 && sp.vx0 ? 1 : 0) | (sp.vy0 && sp.vx1 ? 2 : 0) |
+                      (sp.vy1 && sp.vx0 ? 4 : 0) | (sp.vy1 && sp.vx1 ? 8 : 0);
+            d.ly = sp.ly;
+            d.lx = sp.lx;
+            sD[X][pr] = d;
         }
-        __syncthreads();
+    };
 
-        // grad_mask / grad_offset: corner sums over this lane's channels.
-        {
-            float cgv[CPL];
+    // Column gradient of chunk c (block (kb, nb), M share wr) into sCG[X].
+    auto colgrad = [&](int X, int c) __attribute__((always_inline)) {
+        f32x16 acc;
 #pragma unroll
-            for (int c4 = 0; c4 < CPL / 4; ++c4) {
-                f32x4 v = *reinterpret_cast<const f32x4 *>(&sCG[0][pr][lq * CPL + 4 * c4]);
+        for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+        // A = W'^T in fragment order (pack_weight_kernel layout 1): the
+        // fragment (row block c*KC/32 + kb, step ms) is one contiguous run.
+        const T *wrow = wt + ((size_t)(c * KC / 32 + kb) * (p.Mp / KSTEP) + wr * (MPW / KSTEP)) *
+                                 64 * KPL + lane * KPL;
+        const T *arow = reinterpret_cast<const T *>(&sA[X][0]) +
+                        ((size_t)kb * (p.Mp / KSTEP) + wr * (MPW / KSTEP)) * 64 * KPL + lane * KPL;
+        if constexpr (ONEM) {
+            // gO is resident: no memory access here, so the MFMAs never wait
+            // for the gathers issued just before them
+#pragma unroll
+            for (int s = 0; s < NMS; ++s) {
+                const frag a = *reinterpret_cast<const frag *>((ALDS ? arow : wrow) +
+                                                               (size_t)s * 64 * KPL);
+                acc = M::mma(a, gfr[s], acc);
+            }
+        } else {
+            for (int mc = 0; mc < nmc; ++mc) {
+                load_go(mc);
+#pragma unroll
+                for (int s = 0; s < NMS; ++s) {
+                    const size_t fo = (size_t)(mc * (MCH / KSTEP) + s) * 64 * KPL;
+                    const frag a = *reinterpret_cast<const frag *>((ALDS ? arow : wrow) + fo);
+                    acc = M::mma(a, gfr[s], acc);
+                }
+            }
+        }
+        const int nl = nb * 32 + (lane & 31);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int kl = kb * 32 + 8 * j + 4 * (lane >> 5);
+            *reinterpret_cast<f32x4 *>(&sCG[X][wr][nl][kl]) =
+                f32x4{acc[4 * j], acc[4 * j + 1], acc[4 * j + 2], acc[4 * j + 3]};
+        }
+    };
+
+    // Chunk c (parity X): grad_mask / grad_offset from corner sums over this
+    // lane's channels.  The shuffles leave the sums in all QPP lanes of the
+    // pixel, which all store the same values at the last chunk of its (tap,
+    // group) (the lanes of a dead pixel store to dcn2_trash).
+    auto reduce_corners = [&](int X, int c) __attribute__((always_inline)) {
+        const ChunkId id = chunk_id(c);
+        float cgv[CPL];
+#pragma unroll
+        for (int c4 = 0; c4 < CPL / 4; ++c4) {
+            f32x4 v = *reinterpret_cast<const f32x4 *>(&sCG[X][0][pr][lq * CPL + 4 * c4]);
+#pragma unroll
+            for (int w2 = 1; w2 < WPB; ++w2)
+                v += *reinterpret_cast<const f32x4 *>(&sCG[X][w2][pr][lq * CPL + 4 * c4]);
+            cgv[4 * c4] = v[0];
+            cgv[4 * c4 + 1] = v[1];
+            cgv[4 * c4 + 2] = v[2];
+            cgv[4 * c4 + 3] = v[3];
+        }
+        float S[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            float s = 0.0f;
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                float v[E];
+                Unpack<T>::run(raw[q][u], v);
+#pragma unroll
+                for (int e = 0; e < E; ++e) s = fmaf(cgv[u * E + e], v[e], s);
+            }
+            S[q] = s;
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+#pragma unroll
+            for (int x = 1; x < QPP; x <<= 1) S[q] += shfl_xor_f(S[q], x);
+        }
+        // mask value, corner validity and fractions of the sample (one LDS read)
+        const DescFrac f = *reinterpret_cast<const DescFrac *>(&sD[X][pr].m);
+        const int vq = f.valid;
+        const float S0 = (vq & 1) ? S[0] : 0.0f, S1 = (vq & 2) ? S[1] : 0.0f;
+        const float S2 = (vq & 4) ? S[2] : 0.0f, S3 = (vq & 8) ? S[3] : 0.0f;
+        const float ly = f.ly, lx = f.lx, hy = 1.0f - ly, hx = 1.0f - lx;
+        const float mv = f.m;
+        racc[0] += hy * hx * S0 + hy * lx * S1 + ly * hx * S2 + ly * lx * S3;
+        racc[1] += mv * (hx * (S2 - S0) + lx * (S3 - S1));
+        racc[2] += mv * (hy * (S1 - S0) + ly * (S3 - S2));
+        if (id.cc == cpg - 1) {
+            const size_t plane = (size_t)id.g * KK + id.tap;
+            *(live ? goff + plane * 2 * N + nr : trash_t) = from_f32<T>(racc[1]);
+            *(live ? goff + plane * 2 * N + N + nr : trash_t + 1) = from_f32<T>(racc[2]);
+            if (gmask) *(live ? gmask + plane * N + nr : trash_t + 2) = from_f32<T>(racc[0]);
+            racc[0] = racc[1] = racc[2] = 0.0f;
+        }
+    };
+
+    // grad_input hand-off of chunk c (parity X): 8 lanes per pixel, 16 bytes
+    // (EPL channels) per lane.  A bucketed sample stores its masked
+    // column-gradient row (8 rows of 16-byte pieces per wave instruction) for
+    // the gather kernel; a sample of a full bucket adds to grad_input here
+    // with fp32 atomics (the one conditional memory operation of the step).
+    auto handoff = [&](int X, int c) __attribute__((always_inline)) {
+        const ChunkId id = chunk_id(c);
+        constexpr int EPL = 16 / sizeof(T), LPP = KC / EPL, PPI = 64 / LPP;
+        static_assert(LPP == 8, "8 lanes cover one chunk row");
+        const int co = lane % LPP, r = lane / LPP;
+#pragma unroll
+        for (int it = 0; it < BN / (8 * PPI); ++it) {
+            const int pl = (it * 8 + wave) * PPI + r;
+            const bool in = n0 + pl < N;
+            const Desc d = sD[X][pl];
+            float v[EPL];
+#pragma unroll
+            for (int e4 = 0; e4 < EPL / 4; ++e4) {
+                f32x4 x = *reinterpret_cast<const f32x4 *>(&sCG[X][0][pl][co * EPL + 4 * e4]);
 #pragma unroll
                 for (int w2 = 1; w2 < WPB; ++w2)
-                    v += *reinterpret_cast<const f32x4 *>(&sCG[w2][pr][lq * CPL + 4 * c4]);
-                cgv[4 * c4] = v[0];
-                cgv[4 * c4 + 1] = v[1];
-                cgv[4 * c4 + 2] = v[2];
-                cgv[4 * c4 + 3] = v[3];
+                    x += *reinterpret_cast<const f32x4 *>(&sCG[X][w2][pl][co * EPL + 4 * e4]);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[4 * e4 + e] = x[e];
             }
-            float S[4];
+            float mv8[EPL];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                float s = 0.0f;
+            for (int e = 0; e < EPL; ++e) mv8[e] = v[e] * d.m;
+            uint4 *row = reinterpret_cast<uint4 *>((T *)p.cgm + (size_t)d.sidx * p.Cgp + id.cc * KC +
+                                                   co * EPL);
+            *(in && d.mode == 1 ? row : trash_v) = pack16<T>(mv8);
+            if (in && d.mode == 2) {
+                float *gib = gi + id.g * p.Cgp + id.cc * KC + co * EPL;
 #pragma unroll
-                for (int u = 0; u < 2; ++u) {
-                    float v[E];
-                    Unpack<T>::run(raw[q][u], v);
+                for (int e = 0; e < EPL; ++e) {
+                    if (id.cc * KC + co * EPL + e >= p.Cg) continue;
 #pragma unroll
-                    for (int e = 0; e < E; ++e) s = fmaf(cgv[u * E + e], v[e], s);
-                }
-                S[q] = s;
-            }
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-#pragma unroll
-                for (int x = 1; x < QPP; x <<= 1) S[q] += shfl_xor_f(S[q], x);
-            }
-            if (lq == 0) {
-                const bool v00 = sp.vy0 && sp.vx0, v01 = sp.vy0 && sp.vx1;
-                const bool v10 = sp.vy1 && sp.vx0, v11 = sp.vy1 && sp.vx1;
-                const float S0 = v00 ? S[0] : 0.0f, S1 = v01 ? S[1] : 0.0f;
-                const float S2 = v10 ? S[2] : 0.0f, S3 = v11 ? S[3] : 0.0f;
-                const float ly = sp.ly, lx = sp.lx, hy = 1.0f - ly, hx = 1.0f - lx;
-                racc[0] += hy * hx * S0 + hy * lx * S1 + ly * hx * S2 + ly * lx * S3;
-                racc[1] += mv * (hx * (S2 - S0) + lx * (S3 - S1));
-                racc[2] += mv * (hy * (S1 - S0) + ly * (S3 - S2));
-                if (cc == cpg - 1) {
-                    if (live) {
-                        const size_t ob = ((size_t)g * KK + tap) * 2 * N + nr;
-                        goff[ob] = from_f32<T>(racc[1]);
-                        goff[ob + N] = from_f32<T>(racc[2]);
-                        if (gmask) gmask[((size_t)g * KK + tap) * N + nr] = from_f32<T>(racc[0]);
-                    }
-                    racc[0] = racc[1] = racc[2] = 0.0f;
+                    for (int q = 0; q < 4; ++q)
+                        if (d.w[q] != 0.0f) unsafeAtomicAdd(gib + d.off[q] + e, v[e] * d.w[q]);
                 }
             }
         }
+    };
 
-        // grad_input: 8 lanes per pixel, 16 bytes (EPL channels) per lane.
-        // A bucketed sample stores its masked column-gradient row (8 rows of
-        // 16-byte pieces per wave instruction) for the gather kernel; a sample
-        // of a full bucket adds to grad_input here with fp32 atomics.
-        {
-            constexpr int EPL = 16 / sizeof(T), LPP = KC / EPL, PPI = 64 / LPP;
-            static_assert(LPP == 8, "8 lanes cover one chunk row");
-            const int co = lane % LPP, r = lane / LPP;
-#pragma unroll
-            for (int it = 0; it < BN / (8 * PPI); ++it) {
-                const int pl = (it * 8 + wave) * PPI + r;
-                if (n0 + pl >= N) continue;
-                const Desc d = sD[pl];
-                if (d.mode == 0) continue;
-                float v[EPL];
-#pragma unroll
-                for (int e4 = 0; e4 < EPL / 4; ++e4) {
-                    f32x4 x = *reinterpret_cast<const f32x4 *>(&sCG[0][pl][co * EPL + 4 * e4]);
-#pragma unroll
-                    for (int w2 = 1; w2 < WPB; ++w2)
-                        x += *reinterpret_cast<const f32x4 *>(&sCG[w2][pl][co * EPL + 4 * e4]);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) v[4 * e4 + e] = x[e];
-                }
-                if (d.mode == 1) {
-                    float mv8[EPL];
-#pragma unroll
-                    for (int e = 0; e < EPL; ++e) mv8[e] = v[e] * d.m;
-                    *reinterpret_cast<uint4 *>((T *)p.cgm + (size_t)d.sidx * p.Cgp + cc * KC + co * EPL) =
-                        pack16<T>(mv8);
-                } else {
-                    float *gib = gi + g * p.Cgp + cc * KC + co * EPL;
-#pragma unroll
-                    for (int e = 0; e < EPL; ++e) {
-                        if (cc * KC + co * EPL + e >= p.Cg) continue;
-#pragma unroll
-                        for (int q = 0; q < 4; ++q)
-                            if (d.w[q] != 0.0f) unsafeAtomicAdd(gib + d.off[q] + e, v[e] * d.w[q]);
-                    }
-                }
-            }
-        }
-        if (ch + 1 < nch) {
-            a_commit((ch + 1) & 1);
-            om_cur = om_nxt;
-        }
+    // Prologue: chunk 0 sampled and multiplied, W'^T of chunk 1 staged,
+    // offsets of chunk 1 loaded.
+    OM om_c, om_n;  // offsets of the chunk sampled next, and of the one after
+    // Loads past the last chunk re-read the last chunk (clamped index) rather
+    // than sitting in a branch: with every memory operation of a step issued
+    // unconditionally the compiler's load counting stays exact across steps.
+    const int last = nch - 1;
+    if constexpr (ONEM) load_go(0);
+    load_om(0, om_c);
+    a_prefetch(0);
+    load_om(min(1, last), om_n);
+    sample(0, 0, om_c);
+    a_commit(0);
+    a_prefetch(min(1, last));
+    __syncthreads();
+    colgrad(0, 0);
+    a_commit(1);
+    om_c = om_n;
+    __syncthreads();
+
+    for (int c = 0; c < last; ++c) {
+        const int X = c & 1, Y = X ^ 1;
+        reduce_corners(X, c);
+        a_prefetch(min(c + 2, last));
+        load_om(min(c + 2, last), om_n);
+        sample(Y, c + 1, om_c);
+        colgrad(Y, c + 1);
+        handoff(X, c);
+        a_commit(X);  // chunk c+2 has chunk c's parity, and MFMA(c) is done
+        om_c = om_n;
         __syncthreads();
     }
+    reduce_corners(last & 1, last);
+    handoff(last & 1, last);
 }
 
 // ---------------------------------------------------------------------------
@@ -1034,20 +1125,23 @@ static hipError_t backward_t(const Geo &g, const BwdParams &p0, void *grad_input
             }
             if ((e = hipGetLastError()) != hipSuccess) return e;
             dim3 grid(p.tiles_per_img, g.B);
+            // W'^T staged in LDS when a chunk of it fits (Mp <= 256); gO resident
+            // in registers when one M chunk covers all rows.  fp32 keeps the
+            // 128-wide M chunk: 256 would hold 128 gO registers.
             const bool alds = g.Mp <= 256;
-            // fp32 keeps the 128-wide M chunk: 256 would hold 128 gO registers.
+#define DCN2_COLGRAD(MCHV)                                                                      \
+    do {                                                                                        \
+        if (g.Mp == MCHV) dcn2_colgrad_kernel<T, MCHV, true, true><<<grid, 512, 0, s>>>(p);     \
+        else if (alds) dcn2_colgrad_kernel<T, MCHV, true, false><<<grid, 512, 0, s>>>(p);       \
+        else dcn2_colgrad_kernel<T, MCHV, false, false><<<grid, 512, 0, s>>>(p);                \
+    } while (0)
             if constexpr (sizeof(T) == 2) {
-                if (g.Mp % 256 == 0) {
-                    if (alds) dcn2_colgrad_kernel<T, 256, true><<<grid, 512, 0, s>>>(p);
-                    else dcn2_colgrad_kernel<T, 256, false><<<grid, 512, 0, s>>>(p);
-                } else {
-                    if (alds) dcn2_colgrad_kernel<T, 128, true><<<grid, 512, 0, s>>>(p);
-                    else dcn2_colgrad_kernel<T, 128, false><<<grid, 512, 0, s>>>(p);
-                }
+                if (g.Mp % 256 == 0) DCN2_COLGRAD(256);
+                else DCN2_COLGRAD(128);
             } else {
-                if (alds) dcn2_colgrad_kernel<T, 128, true><<<grid, 512, 0, s>>>(p);
-                else dcn2_colgrad_kernel<T, 128, false><<<grid, 512, 0, s>>>(p);
+                DCN2_COLGRAD(128);
             }
+#undef DCN2_COLGRAD
             if ((e = hipGetLastError()) != hipSuccess) return e;
         }
         prof_end(DCN2_STAGE_BWD_COLGRAD, s);
