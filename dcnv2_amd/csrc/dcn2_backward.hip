@@ -877,13 +877,19 @@ __global__ __launch_bounds__(512) void dcn2_gradw_kernel(const BwdParams p) {
 // pixel (py, px) is corner 00 of cell (py, px), 01 of (py, px-1), 10 of
 // (py-1, px) and 11 of (py-1, px-1), so its value is the sum over the records
 // of those four cells of (bilinear corner weight) x (masked column-gradient
-// row), computed in a register with up to UNR independent row loads in
+// row), computed in a register with up to two batches of row loads in
 // flight.  Interior pixels (reachable from this tile's cells only) are
 // complete and added by a plain read-modify-write; the one-pixel border ring,
 // shared with the neighbouring tiles, is added with fp32 atomics.  This
 // replaces one global atomic per (sample, corner, channel) -- the reference's
 // col2im scatter, com.cu:553-609 -- by one per border pixel and channel.
 constexpr int kGatherCapMax = 4096;  // records of one bucket the LDS sort holds
+// Buffer offset past every bucket's rows (cap * Cgp * esz stays far below it),
+// so a load there reads 0.
+constexpr int kGatherOutOfRange = 0x7ffffff0;
+// static LDS of dcn2_gi_gather_kernel: cell counts and starts, sorted slots and fractions
+constexpr int kGatherStaticLds = kCellTile * kCellTile * 4 + (kCellTile * kCellTile + 1) * 4 +
+                                 kGatherCapMax * 2 + kGatherCapMax * 8;
 
 template <typename T>
 __global__ __launch_bounds__(512) void dcn2_gi_gather_kernel(const BwdParams p) {
@@ -894,6 +900,8 @@ __global__ __launch_bounds__(512) void dcn2_gi_gather_kernel(const BwdParams p) 
     __shared__ int cstart[NCELL + 1];
     __shared__ unsigned short sslot[kGatherCapMax];   // bucket slot, sorted by cell
     __shared__ float2 sfrac[kGatherCapMax];           // (ly, lx), sorted by cell
+    static_assert(sizeof(ccnt) + sizeof(cstart) + sizeof(sslot) + sizeof(sfrac) == kGatherStaticLds,
+                  "the launch's occupancy cap assumes this static LDS");
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int nb = p.B * p.G * p.nty * p.ntx;
@@ -958,20 +966,29 @@ __global__ __launch_bounds__(512) void dcn2_gi_gather_kernel(const BwdParams p) 
 
     // 2. pull every pixel of the window.  A wave takes PPW pixels at a time;
     //    lane (pixel slot ps, channel group co) sums the 16-byte slices (EPL
-    //    channels) of all rows of its pixel's records, UNR rows in flight, so
-    //    one load instruction reads PPW whole rows and the pixels' dependency
-    //    chains (LDS record lookup -> row load -> FMA) overlap.  Pixel
-    //    (py, px) is corner 00 of cell (py, px), 01 of (py, px-1), 10 of
-    //    (py-1, px) and 11 of (py-1, px-1).
+    //    channels) of all rows of its pixel's records, so one load instruction
+    //    reads PPW whole rows.  Pixel (py, px) is corner 00 of cell (py, px),
+    //    01 of (py, px-1), 10 of (py-1, px) and 11 of (py-1, px-1).
+    //    Rows come in batches of UNR from buffer loads over the bucket's rows:
+    //    a row index past the pixel's count reads 0 through an out-of-range
+    //    offset, so no load sits in a branch, the compiler's load counting
+    //    stays exact, and the next batch is in flight while one is summed
+    //    (two register sets, the loop unrolled by two).
     constexpr int EPL = 16 / sizeof(T);  // channels per lane per row
     constexpr int LPR = KC / EPL;        // lanes per row (8)
     constexpr int PPW = 64 / LPR;        // pixels per wave pass (8)
     constexpr int UNR = 4;
     static_assert(LPR == 8, "a 16-byte lane slice of a KC-channel row");
+    typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
     const int co = lane % LPR, ps = lane / LPR;
+    const int row_bytes = p.Cgp * (int)sizeof(T);
     for (int cc = 0; cc < cpg; ++cc) {
-        const T *__restrict__ rows = (const T *)p.cgm + ((size_t)bucket * p.cap) * p.Cgp +
-                                     cc * KC + co * EPL;
+        // buffer over the bucket's rows from this chunk's first channel (uniform);
+        // the lane's 16-byte slice goes into the offset
+        const T *rows = (const T *)p.cgm + ((size_t)bucket * p.cap) * p.Cgp + cc * KC;
+        const __amdgpu_buffer_rsrc_t rrs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<T *>(rows), (short)0, p.cap * row_bytes, 0x00020000);
+        const int slice = co * 16;
         for (int pl0 = wave * PPW; pl0 < TW * TW; pl0 += 8 * PPW) {
             const int pl = pl0 + ps;
             const int py = pl / TW, px = pl - py * TW;
@@ -991,32 +1008,52 @@ __global__ __launch_bounds__(512) void dcn2_gi_gather_kernel(const BwdParams p) 
             float sum[EPL];
 #pragma unroll
             for (int e = 0; e < EPL; ++e) sum[e] = 0.0f;
-            for (int j0 = 0; j0 < tot; j0 += UNR) {
-                uint4 raw[UNR];
-                float wgt[UNR];
+            // batch j0..j0+UNR-1 of this pixel's rows -> raw, wgt
+            auto fetch = [&](int j0, u32x4 (&raw)[UNR], float (&wgt)[UNR]) __attribute__((always_inline)) {
 #pragma unroll
                 for (int u = 0; u < UNR; ++u) {
+                    // selects only (no branch): record position of row j in the
+                    // corner-ordered ranges, its weight, and its row offset
+                    // (OR-ed out of range past the pixel's count)
                     const int j = j0 + u;
-                    const int q = (j >= e1) + (j >= e2) + (j >= e3);
-                    const int pos = (q == 0 ? beg[0] + j : q == 1 ? beg[1] + j - e1
-                                    : q == 2 ? beg[2] + j - e2 : beg[3] + j - e3);
-                    wgt[u] = 0.0f;
-                    raw[u] = make_uint4(0, 0, 0, 0);
-                    if (j < tot) {
-                        const float2 f = sfrac[pos];
-                        const float wy = (q & 2) ? f.x : 1.0f - f.x;
-                        const float wx = (q & 1) ? f.y : 1.0f - f.y;
-                        wgt[u] = wy * wx;
-                        raw[u] = *reinterpret_cast<const uint4 *>(rows + (size_t)sslot[pos] * p.Cgp);
-                    }
+                    const bool ok = j < tot, q1 = j >= e1, q2 = j >= e2, q3 = j >= e3;
+                    int pos = beg[0] + j;
+                    pos = q1 ? beg[1] + j - e1 : pos;
+                    pos = q2 ? beg[2] + j - e2 : pos;
+                    pos = q3 ? beg[3] + j - e3 : pos;
+                    pos = ok ? pos : 0;
+                    const float2 f = sfrac[pos];
+                    const int off = (int)sslot[pos] * row_bytes + slice;
+                    const float wy = q2 ? f.x : 1.0f - f.x;             // corners 10, 11
+                    const float wx = (q1 != q2) || q3 ? f.y : 1.0f - f.y;  // corners 01, 11
+                    wgt[u] = ok ? wy * wx : 0.0f;
+                    raw[u] = __builtin_amdgcn_raw_buffer_load_b128(
+                        rrs, off | (ok ? 0 : kGatherOutOfRange), 0, 0);
                 }
+            };
+            auto accumulate = [&](const u32x4 (&raw)[UNR], const float (&wgt)[UNR]) __attribute__((always_inline)) {
 #pragma unroll
                 for (int u = 0; u < UNR; ++u) {
                     float v[EPL];
-                    Unpack<T>::run(raw[u], v);
+                    Unpack<T>::run(make_uint4(raw[u].x, raw[u].y, raw[u].z, raw[u].w), v);
 #pragma unroll
                     for (int e = 0; e < EPL; ++e) sum[e] = fmaf(wgt[u], v[e], sum[e]);
                 }
+            };
+            u32x4 ra[UNR], rb[UNR];
+            float wa[UNR], wb[UNR];
+            // (scheduling barriers keep each batch's loads ahead of the sums of
+            // the previous one; left alone the scheduler groups the fetches)
+            fetch(0, ra, wa);
+            for (int j0 = 0; j0 < tot; j0 += 2 * UNR) {
+                fetch(j0 + UNR, rb, wb);
+                __builtin_amdgcn_sched_barrier(0);
+                accumulate(ra, wa);
+                __builtin_amdgcn_sched_barrier(0);
+                fetch(j0 + 2 * UNR, ra, wa);
+                __builtin_amdgcn_sched_barrier(0);
+                accumulate(rb, wb);
+                __builtin_amdgcn_sched_barrier(0);
             }
             if (tot == 0) continue;
             float *dst = gi + ((size_t)Y * p.W + X) * cs + cc * KC + co * EPL;
@@ -1146,7 +1183,19 @@ static hipError_t backward_t(const Geo &g, const BwdParams &p0, void *grad_input
         }
         prof_end(DCN2_STAGE_BWD_COLGRAD, s);
         prof_begin(DCN2_STAGE_BWD_GATHER, s);
-        dcn2_gi_gather_kernel<T><<<g.B * g.G * p.nty * p.ntx, 512, 0, s>>>(p);
+        {
+            // At most two workgroups per CU (extra LDS reserved at launch): each
+            // bucket's rows are read once per corner, and with three buckets per
+            // CU the rows in use no longer fit an XCD's L2 (measured at c2:
+            // 138 us at three per CU, 113 us at two, 119 us at one).
+            int dev = 0, lds_cu = 0;
+            if (hipGetDevice(&dev) != hipSuccess ||
+                hipDeviceGetAttribute(&lds_cu, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor,
+                                      dev) != hipSuccess)
+                lds_cu = 0;
+            const int pad = std::max(0, lds_cu / 3 + 256 - kGatherStaticLds);
+            dcn2_gi_gather_kernel<T><<<g.B * g.G * p.nty * p.ntx, 512, pad, s>>>(p);
+        }
         if ((e = hipGetLastError()) != hipSuccess) return e;
         prof_end(DCN2_STAGE_BWD_GATHER, s);
         // 3. grad_weight / grad_bias
