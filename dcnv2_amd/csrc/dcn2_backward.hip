@@ -754,9 +754,11 @@ __global__ __launch_bounds__(512) void dcn2_gradw_kernel(const BwdParams p) {
         }
     };
     // gO fragments of a whole tile are prefetched one step ahead for 2-byte
-    // types (8 registers of 16 bytes); fp32 (64 one-float steps) loads at use.
+    // types (8 registers of 16 bytes), in the set of the tile's parity (the
+    // loop is unrolled by two, so no register copies); fp32 (64 one-float
+    // steps) loads at use.
     constexpr bool PREA = KPL == 8;
-    frag a_cur[PREA ? NKS : 1], a_nxt[PREA ? NKS : 1];
+    frag a_set[2][PREA ? NKS : 1];
     auto load_a_tile = [&](frag (&a)[PREA ? NKS : 1], int t) __attribute__((always_inline)) {
         if constexpr (PREA) {
 #pragma unroll
@@ -764,22 +766,23 @@ __global__ __launch_bounds__(512) void dcn2_gradw_kernel(const BwdParams p) {
         }
     };
 
-    auto mfma_tile = [&](int t, int buf) __attribute__((always_inline)) {
+    auto mfma_tile = [&](auto s_c, int t) __attribute__((always_inline)) {
+        constexpr int buf = decltype(s_c)::value;
         if (!active) return;
 #pragma unroll
         for (int ks = 0; ks < NKS; ++ks) {
             frag a;
             if constexpr (PREA) {
-                a = a_cur[ks];
+                a = a_set[buf][ks];
             } else {
                 load_a(a, t, ks);
-            }
-            if (do_bias) {
-                if constexpr (KPL == 1) {
-                    bsum += to_f32(a);
-                } else {
+                if (do_bias) {
+                    if constexpr (KPL == 1) {
+                        bsum += to_f32(a);
+                    } else {
 #pragma unroll
-                    for (int e = 0; e < KPL; ++e) bsum += to_f32(a[e]);
+                        for (int e = 0; e < KPL; ++e) bsum += to_f32(a[e]);
+                    }
                 }
             }
 #pragma unroll
@@ -795,6 +798,17 @@ __global__ __launch_bounds__(512) void dcn2_gradw_kernel(const BwdParams p) {
                 acc[i] = M::mma(a, bf, acc[i]);
             }
         }
+        // grad_bias from the resident gO fragments, after the MFMA loop: a
+        // branch between MFMAs would keep the B-fragment reads from being
+        // issued ahead of them
+        if constexpr (PREA) {
+            if (do_bias) {
+#pragma unroll
+                for (int ks = 0; ks < NKS; ++ks)
+#pragma unroll
+                    for (int e = 0; e < KPL; ++e) bsum += to_f32(a_set[buf][ks][e]);
+            }
+        }
     };
 
     // One step for tile t (the it-th of this work item, set S = it % 2).
@@ -804,26 +818,16 @@ __global__ __launch_bounds__(512) void dcn2_gradw_kernel(const BwdParams p) {
         constexpr int O = S ^ 1;
         if constexpr (VEC) {
             load_om_tile(min(t + 3, t_last), om[O]);
-            if (active) load_a_tile(a_nxt, min(t + 1, t_last));
+            if (active) load_a_tile(a_set[O], min(t + 1, t_last));
             issue_tile(std::integral_constant<int, S>{}, min(t + 2, t_last), om[S]);
-            mfma_tile(t, S);
+            mfma_tile(s_c, t);
             store_stage(std::integral_constant<int, O>{}, O);
-            if constexpr (PREA) {
-#pragma unroll
-                for (int ks = 0; ks < NKS; ++ks) a_cur[ks] = a_nxt[ks];
-            }
         } else {
             if (t + 3 < t_end) load_om_tile(t + 3, om[O]);
-            if (t + 1 < t_end && active) load_a_tile(a_nxt, t + 1);
+            if (t + 1 < t_end && active) load_a_tile(a_set[O], t + 1);
             if (t + 2 < t_end) issue_tile(std::integral_constant<int, S>{}, t + 2, om[S]);
-            mfma_tile(t, S);
-            if (t + 1 < t_end) {
-                store_stage(std::integral_constant<int, O>{}, O);
-                if constexpr (PREA) {
-#pragma unroll
-                    for (int ks = 0; ks < NKS; ++ks) a_cur[ks] = a_nxt[ks];
-                }
-            }
+            mfma_tile(s_c, t);
+            if (t + 1 < t_end) store_stage(std::integral_constant<int, O>{}, O);
         }
         __syncthreads();
     };
@@ -832,14 +836,14 @@ __global__ __launch_bounds__(512) void dcn2_gradw_kernel(const BwdParams p) {
         if constexpr (VEC) {
             load_om_tile(t_begin, om[0]);
             load_om_tile(min(t_begin + 1, t_last), om[1]);
-            if (active) load_a_tile(a_cur, t_begin);
+            if (active) load_a_tile(a_set[0], t_begin);
             issue_tile(std::integral_constant<int, 0>{}, t_begin, om[0]);
             load_om_tile(min(t_begin + 2, t_last), om[0]);
             issue_tile(std::integral_constant<int, 1>{}, min(t_begin + 1, t_last), om[1]);
         } else {
             load_om_tile(t_begin, om[0]);
             if (t_begin + 1 < t_end) load_om_tile(t_begin + 1, om[1]);
-            if (active) load_a_tile(a_cur, t_begin);
+            if (active) load_a_tile(a_set[0], t_begin);
             issue_tile(std::integral_constant<int, 0>{}, t_begin, om[0]);
             if (t_begin + 2 < t_end) load_om_tile(t_begin + 2, om[0]);
             if (t_begin + 1 < t_end) issue_tile(std::integral_constant<int, 1>{}, t_begin + 1, om[1]);
@@ -847,10 +851,15 @@ __global__ __launch_bounds__(512) void dcn2_gradw_kernel(const BwdParams p) {
         store_stage(std::integral_constant<int, 0>{}, 0);
     }
     __syncthreads();
-    for (int t = t_begin; t < t_end; t += 2) {
-        step(std::integral_constant<int, 0>{}, t);
-        if (t + 1 < t_end) step(std::integral_constant<int, 1>{}, t + 1);
+    // pairs of steps with no condition inside (a skipped second step would
+    // give the loop head a second incoming path and the compiler's load
+    // counting a conservative merge); an odd last tile is peeled
+    int tt = t_begin;
+    for (; tt + 1 < t_end; tt += 2) {
+        step(std::integral_constant<int, 0>{}, tt);
+        step(std::integral_constant<int, 1>{}, tt + 1);
     }
+    if (tt < t_end) step(std::integral_constant<int, 0>{}, tt);
 
     if (!active) return;
 #pragma unroll
