@@ -51,6 +51,26 @@ def _events_ms(fn, steps, torch):
     return e0.elapsed_time(e1) / steps
 
 
+def _median_ms(fn, steps, torch, scrub=None):
+    """Median of per-call event times; with `scrub` (a large device buffer)
+    every call is preceded by a write of the whole buffer, which evicts the
+    L2 and the MALL (256 MB) so the call starts cold."""
+    evs = []
+    torch.cuda.synchronize()
+    for _ in range(steps):
+        if scrub is not None:
+            scrub.add_(1)
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        fn()
+        e1.record()
+        evs.append((e0, e1))
+    torch.cuda.synchronize()  # once: the GPU never idles between the calls
+    ts = sorted(e0.elapsed_time(e1) for e0, e1 in evs)
+    return ts[len(ts) // 2]
+
+
 def _stage_avgs(_C, names):
     out = {}
     for s in names:
@@ -150,6 +170,13 @@ def main():
         fwd()
     ms = _events_ms(fwd, args.steps, torch)
     value = fwd_w.readme_flops() / (ms * 1e-3) / 1e12
+    # per-call medians: hot (back to back) and cold (512 MiB scrub before each call)
+    hot_med = _median_ms(fwd, args.steps, torch)
+    scrub = torch.zeros(128 << 20, dtype=torch.float32, device=dev)
+    cold_med = _median_ms(fwd, max(10, args.steps // 4), torch, scrub)
+    del scrub
+    for _ in range(50):
+        fwd()
 
     # second loop with per-stage events for the kernel roofline
     _C.profile_enable(True)
@@ -162,7 +189,8 @@ def main():
 
     if args.mode == "fwd":
         print(json.dumps({"mode": "fwd", "ms_per_step": round(ms, 5),
-                          "kernel_ms": round(kern_ms, 5)}), flush=True)
+                          "kernel_ms": round(kern_ms, 5), "fwd_hot_median_ms": round(hot_med, 5),
+                          "fwd_cold_median_ms": round(cold_med, 5)}), flush=True)
         return
 
     # forward + backward at the same shape (config 2)
@@ -201,13 +229,16 @@ def main():
         "config": {"workload": "c1_readme_fwd: B8 C64 H128 W128 Cout256 3x3 s1 p1 d1 dg1 fp16, "
                                "forward", "global_batch": fwd_w.B, "parallelism": "single GPU"},
         "fwd_real_tflops": round(fwd_w.gemm_flops() / (ms * 1e-3) / 1e12, 2),
+        "fwd_hot_median_ms": round(hot_med, 5),
+        "fwd_cold_median_ms": round(cold_med, 5),
+        "fwd_cold_note": "median per call after a 512 MiB write that evicts L2 and MALL",
         "fwd_bwd_ms": round(fb_ms, 5),
         "fwd_bwd_workload": "c2_readme_fwd_bwd: same shape, forward + all five gradients, fp16",
         "stages_ms": {"forward": {k: round(v, 5) for k, v in fstages.items()},
                       "forward_backward": {k: round(v, 5) for k, v in bstages.items()}},
         "roofline": {
             "bound": "mfma",
-            "kernel": "dcn2_fwd_kernel (fused bilinear sampling + 32x32x16 f16 MFMA)",
+            "kernel": "dcn2_fwd_ws_kernel (fused bilinear sampling + 32x32x16 f16 MFMA)",
             "achieved": round(achieved, 2),
             "peak": PEAK_FP16_TFLOPS,
             "unit": "TFLOP/s",
@@ -217,6 +248,19 @@ def main():
             "kernel_ms": round(kern_ms, 5),
         },
     }
+    # Attainable dense fp16 MFMA rate of this GPU (probe in the forward kernel's
+    # issue pattern): the shader clock drops under MFMA work on toggling data.
+    try:
+        from dcnv2_amd.probe import mfma_ceiling
+        mc = mfma_ceiling()
+        result["mfma_ceiling"] = {
+            "unit": "TFLOP/s", "zero_operands": mc["zero"], "normal_operands": mc["normal"],
+            "fwd_kernel_frac_of_normal": round(achieved / mc["normal"]["tflops"], 4),
+            "note": "32x32x16 f16 MFMA, 4 MFMA waves per CU with a barrier per 32 MFMAs; "
+                    "N(0,1) operands lower the shader clock (power limit)",
+        }
+    except (OSError, RuntimeError) as exc:
+        result["mfma_ceiling"] = {"error": str(exc)}
     if not args.no_cpu:
         threads = max(1, min(16, os.cpu_count() or 1))
         result["cpu_baseline"] = cpu_baseline(fwd_w, args.cpu_seconds, threads)
