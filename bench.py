@@ -248,6 +248,30 @@ def main():
             "kernel_ms": round(kern_ms, 5),
         },
     }
+    # The DCN module (offset/mask predictor conv + operator) at the same shape,
+    # forward + backward: the fused path hands the predictor output to the
+    # kernels; the separate path materialises chunk / cat / sigmoid as the
+    # reference's DCN.forward does (dcn_v2_mm.py:133-137).
+    from dcnv2_amd.dcn_v2_mm import DCN
+    mod_ms = {}
+    x = t2["input"].clone().requires_grad_(True)
+    for fused in (True, False):
+        torch.manual_seed(0)
+        mod = DCN(fb_w.C, fb_w.Cout, fb_w.k, fb_w.stride, fb_w.pad, fb_w.dil, fb_w.groups,
+                  fused_offset_mask=fused).to(dev).half()
+        with torch.no_grad():
+            mod.conv_offset_mask.weight.normal_(0.0, 0.01)
+
+        def module_step():
+            y = mod(x)
+            y.backward(t2["grad_output"])
+
+        for _ in range(5):
+            module_step()
+        mod_ms["fused" if fused else "separate"] = round(_events_ms(module_step, fb_steps, torch), 5)
+    result["dcn_module_fwd_bwd_ms"] = dict(mod_ms, workload="DCN module (predictor conv + "
+                                           "operator), c2 shape, fp16, forward + backward")
+
     # Attainable dense fp16 MFMA rate of this GPU (probe in the forward kernel's
     # issue pattern): the shader clock drops under MFMA work on toggling data.
     try:

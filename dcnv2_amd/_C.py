@@ -69,6 +69,10 @@ def lib() -> ctypes.CDLL:
             L.dcn2_forward.restype = ctypes.c_int
             L.dcn2_backward.argtypes = [dp] + [vp] * 11 + [sz, vp]
             L.dcn2_backward.restype = ctypes.c_int
+            L.dcn2_forward_om.argtypes = [dp] + [vp] * 6 + [sz, vp]
+            L.dcn2_forward_om.restype = ctypes.c_int
+            L.dcn2_backward_om.argtypes = [dp] + [vp] * 9 + [sz, vp]
+            L.dcn2_backward_om.restype = ctypes.c_int
             L.dcn2_last_error.argtypes = []
             L.dcn2_last_error.restype = ctypes.c_char_p
             L.dcn2_version.argtypes = []
@@ -215,6 +219,82 @@ def dcn_v2_backward(input, weight, mask, offset, bias, grad_output, stride_h, st
         raise _err(name)
     del ws_buf
     return [grad_input, grad_offset, grad_mask, grad_weight, grad_bias]
+
+
+def _om_geometry(name, desc, om):
+    ho, wo = ctypes.c_int32(), ctypes.c_int32()
+    if lib().dcn2_output_shape(ctypes.byref(desc), ctypes.byref(ho), ctypes.byref(wo)) != 0:
+        raise _err(name)
+    want = (desc.batch, 3 * desc.deformable_groups * desc.kernel_h * desc.kernel_w, ho.value,
+            wo.value)
+    if tuple(om.shape) != want:
+        raise RuntimeError(f"{name}: om shape {tuple(om.shape)} != {want}")
+    return ho.value, wo.value
+
+
+def dcn_v2_forward_om(input, weight, om, bias, stride_h, stride_w, pad_h, pad_w,
+                      dilation_h=1, dilation_w=1, deformable_groups=1):
+    """Forward on the offset-and-mask predictor's raw output ``om``
+    ``[B, 3*G*kh*kw, Ho, Wo]``: offsets are its first ``2*G*kh*kw`` channels and
+    the mask is ``sigmoid`` of the rest, exactly the split the reference's
+    ``DCN.forward`` makes with ``chunk(3)`` / ``cat`` / ``sigmoid``
+    (``dcn_v2_mm.py:133-137``), done inside the kernels."""
+    name = "dcn_v2_forward_om"
+    _validate(name, input, weight, None, om, bias)
+    input, weight, om = input.contiguous(), weight.contiguous(), om.contiguous()
+    bias = bias.contiguous() if bias is not None else None
+    desc = make_desc(input, weight, stride_h, stride_w, pad_h, pad_w, dilation_h, dilation_w,
+                     deformable_groups)
+    ho, wo = _om_geometry(name, desc, om)
+    L = lib()
+    out = torch.empty((desc.batch, desc.out_channels, ho, wo), dtype=input.dtype,
+                      device=input.device)
+    with torch.cuda.device(input.device):
+        ws_buf, ws, ws_bytes = _workspace(L.dcn2_forward_workspace_bytes(ctypes.byref(desc)),
+                                          input.device)
+        stream = torch.cuda.current_stream(input.device).cuda_stream
+        rc = L.dcn2_forward_om(ctypes.byref(desc), _ptr(input), _ptr(weight), _ptr(om),
+                               _ptr(bias), _ptr(out), ctypes.c_void_p(ws), ws_bytes,
+                               ctypes.c_void_p(stream))
+    if rc != 0:
+        raise _err(name)
+    del ws_buf
+    return out
+
+
+def dcn_v2_backward_om(input, weight, om, bias, grad_output, stride_h, stride_w, pad_h, pad_w,
+                       dilation_h=1, dilation_w=1, deformable_groups=1):
+    """Backward of :func:`dcn_v2_forward_om`: returns ``[grad_input, grad_om,
+    grad_weight, grad_bias]``; ``grad_om`` holds the offset gradient and the
+    gradient of the mask logits (``grad_mask * mask * (1 - mask)``)."""
+    name = "dcn_v2_backward_om"
+    _validate(name, input, weight, None, om, bias, extra=[("grad_output", grad_output)])
+    input, weight, om = input.contiguous(), weight.contiguous(), om.contiguous()
+    grad_output = grad_output.contiguous()
+    desc = make_desc(input, weight, stride_h, stride_w, pad_h, pad_w, dilation_h, dilation_w,
+                     deformable_groups)
+    ho, wo = _om_geometry(name, desc, om)
+    if tuple(grad_output.shape) != (desc.batch, desc.out_channels, ho, wo):
+        raise RuntimeError(f"{name}: grad_output shape {tuple(grad_output.shape)} != "
+                           f"{(desc.batch, desc.out_channels, ho, wo)}")
+    L = lib()
+    grad_input = torch.empty_like(input)
+    grad_om = torch.empty_like(om)
+    grad_weight = torch.empty_like(weight)
+    grad_bias = torch.empty((desc.out_channels,), dtype=input.dtype, device=input.device) \
+        if bias is not None else None
+    with torch.cuda.device(input.device):
+        ws_buf, ws, ws_bytes = _workspace(L.dcn2_backward_workspace_bytes(ctypes.byref(desc)),
+                                          input.device)
+        stream = torch.cuda.current_stream(input.device).cuda_stream
+        rc = L.dcn2_backward_om(ctypes.byref(desc), _ptr(input), _ptr(weight), _ptr(om),
+                                _ptr(grad_output), _ptr(grad_input), _ptr(grad_om),
+                                _ptr(grad_weight), _ptr(grad_bias), ctypes.c_void_p(ws),
+                                ws_bytes, ctypes.c_void_p(stream))
+    if rc != 0:
+        raise _err(name)
+    del ws_buf
+    return [grad_input, grad_om, grad_weight, grad_bias]
 
 
 def version() -> str:

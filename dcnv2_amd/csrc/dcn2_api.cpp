@@ -87,6 +87,23 @@ static int make_geo(const dcn2_desc *d, Geo &g) {
         (long long)g.B * g.G * g.KK * g.Ho * g.Wo >= lim || g.H > 32767 || g.W > 32767)
         return fail(DCN2_ERANGE, "dcn2: problem exceeds the 32-bit per-image index range");
     g.Kp = (int)Kp;
+    // separate offset and mask tensors (dcn2_forward / dcn2_backward)
+    g.off_bs = 2LL * g.G * g.KK * g.N;
+    g.msk_bs = (long long)g.G * g.KK * g.N;
+    g.msk_logit = 0;
+    return DCN2_OK;
+}
+
+// The predictor-output layout of dcn2_forward_om / dcn2_backward_om: one
+// [B, 3*G*KK, Ho, Wo] tensor, offsets in its first 2*G*KK channels and mask
+// logits in the rest (the reference's chunk(3) / cat / sigmoid split,
+// dcn_v2_mm.py:133-137).  Returns the element offset of the mask channels.
+static int use_om_layout(Geo &g, long long &mask_off) {
+    if (3LL * g.G * g.KK * g.N >= 0x7fffffffLL)
+        return fail(DCN2_ERANGE, "dcn2: offset/mask tensor exceeds the 32-bit per-image index range");
+    g.off_bs = g.msk_bs = 3LL * g.G * g.KK * g.N;
+    g.msk_logit = 1;
+    mask_off = 2LL * g.G * g.KK * g.N;
     return DCN2_OK;
 }
 
@@ -137,6 +154,66 @@ static int check_launch(hipError_t e, const char *what) {
     return DCN2_OK;
 }
 
+static int forward_impl(const Geo &g, const void *input, const void *weight, const void *mask,
+                        const void *offset, const void *bias, void *output, void *workspace,
+                        size_t workspace_bytes, void *stream) {
+    int rc = DCN2_OK;
+    if (g.B > 0 && (!input || !offset || !output))
+        return fail(DCN2_EINVAL, "dcn2_forward: null input/offset/output pointer");
+    if (!weight) return fail(DCN2_EINVAL, "dcn2_forward: null weight pointer");
+    const FwdWorkspace ws = fwd_workspace(g);
+    if (!workspace || workspace_bytes < ws.total || ((uintptr_t)workspace & 255))
+        return fail(DCN2_EWORKSPACE,
+                    "dcn2_forward: workspace needs %zu bytes at 256-byte alignment (got %zu)",
+                    ws.total, workspace_bytes);
+    if (g.B == 0) return DCN2_OK;
+    hipStream_t s = (hipStream_t)stream;
+    char *base = (char *)workspace;
+    void *xt = base + ws.xt, *wp = base + ws.wp, *tab = base + ws.tab;
+    prof_begin(DCN2_STAGE_FWD_PACK, s);
+    if ((rc = check_launch(launch_pack(g, input, xt, weight, wp, tab, false, s), "pack")))
+        return rc;
+    prof_end(DCN2_STAGE_FWD_PACK, s);
+    prof_begin(DCN2_STAGE_FWD_MAIN, s);
+    rc = check_launch(launch_forward(g, xt, wp, tab, offset, mask, bias, output, s), "forward");
+    prof_end(DCN2_STAGE_FWD_MAIN, s);
+    return rc;
+}
+
+static int backward_impl(const Geo &g, const void *input, const void *weight, const void *mask,
+                         const void *offset, const void *grad_output, void *grad_input,
+                         void *grad_offset, void *grad_mask, void *grad_weight, void *grad_bias,
+                         void *workspace, size_t workspace_bytes, void *stream) {
+    int rc = DCN2_OK;
+
+    if (!weight || !grad_weight)
+        return fail(DCN2_EINVAL, "dcn2_backward: null weight/grad_weight pointer");
+    if (g.B > 0 && (!input || !offset || !grad_output || !grad_input || !grad_offset))
+        return fail(DCN2_EINVAL, "dcn2_backward: null input/offset/grad pointer");
+    if ((mask == nullptr) != (grad_mask == nullptr))
+        return fail(DCN2_EINVAL, "dcn2_backward: grad_mask must be given exactly when mask is");
+    const BwdWorkspace ws = bwd_workspace(g);
+    if (!workspace || workspace_bytes < ws.total || ((uintptr_t)workspace & 255))
+        return fail(DCN2_EWORKSPACE,
+                    "dcn2_backward: workspace needs %zu bytes at 256-byte alignment (got %zu)",
+                    ws.total, workspace_bytes);
+    hipStream_t s = (hipStream_t)stream;
+    char *base = (char *)workspace;
+    void *xt = base + ws.xt, *wt = base + ws.wt, *tab = base + ws.tab;
+    prof_begin(DCN2_STAGE_BWD_PACK, s);
+    if ((rc = check_launch(launch_pack(g, input, xt, weight, wt, tab, true, s), "pack")))
+        return rc;
+    prof_end(DCN2_STAGE_BWD_PACK, s);
+    return check_launch(launch_backward(g, xt, wt, tab, offset, mask, grad_output,
+                                        grad_input, grad_offset, grad_mask, grad_weight,
+                                        grad_bias, (float *)(base + ws.gi_acc),
+                                        (float *)(base + ws.gw_acc), (float *)(base + ws.gb_acc),
+                                        base + ws.cgm, base + ws.rec, (int *)(base + ws.cnt),
+                                        (int *)(base + ws.sidx), s),
+                        "backward");
+}
+
+
 }  // namespace dcn2
 
 using namespace dcn2;
@@ -164,32 +241,15 @@ size_t dcn2_backward_workspace_bytes(const dcn2_desc *d) {
     return bwd_workspace(g).total;
 }
 
+
 int dcn2_forward(const dcn2_desc *d, const void *input, const void *weight, const void *mask,
                  const void *offset, const void *bias, void *output, void *workspace,
                  size_t workspace_bytes, void *stream) {
     Geo g;
     int rc = make_geo(d, g);
     if (rc) return rc;
-    if (g.B > 0 && (!input || !offset || !output))
-        return fail(DCN2_EINVAL, "dcn2_forward: null input/offset/output pointer");
-    if (!weight) return fail(DCN2_EINVAL, "dcn2_forward: null weight pointer");
-    const FwdWorkspace ws = fwd_workspace(g);
-    if (!workspace || workspace_bytes < ws.total || ((uintptr_t)workspace & 255))
-        return fail(DCN2_EWORKSPACE,
-                    "dcn2_forward: workspace needs %zu bytes at 256-byte alignment (got %zu)",
-                    ws.total, workspace_bytes);
-    if (g.B == 0) return DCN2_OK;
-    hipStream_t s = (hipStream_t)stream;
-    char *base = (char *)workspace;
-    void *xt = base + ws.xt, *wp = base + ws.wp, *tab = base + ws.tab;
-    prof_begin(DCN2_STAGE_FWD_PACK, s);
-    if ((rc = check_launch(launch_pack(g, input, xt, weight, wp, tab, false, s), "pack")))
-        return rc;
-    prof_end(DCN2_STAGE_FWD_PACK, s);
-    prof_begin(DCN2_STAGE_FWD_MAIN, s);
-    rc = check_launch(launch_forward(g, xt, wp, tab, offset, mask, bias, output, s), "forward");
-    prof_end(DCN2_STAGE_FWD_MAIN, s);
-    return rc;
+    return forward_impl(g, input, weight, mask, offset, bias, output, workspace, workspace_bytes,
+                        stream);
 }
 
 int dcn2_backward(const dcn2_desc *d, const void *input, const void *weight, const void *mask,
@@ -199,31 +259,38 @@ int dcn2_backward(const dcn2_desc *d, const void *input, const void *weight, con
     Geo g;
     int rc = make_geo(d, g);
     if (rc) return rc;
-    if (!weight || !grad_weight)
-        return fail(DCN2_EINVAL, "dcn2_backward: null weight/grad_weight pointer");
-    if (g.B > 0 && (!input || !offset || !grad_output || !grad_input || !grad_offset))
-        return fail(DCN2_EINVAL, "dcn2_backward: null input/offset/grad pointer");
+    return backward_impl(g, input, weight, mask, offset, grad_output, grad_input, grad_offset,
+                         grad_mask, grad_weight, grad_bias, workspace, workspace_bytes, stream);
+}
+
+int dcn2_forward_om(const dcn2_desc *d, const void *input, const void *weight, const void *om,
+                    const void *bias, void *output, void *workspace, size_t workspace_bytes,
+                    void *stream) {
+    Geo g;
+    long long moff = 0;
+    int rc = make_geo(d, g);
+    if (rc || (rc = use_om_layout(g, moff))) return rc;
+    if (g.B > 0 && !om) return fail(DCN2_EINVAL, "dcn2_forward_om: null om pointer");
+    const void *mask = om ? (const char *)om + moff * g.esz : nullptr;
+    return forward_impl(g, input, weight, mask, om, bias, output, workspace, workspace_bytes, stream);
+}
+
+int dcn2_backward_om(const dcn2_desc *d, const void *input, const void *weight, const void *om,
+                     const void *grad_output, void *grad_input, void *grad_om, void *grad_weight,
+                     void *grad_bias, void *workspace, size_t workspace_bytes, void *stream) {
+    Geo g;
+    long long moff = 0;
+    int rc = make_geo(d, g);
+    if (rc || (rc = use_om_layout(g, moff))) return rc;
+    if (g.B > 0 && (!om || !grad_om))
+        return fail(DCN2_EINVAL, "dcn2_backward_om: null om/grad_om pointer");
+    // with B == 0 the buffers may be NULL; the mask pointers then stay NULL together
+    const void *mask = om ? (const char *)om + moff * g.esz : nullptr;
+    void *grad_mask = grad_om ? (char *)grad_om + moff * g.esz : nullptr;
     if ((mask == nullptr) != (grad_mask == nullptr))
-        return fail(DCN2_EINVAL, "dcn2_backward: grad_mask must be given exactly when mask is");
-    const BwdWorkspace ws = bwd_workspace(g);
-    if (!workspace || workspace_bytes < ws.total || ((uintptr_t)workspace & 255))
-        return fail(DCN2_EWORKSPACE,
-                    "dcn2_backward: workspace needs %zu bytes at 256-byte alignment (got %zu)",
-                    ws.total, workspace_bytes);
-    hipStream_t s = (hipStream_t)stream;
-    char *base = (char *)workspace;
-    void *xt = base + ws.xt, *wt = base + ws.wt, *tab = base + ws.tab;
-    prof_begin(DCN2_STAGE_BWD_PACK, s);
-    if ((rc = check_launch(launch_pack(g, input, xt, weight, wt, tab, true, s), "pack")))
-        return rc;
-    prof_end(DCN2_STAGE_BWD_PACK, s);
-    return check_launch(launch_backward(g, xt, wt, tab, offset, mask, grad_output,
-                                        grad_input, grad_offset, grad_mask, grad_weight,
-                                        grad_bias, (float *)(base + ws.gi_acc),
-                                        (float *)(base + ws.gw_acc), (float *)(base + ws.gb_acc),
-                                        base + ws.cgm, base + ws.rec, (int *)(base + ws.cnt),
-                                        (int *)(base + ws.sidx), s),
-                        "backward");
+        return fail(DCN2_EINVAL, "dcn2_backward_om: om and grad_om must both be given");
+    return backward_impl(g, input, weight, mask, om, grad_output, grad_input, grad_om, grad_mask,
+                         grad_weight, grad_bias, workspace, workspace_bytes, stream);
 }
 
 const char *dcn2_last_error(void) { return g_last_error.c_str(); }

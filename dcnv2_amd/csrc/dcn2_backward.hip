@@ -44,6 +44,11 @@ struct BwdParams {
     int *cnt;           // [nbuckets] records appended per bucket
     int *sidx;          // [B][G*KK][N] bucket-slot row of each sample; -1 no corner, -2 bucket full
     int ntx, nty, cap;  // cell tiles per row / column, bucket capacity
+    // offset / mask (and grad_offset / grad_mask) elements between images, and
+    // whether the mask buffer holds logits (see mask_value; grad_mask is then
+    // the gradient of the logits)
+    long long off_bs, msk_bs;
+    int msk_logit;
 };
 
 // Cell tiles of the grad_input gather: a sample with floor corner (y0, x0)
@@ -140,7 +145,7 @@ __device__ __forceinline__ BucketSample bucket_sample(const BwdParams &p, const 
     const bool live = n < N;
     const int nn = live ? n : 0;
     const int oy = nn / p.Wo, ox = nn - oy * p.Wo;
-    const size_t ob = ((size_t)b * p.G * KK + plane) * 2 * N + nn;
+    const size_t ob = (size_t)b * p.off_bs + (size_t)plane * 2 * N + nn;
     float dy, dx;
     if (esz_is_f32) {
         dy = ((const float *)offset_v)[ob];
@@ -289,12 +294,12 @@ __global__ __launch_bounds__(512) void dcn2_colgrad_kernel(const BwdParams p) {
     const int cpg = p.Cgp / KC, nch = KK * p.G * cpg, nmc = p.Mp / MCH;
 
     const T *__restrict__ xt = (const T *)p.xt + (size_t)b * p.H * p.W * cs;
-    const T *__restrict__ offs = (const T *)p.offset + (size_t)b * p.G * KK * 2 * N;
-    const T *__restrict__ msk = p.mask ? (const T *)p.mask + (size_t)b * p.G * KK * N : nullptr;
+    const T *__restrict__ offs = (const T *)p.offset + (size_t)b * p.off_bs;
+    const T *__restrict__ msk = p.mask ? (const T *)p.mask + (size_t)b * p.msk_bs : nullptr;
     const T *__restrict__ go = (const T *)p.gout + (size_t)b * p.Cout * N;
     const T *__restrict__ wt = (const T *)p.wt;
-    T *__restrict__ goff = (T *)p.goff + (size_t)b * p.G * KK * 2 * N;
-    T *__restrict__ gmask = p.gmask ? (T *)p.gmask + (size_t)b * p.G * KK * N : nullptr;
+    T *__restrict__ goff = (T *)p.goff + (size_t)b * p.off_bs;
+    T *__restrict__ gmask = p.gmask ? (T *)p.gmask + (size_t)b * p.msk_bs : nullptr;
     float *__restrict__ gi = p.gi_acc + (size_t)b * p.H * p.W * cs;
 
     // gO fragments (MFMA B operand, [m][n]): n = this wave's 32-pixel block.
@@ -397,7 +402,7 @@ __global__ __launch_bounds__(512) void dcn2_colgrad_kernel(const BwdParams p) {
         if (live) {
             const float y = (float)(oyr * p.sh - p.ph + ki * p.dh) + to_f32(o.dy);
             const float x = (float)(oxr * p.sw - p.pw + kj * p.dw) + to_f32(o.dx);
-            mv = to_f32(o.m);
+            mv = mask_value(to_f32(o.m), p.msk_logit);
             sp = sample_pos(y, x, p.H, p.W);
         } else {
             sp = sample_pos(-2.0f, -2.0f, p.H, p.W);
@@ -523,7 +528,9 @@ __global__ __launch_bounds__(512) void dcn2_colgrad_kernel(const BwdParams p) {
             const size_t plane = (size_t)id.g * KK + id.tap;
             *(live ? goff + plane * 2 * N + nr : trash_t) = from_f32<T>(racc[1]);
             *(live ? goff + plane * 2 * N + N + nr : trash_t + 1) = from_f32<T>(racc[2]);
-            if (gmask) *(live ? gmask + plane * N + nr : trash_t + 2) = from_f32<T>(racc[0]);
+            // d/d(logit) of sigmoid = s (1 - s), s = the mask value used
+            const float gm = p.msk_logit ? racc[0] * mv * (1.0f - mv) : racc[0];
+            if (gmask) *(live ? gmask + plane * N + nr : trash_t + 2) = from_f32<T>(gm);
             racc[0] = racc[1] = racc[2] = 0.0f;
         }
     };
@@ -680,7 +687,7 @@ __global__ __launch_bounds__(512) void dcn2_gradw_kernel(const BwdParams p) {
     SampleGeo sg;
     sg.H = p.H; sg.W = p.W; sg.kh = p.kh; sg.kw = p.kw; sg.sh = p.sh; sg.sw = p.sw;
     sg.ph = p.ph; sg.pw = p.pw; sg.dh = p.dh; sg.dw = p.dw; sg.G = p.G; sg.Cgp = p.Cgp;
-    sg.Wo = p.Wo; sg.N = N; sg.cs = cs; sg.KK = KK;
+    sg.Wo = p.Wo; sg.N = N; sg.cs = cs; sg.KK = KK; sg.msk_logit = p.msk_logit;
     const ChunkEnt cp = ((const ChunkEnt *)p.tab)[ch];
     // Two sampler register sets / offset-mask sets alternate between even and
     // odd tiles (loop unrolled by two): offset/mask loads run 3 tiles ahead of
@@ -692,8 +699,8 @@ __global__ __launch_bounds__(512) void dcn2_gradw_kernel(const BwdParams p) {
 
     auto load_om_tile = [&](int t, SlotOM<T, 1> &o) __attribute__((always_inline)) {
         const int b = t / p.tiles_per_img, n0 = (t - b * p.tiles_per_img) * BN;
-        smp[0].load_om(n0, cp.x, sg, tid, (const T *)p.offset + (size_t)b * p.G * KK * 2 * N,
-                       MASK ? (const T *)p.mask + (size_t)b * p.G * KK * N : nullptr, o);
+        smp[0].load_om(n0, cp.x, sg, tid, (const T *)p.offset + (size_t)b * p.off_bs,
+                       MASK ? (const T *)p.mask + (size_t)b * p.msk_bs : nullptr, o);
     };
     auto issue_tile = [&](auto set_c, int t, const SlotOM<T, 1> &o) __attribute__((always_inline)) {
         constexpr int set = decltype(set_c)::value;
@@ -1291,6 +1298,9 @@ hipError_t launch_backward(const Geo &g, const void *xt, const void *wt, const v
     p.gout = grad_out;
     p.goff = grad_offset;
     p.gmask = grad_mask;
+    p.off_bs = g.off_bs;
+    p.msk_bs = g.msk_bs;
+    p.msk_logit = mask ? g.msk_logit : 0;
     p.gi_acc = gi_acc;
     p.gw_acc = gw_acc;
     p.gb_acc = grad_bias ? gb_acc : nullptr;

@@ -67,6 +67,13 @@ template <> struct Mma<float> {
 template <typename T> __device__ __forceinline__ float to_f32(T v) { return (float)v; }
 template <typename T> __device__ __forceinline__ T from_f32(float v) { return (T)v; }
 
+// Modulation mask value from its stored value: the value itself, or
+// sigmoid(v) when the mask buffer holds the predictor's logits (the
+// reference's DCN module applies torch.sigmoid, dcn_v2_mm.py:137).
+__device__ __forceinline__ float mask_value(float v, int logit) {
+    return logit ? 1.0f / (1.0f + __expf(-v)) : v;
+}
+
 // Bilinear sampling descriptor of one (pixel, tap, group): the four corner
 // element offsets inside one image of xt (0 for a corner outside the image)
 // and the four corner weights with the modulation mask folded in (0 for a

@@ -39,6 +39,8 @@ struct FwdParams {
     int Mp;                     // padded output rows of the packed weight
     int ntiles, mtiles, tiles;  // pixel tiles per image, M tiles, B*ntiles*mtiles
     int out_vec;                // output rows can be written with 16-byte stores
+    long long off_bs, msk_bs;   // offset / mask elements between images
+    int msk_logit;              // mask buffer holds logits (see mask_value)
 };
 
 template <typename T, int WM, int WN, int IB, int JB, bool MASK>
@@ -78,14 +80,14 @@ __global__ __launch_bounds__(512) void dcn2_fwd_kernel(const FwdParams p) {
     const int nch = p.Kp / KC, last = nch - 1;
 
     const T *__restrict__ xt = (const T *)p.xt + (size_t)b * p.H * p.W * cs;
-    const T *__restrict__ offs = (const T *)p.offset + (size_t)b * p.G * KK * 2 * N;
-    const T *__restrict__ msk = MASK ? (const T *)p.mask + (size_t)b * p.G * KK * N : nullptr;
+    const T *__restrict__ offs = (const T *)p.offset + (size_t)b * p.off_bs;
+    const T *__restrict__ msk = MASK ? (const T *)p.mask + (size_t)b * p.msk_bs : nullptr;
     const ChunkEnt *__restrict__ tab = (const ChunkEnt *)p.tab;
 
     SampleGeo sg;
     sg.H = p.H; sg.W = p.W; sg.kh = p.kh; sg.kw = p.kw; sg.sh = p.sh; sg.sw = p.sw;
     sg.ph = p.ph; sg.pw = p.pw; sg.dh = p.dh; sg.dw = p.dw; sg.G = p.G; sg.Cgp = p.Cgp;
-    sg.Wo = p.Wo; sg.N = N; sg.cs = cs; sg.KK = KK;
+    sg.Wo = p.Wo; sg.N = N; sg.cs = cs; sg.KK = KK; sg.msk_logit = p.msk_logit;
 
     // Chunk c lives in set c % 2 of every pipeline buffer: offset/mask bits
     // om, corner gathers smp, A fragments a and the LDS stage sB.  The loop
@@ -622,8 +624,8 @@ __global__ __launch_bounds__(512) void dcn2_fwd_ws_kernel(const FwdParams p) {
         const T *offb, *mskb;
         int n_t, nn_t, by_t, bx_t;
         auto set_om_tile = [&](const Cursor &c) __attribute__((always_inline)) {
-            offb = (const T *)p.offset + (size_t)c.b * p.G * KK * 2 * N;
-            mskb = MASK ? (const T *)p.mask + (size_t)c.b * p.G * KK * N : nullptr;
+            offb = (const T *)p.offset + (size_t)c.b * p.off_bs;
+            mskb = MASK ? (const T *)p.mask + (size_t)c.b * p.msk_bs : nullptr;
             n_t = c.n0 + dpix;
             nn_t = n_t < N ? n_t : 0;
             const int oy = nn_t / p.Wo, ox = nn_t - oy * p.Wo;
@@ -659,7 +661,7 @@ __global__ __launch_bounds__(512) void dcn2_fwd_ws_kernel(const FwdParams p) {
             const float y = (float)(by_om + e.y) + to_f32(dy_om);
             const float x = (float)(bx_om + e.z) + to_f32(dx_om);
             float mv = 1.0f;
-            if constexpr (MASK) mv = to_f32(m_om);
+            if constexpr (MASK) mv = mask_value(to_f32(m_om), p.msk_logit);
             mv = n_om < N ? mv : 0.0f;  // pixels past N sample 0
             const Corners cr = make_corners(sample_pos(y, x, p.H, p.W), mv, p.W, cs);
             const uint4 wq = Blend8<T>::weights(cr.w);
@@ -839,6 +841,9 @@ hipError_t launch_forward(const Geo &g, const void *xt, const void *wp, const vo
     p.tab = tab;
     p.offset = offset;
     p.mask = mask;
+    p.off_bs = g.off_bs;
+    p.msk_bs = g.msk_bs;
+    p.msk_logit = mask ? g.msk_logit : 0;
     p.bias = bias;
     p.out = out;
     p.H = g.H;

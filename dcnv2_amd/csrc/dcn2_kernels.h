@@ -22,6 +22,11 @@ struct Geo {
     int Kp;         // packed GEMM K = KK*G*Cgp
     int BM;         // forward block tile in M (128 or 256)
     int Mp;         // Cout rounded up to BM
+    // Offset / mask buffers (and their gradients): elements between images,
+    // and whether the mask buffer holds logits that the kernels pass through
+    // sigmoid (the offset-and-mask predictor's raw output, dcn2_*_om).
+    long long off_bs, msk_bs;
+    int msk_logit;
 };
 
 // Workspace carving shared by forward and backward (byte offsets).

@@ -56,6 +56,7 @@ template <typename T> __device__ __forceinline__ uint4 pack16(const float *v) {
 // Geometry of one sampling problem (one image at a time).
 struct SampleGeo {
     int H, W, kh, kw, sh, sw, ph, pw, dh, dw, G, Cgp, Wo, N, cs, KK;
+    int msk_logit;  // mask buffer holds logits (see mask_value)
 };
 
 // Raw offset/mask bits and output-pixel coordinates of one chunk for the SPT
@@ -115,7 +116,7 @@ template <typename T, int SPT, bool MASK> struct Sampler {
             const float y = (float)(om.by[s] + e.y) + to_f32(om.dy[s]);
             const float x = (float)(om.bx[s] + e.z) + to_f32(om.dx[s]);
             float mv = 1.0f;
-            if constexpr (MASK) mv = to_f32(om.m[s]);
+            if constexpr (MASK) mv = mask_value(to_f32(om.m[s]), sg.msk_logit);
             mv = om.n[s] < sg.N ? mv : 0.0f;  // pixels past N sample 0
             const Corners c = make_corners(sample_pos(y, x, sg.H, sg.W), mv, sg.W, sg.cs);
             const int cbase = e.w + q * CPS;

@@ -13,10 +13,17 @@ Same names, positional order and return order as the reference:
   splits its output as ``o1, o2, mask = chunk(3)``, ``offset = cat(o1, o2)``,
   ``mask = sigmoid(mask)`` (``:105-146``).
 
-Difference from the reference, by design: ``dilation`` and
-``deformable_groups`` are forwarded to the operator (the reference accepts and
-drops them, ``:94-102``), appended as two optional trailing arguments of
-``dcn_v2_conv``.
+Differences from the reference, by design:
+
+* ``dilation`` and ``deformable_groups`` are forwarded to the operator (the
+  reference accepts and drops them, ``:94-102``), appended as two optional
+  trailing arguments of ``dcn_v2_conv``;
+* ``DCN.forward`` hands the predictor's raw output to the operator
+  (``dcn_v2_conv_om``): the kernels read the offsets from its first
+  ``2*G*kh*kw`` channels and apply ``sigmoid`` to the rest while loading, and
+  the backward returns the gradient of that tensor, so the ``chunk`` / ``cat`` /
+  ``sigmoid`` passes (``:133-137``) and their backward are not materialised.
+  ``DCN(..., fused_offset_mask=False)`` keeps the reference's separate steps.
 """
 from __future__ import annotations
 
@@ -61,6 +68,38 @@ class _DCNv2(Function):
 dcn_v2_conv = _DCNv2.apply
 
 
+class _DCNv2OM(Function):
+    """``dcn_v2_conv`` on the offset-and-mask predictor's raw output ``om``
+    ``[B, 3*G*kh*kw, Ho, Wo]``: equal to ``dcn_v2_conv(input, weight,
+    sigmoid(m), cat(o1, o2), bias, ...)`` with ``o1, o2, m = om.chunk(3, 1)``."""
+
+    @staticmethod
+    def forward(ctx, input, weight, om, bias, stride, padding, dilation=1, deformable_groups=1):
+        ctx.stride = _pair(stride)
+        ctx.padding = _pair(padding)
+        ctx.dilation = _pair(dilation)
+        ctx.deformable_groups = int(deformable_groups)
+        output = _C.dcn_v2_forward_om(
+            input, weight, om, bias,
+            ctx.stride[0], ctx.stride[1], ctx.padding[0], ctx.padding[1],
+            ctx.dilation[0], ctx.dilation[1], ctx.deformable_groups)
+        ctx.save_for_backward(input, weight, om, bias)
+        return output
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, grad_output):
+        input, weight, om, bias = ctx.saved_tensors
+        grad_input, grad_om, grad_weight, grad_bias = _C.dcn_v2_backward_om(
+            input, weight, om, bias, grad_output,
+            ctx.stride[0], ctx.stride[1], ctx.padding[0], ctx.padding[1],
+            ctx.dilation[0], ctx.dilation[1], ctx.deformable_groups)
+        return grad_input, grad_weight, grad_om, grad_bias, None, None, None, None
+
+
+dcn_v2_conv_om = _DCNv2OM.apply
+
+
 class DCNv2(nn.Module):
     def __init__(self, in_channels, out_channels, kernel_size, stride, padding, dilation=1,
                  deformable_groups=1):
@@ -97,9 +136,10 @@ class DCNv2(nn.Module):
 
 class DCN(DCNv2):
     def __init__(self, in_channels, out_channels, kernel_size, stride=1, padding=0,
-                 dilation=1, deformable_groups=1):
+                 dilation=1, deformable_groups=1, fused_offset_mask=True):
         super().__init__(in_channels, out_channels, kernel_size, stride, padding, dilation,
                          deformable_groups)
+        self.fused_offset_mask = fused_offset_mask
         channels_ = self.deformable_groups * 3 * self.kernel_size[0] * self.kernel_size[1]
         # The offset/mask predictor sees the same sampling grid as the DCN
         # (stride, padding and dilation), so its output matches Ho x Wo.
@@ -114,6 +154,9 @@ class DCN(DCNv2):
 
     def forward(self, input):
         out = self.conv_offset_mask(input)
+        if self.fused_offset_mask:
+            return dcn_v2_conv_om(input, self.weight, out, self.bias, self.stride, self.padding,
+                                  self.dilation, self.deformable_groups)
         o1, o2, mask = torch.chunk(out, 3, dim=1)
         offset = torch.cat((o1, o2), dim=1)
         mask = torch.sigmoid(mask)

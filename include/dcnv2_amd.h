@@ -92,6 +92,27 @@ DCN2_API int dcn2_backward(const dcn2_desc *d, const void *input, const void *we
                   void *grad_offset, void *grad_mask, void *grad_weight, void *grad_bias,
                   void *workspace, size_t workspace_bytes, void *stream);
 
+/* Forward and backward on the offset-and-mask predictor's raw output.  No
+ * counterpart in the reference's C++: they replace the chunk(3) / cat / sigmoid
+ * its DCN module applies to conv_offset_mask(x) before calling the operator
+ * (dcn_v2_mm.py:133-137), so the kernels read that tensor directly.
+ *   om      [B, 3*G*kh*kw, Ho, Wo]: channels [0, 2*G*kh*kw) are the offsets,
+ *           in the layout of dcn2_forward's `offset`; channels
+ *           [2*G*kh*kw, 3*G*kh*kw) are mask logits, mask = sigmoid(logit)
+ *           (computed in fp32 from the stored value).
+ *   grad_om same shape: the offset gradient in the first 2*G*kh*kw channels,
+ *           the gradient of the logits, grad_mask * mask * (1 - mask), in the
+ *           rest; fully overwritten.
+ * Everything else (including the workspace, sized by
+ * dcn2_forward_workspace_bytes / dcn2_backward_workspace_bytes of the same
+ * descriptor) is as in dcn2_forward / dcn2_backward. */
+DCN2_API int dcn2_forward_om(const dcn2_desc *d, const void *input, const void *weight, const void *om,
+                    const void *bias, void *output, void *workspace, size_t workspace_bytes,
+                    void *stream);
+DCN2_API int dcn2_backward_om(const dcn2_desc *d, const void *input, const void *weight, const void *om,
+                     const void *grad_output, void *grad_input, void *grad_om, void *grad_weight,
+                     void *grad_bias, void *workspace, size_t workspace_bytes, void *stream);
+
 /* Per-stage kernel timing (no counterpart in the reference, whose timing loops
  * live inside its forward, com_2buffer_cpasyc.cu:334-392).  While enabled on
  * the calling thread, every stage of dcn2_forward / dcn2_backward is bracketed

@@ -149,6 +149,18 @@ def test_entry_points_reject_before_any_launch(L):
     rc = L.dcn2_backward(ctypes.byref(d), fake, fake, None, fake, fake, fake, fake, None,
                          fake, None, vp(0x10000), need - 256, None)
     assert rc == 2
+    # the fused offset/mask entry points: null om, invalid descriptor, small workspace
+    rc = L.dcn2_forward_om(ctypes.byref(d), fake, fake, None, None, fake, fake, 1 << 20, None)
+    assert rc == 1 and "om" in L.dcn2_last_error().decode()
+    rc = L.dcn2_forward_om(ctypes.byref(desc(G=3)), fake, fake, fake, None, fake, fake,
+                           1 << 20, None)
+    assert rc == 1
+    rc = L.dcn2_backward_om(ctypes.byref(d), fake, fake, fake, fake, fake, None, fake, None,
+                            fake, 1 << 30, None)
+    assert rc == 1 and "grad_om" in L.dcn2_last_error().decode()
+    rc = L.dcn2_backward_om(ctypes.byref(d), fake, fake, fake, fake, fake, fake, fake, None,
+                            vp(0x10000), need - 256, None)
+    assert rc == 2
 
 
 # -- the Python operator surface -------------------------------------------------
@@ -164,6 +176,12 @@ def test_cpu_tensors_raise_runtime_error():
     with pytest.raises(RuntimeError, match="GPU"):
         _C.dcn_v2_backward(t["input"], t["weight"], t["mask"], t["offset"], t["bias"],
                            t["grad_output"], 1, 1, 1, 1)
+    om = torch.cat([t["offset"], t["mask"]], 1)
+    with pytest.raises(RuntimeError, match="GPU"):
+        _C.dcn_v2_forward_om(t["input"], t["weight"], om, t["bias"], 1, 1, 1, 1)
+    with pytest.raises(RuntimeError, match="GPU"):
+        _C.dcn_v2_backward_om(t["input"], t["weight"], om, t["bias"], t["grad_output"],
+                              1, 1, 1, 1)
 
 
 def test_module_without_gpu_raises_not_falls_back():
@@ -188,10 +206,26 @@ def _oracle_backward(input, weight, mask, offset, bias, grad_output, sh, sw, ph,
     return [torch.from_numpy(gi), torch.from_numpy(goff), gm, torch.from_numpy(gw), gb]
 
 
+def _oracle_forward_om(input, weight, om, bias, sh, sw, ph, pw, dh=1, dw=1, G=1):
+    n = om.shape[1] // 3 * 2
+    return _oracle_forward(input, weight, torch.sigmoid(om[:, n:]), om[:, :n], bias, sh, sw,
+                           ph, pw, dh, dw, G)
+
+
+def _oracle_backward_om(input, weight, om, bias, grad_output, sh, sw, ph, pw, dh=1, dw=1, G=1):
+    n = om.shape[1] // 3 * 2
+    s = torch.sigmoid(om[:, n:])
+    gi, goff, gm, gw, gb = _oracle_backward(input, weight, s, om[:, :n], bias, grad_output,
+                                            sh, sw, ph, pw, dh, dw, G)
+    return [gi, torch.cat([goff, gm * s * (1 - s)], 1), gw, gb]
+
+
 @pytest.fixture
 def oracle_C(monkeypatch):
     monkeypatch.setattr(dcn_v2_mm._C, "dcn_v2_forward", _oracle_forward)
     monkeypatch.setattr(dcn_v2_mm._C, "dcn_v2_backward", _oracle_backward)
+    monkeypatch.setattr(dcn_v2_mm._C, "dcn_v2_forward_om", _oracle_forward_om)
+    monkeypatch.setattr(dcn_v2_mm._C, "dcn_v2_backward_om", _oracle_backward_om)
 
 
 def test_dcn_v2_conv_gradients_in_reference_order(oracle_C):
@@ -215,12 +249,16 @@ def test_dcn_v2_conv_gradients_in_reference_order(oracle_C):
         assert rel_err(t.grad, ref_by_name[name].grad) < 1e-12, name
 
 
-def test_dcn_module_split_and_sigmoid(oracle_C):
+@pytest.mark.parametrize("fused", [True, False], ids=["fused_om", "separate"])
+def test_dcn_module_split_and_sigmoid(oracle_C, fused):
     """DCN: offset = cat(o1, o2), mask = sigmoid(third chunk) of the predictor
     output; with a non-zero predictor the whole module (predictor included)
-    matches the independent formulation, values and parameter gradients."""
+    matches the independent formulation, values and parameter gradients.  The
+    fused path hands the raw predictor output to the operator, whose backward
+    returns the gradient of the logits (grad_mask * s * (1 - s))."""
     torch.manual_seed(1)
-    mod = dcnv2_amd.DCN(4, 3, 3, stride=1, padding=1, dilation=1, deformable_groups=2).double()
+    mod = dcnv2_amd.DCN(4, 3, 3, stride=1, padding=1, dilation=1, deformable_groups=2,
+                        fused_offset_mask=fused).double()
     assert not mod.conv_offset_mask.weight.any()  # zero-initialised, reference :129-131
     with torch.no_grad():
         mod.conv_offset_mask.weight.normal_(0, 0.3)
