@@ -14,10 +14,11 @@
 //        coordinate weights per channel as com.cu:486-492 does)
 //     grad_input  scatter with fp32 atomics, lanes = channels so one wave
 //       instruction updates a contiguous channel run of one corner.
-//  gradw kernel    (grid: pixel-tile splits x K chunks x M chunks)
+//  gradw kernels   (grid: pixel-tile splits x K chunks x M chunks)
 //     gW[m][k] += sum_n gO[m][n] * col[k][n]           MFMA over re-sampled
 //       columns in LDS; partial tiles are added to an fp32 accumulator.
-//     grad_bias from the same gO fragments.
+//     grad_bias from the same gO fragments.  For 2-byte types gO is read in
+//     whole 128-byte lines and rearranged into MFMA fragments through LDS.
 //  finalize kernels: fp32 accumulators -> caller dtype and layout.
 #include <algorithm>
 #include <cstddef>
@@ -636,12 +637,10 @@ template <> struct GwLayout<bf16> {
 
 __device__ __forceinline__ int gw_swz(int k) { return ((k & 15) ^ (k >> 3)) & 15; }
 
-// VEC (2-byte types, N % 8 == 0, 16-byte aligned gO): gO fragments come from
-// buffer loads (rows past Cout read 0, pixels past N are zeroed with a select)
-// and every pipeline stage runs unconditionally on a clamped tile index, so
-// the loop has no divergent branches around its loads and the compiler's
-// load counting stays exact.  Otherwise a guarded element-wise path is used.
-template <typename T, int MB, bool MASK, bool VEC>
+// This kernel serves fp32 and gO rows that 16-byte loads cannot read (N % 8
+// != 0 or an unaligned base); 2-byte types with aligned rows take
+// dcn2_gradw_line_kernel below.  gO is read with guarded loads.
+template <typename T, int MB, bool MASK>
 __global__ __launch_bounds__(512) void dcn2_gradw_kernel(const BwdParams p) {
     using M = Mma<T>;
     using frag = typename M::frag;
@@ -734,29 +733,17 @@ __global__ __launch_bounds__(512) void dcn2_gradw_kernel(const BwdParams p) {
     float bsum = 0.0f;
 
     const bool aligned = p.go_vec != 0;
-    const uint32_t go_bytes = (uint32_t)((size_t)p.Cout * N * sizeof(T));
     auto load_a = [&](frag &a, int t, int ks) __attribute__((always_inline)) {
         const int b = t / p.tiles_per_img, n0 = (t - b * p.tiles_per_img) * BN;
         const int n = n0 + ks * KSTEP + (lane >> 5) * KPL;
-        if constexpr (VEC && KPL == 8) {
-            typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
-            const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-                const_cast<T *>((const T *)p.gout + (size_t)b * p.Cout * N), (short)0,
-                (int)go_bytes, 0x00020000);
-            u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(
-                rs, (int)(((unsigned)mrow * (unsigned)N + (unsigned)n) * sizeof(T)), 0, 0);
-            if (n >= N) v = u32x4{0u, 0u, 0u, 0u};
-            a = __builtin_bit_cast(frag, v);
+        const T *row = (const T *)p.gout + ((size_t)b * p.Cout + mrow) * N;
+        if (mrow < p.Cout && aligned && n + KPL <= N && KPL == 8) {
+            a = *reinterpret_cast<const frag *>(row + n);
         } else {
-            const T *row = (const T *)p.gout + ((size_t)b * p.Cout + mrow) * N;
-            if (mrow < p.Cout && aligned && n + KPL <= N && KPL == 8) {
-                a = *reinterpret_cast<const frag *>(row + n);
-            } else {
 #pragma unroll
-                for (int e = 0; e < KPL; ++e) {
-                    const T v = (mrow < p.Cout && n + e < N) ? row[n + e] : (T)0.0f;
-                    FragSet<T, KPL>::set(a, e, v);
-                }
+            for (int e = 0; e < KPL; ++e) {
+                const T v = (mrow < p.Cout && n + e < N) ? row[n + e] : (T)0.0f;
+                FragSet<T, KPL>::set(a, e, v);
             }
         }
     };
@@ -823,38 +810,21 @@ __global__ __launch_bounds__(512) void dcn2_gradw_kernel(const BwdParams p) {
     auto step = [&](auto s_c, int t) __attribute__((always_inline)) {
         constexpr int S = decltype(s_c)::value;
         constexpr int O = S ^ 1;
-        if constexpr (VEC) {
-            load_om_tile(min(t + 3, t_last), om[O]);
-            if (active) load_a_tile(a_set[O], min(t + 1, t_last));
-            issue_tile(std::integral_constant<int, S>{}, min(t + 2, t_last), om[S]);
-            mfma_tile(s_c, t);
-            store_stage(std::integral_constant<int, O>{}, O);
-        } else {
-            if (t + 3 < t_end) load_om_tile(t + 3, om[O]);
-            if (t + 1 < t_end && active) load_a_tile(a_set[O], t + 1);
-            if (t + 2 < t_end) issue_tile(std::integral_constant<int, S>{}, t + 2, om[S]);
-            mfma_tile(s_c, t);
-            if (t + 1 < t_end) store_stage(std::integral_constant<int, O>{}, O);
-        }
+        if (t + 3 < t_end) load_om_tile(t + 3, om[O]);
+        if (t + 1 < t_end && active) load_a_tile(a_set[O], t + 1);
+        if (t + 2 < t_end) issue_tile(std::integral_constant<int, S>{}, t + 2, om[S]);
+        mfma_tile(s_c, t);
+        if (t + 1 < t_end) store_stage(std::integral_constant<int, O>{}, O);
         __syncthreads();
     };
 
     if (t_begin < t_end) {
-        if constexpr (VEC) {
-            load_om_tile(t_begin, om[0]);
-            load_om_tile(min(t_begin + 1, t_last), om[1]);
-            if (active) load_a_tile(a_set[0], t_begin);
-            issue_tile(std::integral_constant<int, 0>{}, t_begin, om[0]);
-            load_om_tile(min(t_begin + 2, t_last), om[0]);
-            issue_tile(std::integral_constant<int, 1>{}, min(t_begin + 1, t_last), om[1]);
-        } else {
-            load_om_tile(t_begin, om[0]);
-            if (t_begin + 1 < t_end) load_om_tile(t_begin + 1, om[1]);
-            if (active) load_a_tile(a_set[0], t_begin);
-            issue_tile(std::integral_constant<int, 0>{}, t_begin, om[0]);
-            if (t_begin + 2 < t_end) load_om_tile(t_begin + 2, om[0]);
-            if (t_begin + 1 < t_end) issue_tile(std::integral_constant<int, 1>{}, t_begin + 1, om[1]);
-        }
+        load_om_tile(t_begin, om[0]);
+        if (t_begin + 1 < t_end) load_om_tile(t_begin + 1, om[1]);
+        if (active) load_a_tile(a_set[0], t_begin);
+        issue_tile(std::integral_constant<int, 0>{}, t_begin, om[0]);
+        if (t_begin + 2 < t_end) load_om_tile(t_begin + 2, om[0]);
+        if (t_begin + 1 < t_end) issue_tile(std::integral_constant<int, 1>{}, t_begin + 1, om[1]);
         store_stage(std::integral_constant<int, 0>{}, 0);
     }
     __syncthreads();
@@ -884,6 +854,213 @@ __global__ __launch_bounds__(512) void dcn2_gradw_kernel(const BwdParams p) {
     }
 }
 
+// Buffer offset at or past one image's gO bytes for dcn2_gradw_line_kernel
+// (a load there reads 0).
+constexpr int kGoOutOfRange = 0x7ffffff0;
+
+// grad_weight for 2-byte types whose gO rows take 16-byte loads (N % 8 == 0,
+// aligned base, at most kGoOutOfRange bytes per image): the work items,
+// sampling pipeline and LDS stage of dcn2_gradw_kernel, with gO read in whole
+// 128-byte lines.  The vector L1 looks up the lines of each group of
+// consecutive lanes separately; loading the 32x32 A fragments directly (lane l
+// = row l%32) touches a different line in every lane, 32 bytes of each.
+// Instead load j = 4*lam + q (lam = 64-pixel line, q = 8-row group) gives
+// lane l the 8-pixel chunk 8*lam + l%8 of row 8*q + l/8, so lanes 8g..8g+7
+// read one whole line, and each wave passes its own 8 KB through LDS, chunk c
+// of row r at 16-byte slot 17*r + c (the padding keeps both the stores and
+// the reads of 8 consecutive lanes on distinct banks, and every address is a
+// per-lane base plus a constant).  For K step i lane l reads chunk c = 2i +
+// l/32 of row l%32: its A fragment, whose B fragment is LDS block c.  K steps 0..3 only need line 0, so they are read back after the
+// first four loads.  Rows past Cout and pixels past N read 0 (buffer range).
+// Every stage runs unconditionally on a clamped tile index, so no load sits
+// in a divergent branch and the compiler's count of outstanding loads stays
+// exact across steps.
+template <typename T, int MB, bool MASK>
+__global__ __launch_bounds__(512) void dcn2_gradw_line_kernel(const BwdParams p) {
+    static_assert(sizeof(T) == 2, "2-byte types");
+    using M = Mma<T>;
+    using frag = typename M::frag;
+    constexpr int KC = M::KC, KSTEP = M::KSTEP;
+    constexpr int BN = 128, NKS = BN / KSTEP;
+    constexpr int KB = KC / 32;
+    constexpr int NBLK = MB * KB;
+    constexpr int BPW = NBLK >= 16 ? 2 : 1;  // blocks per wave
+    constexpr int CPS = KC / 4;
+    static_assert(KSTEP == 16 && NKS == 8 && BN == 128, "8 K steps of 16 pixels: one 8x8 transpose");
+
+    __shared__ __attribute__((aligned(16))) T sC[2][KC][BN];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    int mblk, kblk0;
+    if constexpr (BPW == 2) {
+        mblk = wave;
+        kblk0 = 0;
+    } else {
+        mblk = wave / KB;
+        kblk0 = wave - mblk * KB;
+    }
+    // work item as in dcn2_gradw_kernel (every wave is active: NBLK >= 8)
+    const int nch = p.Kp / KC, nmc = p.Mp / (32 * MB);
+    const int wi = xcd_remap(blockIdx.x, p.splits * nch * nmc);
+    const int mc = wi % nmc, ch = (wi / nmc) % nch, sp = wi / (nmc * nch);
+    const bool do_bias = p.gb_acc != nullptr && ch == 0 && kblk0 == 0;
+    const int rbase = mc * 32 * MB + mblk * 32;  // first gO row of this wave
+    const int mrow = rbase + (lane & 31);
+    const int N = p.Ho * p.Wo, KK = p.kh * p.kw, cs = p.G * p.Cgp;
+    const int T_total = p.B * p.tiles_per_img;
+    const int t_begin = (int)((long)T_total * sp / p.splits);
+    const int t_end = (int)((long)T_total * (sp + 1) / p.splits);
+
+    SampleGeo sg;
+    sg.H = p.H; sg.W = p.W; sg.kh = p.kh; sg.kw = p.kw; sg.sh = p.sh; sg.sw = p.sw;
+    sg.ph = p.ph; sg.pw = p.pw; sg.dh = p.dh; sg.dw = p.dw; sg.G = p.G; sg.Cgp = p.Cgp;
+    sg.Wo = p.Wo; sg.N = N; sg.cs = cs; sg.KK = KK; sg.msk_logit = p.msk_logit;
+    const ChunkEnt cp = ((const ChunkEnt *)p.tab)[ch];
+    // offset/mask loads 3 tiles ahead of the MFMA, corner gathers 2 ahead, the
+    // LDS stage and the gO loads 1 ahead; register sets by tile parity (the
+    // loop is unrolled by two, so no register copies)
+    Sampler<T, 1, MASK> smp[2];
+    smp[0].init(tid);
+    smp[1].init(tid);
+    SlotOM<T, 1> om[2];
+
+    auto load_om_tile = [&](int t, SlotOM<T, 1> &o) __attribute__((always_inline)) {
+        const int b = t / p.tiles_per_img, n0 = (t - b * p.tiles_per_img) * BN;
+        smp[0].load_om(n0, cp.x, sg, tid, (const T *)p.offset + (size_t)b * p.off_bs,
+                       MASK ? (const T *)p.mask + (size_t)b * p.msk_bs : nullptr, o);
+    };
+    auto issue_tile = [&](auto set_c, int t, const SlotOM<T, 1> &o) __attribute__((always_inline)) {
+        constexpr int set = decltype(set_c)::value;
+        const int b = t / p.tiles_per_img;
+        smp[set].issue(cp, sg, (const T *)p.xt + (size_t)b * p.H * p.W * cs, o);
+    };
+    auto store_stage = [&](auto set_c, int buf) __attribute__((always_inline)) {
+        constexpr int set = decltype(set_c)::value;
+        const int pl = tid >> 2;
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            float v[8];
+            smp[set].blend(0, u, v);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int k = smp[set].q * CPS + u * 8 + e;
+                sC[buf][k][((pl >> 3) ^ gw_swz(k)) * 8 + (pl & 7)] = (T)v[e];
+            }
+        }
+    };
+
+    // one image's gO rows (the host keeps them within kGoOutOfRange bytes)
+    const uint32_t go_bytes = (uint32_t)((size_t)p.Cout * N * sizeof(T));
+    const int lg = lane >> 3, lc = lane & 7;
+    uint4 ga[2][NKS];  // gO of a tile, by tile parity: loaded by line, then rearranged
+    auto load_a_tile = [&](uint4 (&a)[NKS], int t) __attribute__((always_inline)) {
+        const int b = t / p.tiles_per_img, n0 = (t - b * p.tiles_per_img) * BN;
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<T *>((const T *)p.gout + (size_t)b * p.Cout * N), (short)0, (int)go_bytes,
+            0x00020000);
+#pragma unroll
+        for (int j = 0; j < NKS; ++j) {
+            const unsigned row = (unsigned)(rbase + 8 * (j & 3) + lg);
+            const int n = n0 + 64 * (j >> 2) + 8 * lc;
+            const int off = (int)((row * (unsigned)N + (unsigned)n) * sizeof(T));
+            a[j] = __builtin_bit_cast(
+                uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, n < N ? off : kGoOutOfRange, 0, 0));
+        }
+    };
+    // per-wave rearrangement area: 32 rows x 17 slots of 16 bytes
+    __shared__ uint4 sG[8][32 * 17];
+    uint4 *const gw_st = &sG[wave][17 * lg + lc];                     // + 17*8*q + 8*lam
+    const uint4 *const gw_ld = &sG[wave][17 * (lane & 31) + (lane >> 5)];  // + 2*i
+    auto rearrange = [&](uint4 (&a)[NKS]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+#pragma unroll
+            for (int j = hf * 4; j < hf * 4 + 4; ++j) gw_st[17 * 8 * (j & 3) + 8 * (j >> 2)] = a[j];
+#pragma unroll
+            for (int i = hf * 4; i < hf * 4 + 4; ++i) a[i] = gw_ld[2 * i];
+        }
+    };
+
+    f32x16 acc[BPW];
+#pragma unroll
+    for (int i = 0; i < BPW; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][r] = 0.0f;
+    float bsum = 0.0f;
+
+    auto mfma_tile = [&](auto s_c) __attribute__((always_inline)) {
+        constexpr int buf = decltype(s_c)::value;
+        rearrange(ga[buf]);
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) {
+            const frag a = __builtin_bit_cast(frag, ga[buf][ks]);
+#pragma unroll
+            for (int i = 0; i < BPW; ++i) {
+                const int k = (kblk0 + i) * 32 + (lane & 31);
+                const int nblk = 2 * ks + (lane >> 5);
+                const frag bf = *reinterpret_cast<const frag *>(&sC[buf][k][(nblk ^ gw_swz(k)) * 8]);
+                acc[i] = M::mma(a, bf, acc[i]);
+            }
+        }
+        // grad_bias from the resident fragments, after the MFMA loop (a branch
+        // between MFMAs would keep the B-fragment reads from being issued
+        // ahead of them)
+        if (do_bias) {
+#pragma unroll
+            for (int ks = 0; ks < NKS; ++ks) {
+                const frag a = __builtin_bit_cast(frag, ga[buf][ks]);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) bsum += to_f32(a[e]);
+            }
+        }
+    };
+
+    const int t_last = t_end - 1;
+    auto step = [&](auto s_c, int t) __attribute__((always_inline)) {
+        constexpr int S = decltype(s_c)::value;
+        constexpr int O = S ^ 1;
+        load_om_tile(min(t + 3, t_last), om[O]);
+        load_a_tile(ga[O], min(t + 1, t_last));
+        issue_tile(std::integral_constant<int, S>{}, min(t + 2, t_last), om[S]);
+        mfma_tile(s_c);
+        store_stage(std::integral_constant<int, O>{}, O);
+        __syncthreads();
+    };
+
+    if (t_begin < t_end) {
+        load_om_tile(t_begin, om[0]);
+        load_om_tile(min(t_begin + 1, t_last), om[1]);
+        load_a_tile(ga[0], t_begin);
+        issue_tile(std::integral_constant<int, 0>{}, t_begin, om[0]);
+        load_om_tile(min(t_begin + 2, t_last), om[0]);
+        issue_tile(std::integral_constant<int, 1>{}, min(t_begin + 1, t_last), om[1]);
+        store_stage(std::integral_constant<int, 0>{}, 0);
+    }
+    __syncthreads();
+    // pairs of steps with no condition inside (a skipped second step would
+    // give the loop head a second incoming path and the compiler's load
+    // counting a conservative merge); an odd last tile is peeled
+    int tt = t_begin;
+    for (; tt + 1 < t_end; tt += 2) {
+        step(std::integral_constant<int, 0>{}, tt);
+        step(std::integral_constant<int, 1>{}, tt + 1);
+    }
+    if (tt < t_end) step(std::integral_constant<int, 0>{}, tt);
+
+#pragma unroll
+    for (int i = 0; i < BPW; ++i) {
+        const int k = ch * KC + (kblk0 + i) * 32 + (lane & 31);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int m = rbase + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            if (m < p.Cout) unsafeAtomicAdd(p.gw_acc + (size_t)m * p.Kp + k, acc[i][r]);
+        }
+    }
+    if (do_bias) {
+        bsum += shfl_xor_f(bsum, 32);
+        if (lane < 32 && mrow < p.Cout) unsafeAtomicAdd(p.gb_acc + mrow, bsum);
+    }
+}
 
 // ---------------------------------------------------------------------------
 // grad_input gather.  One block per bucket (image, group, 16x16 cell tile).
@@ -1233,15 +1410,21 @@ static hipError_t backward_t(const Geo &g, const BwdParams &p0, void *grad_input
             S = std::max(1, std::min(S, T_total));
             p.splits = S;
             const int grid = S * nch * nmc;
-            const bool vec = sizeof(T) == 2 && p.go_vec;
-#define DCN2_GRADW(MBV, MK, VC) dcn2_gradw_kernel<T, MBV, MK, VC><<<grid, 512, 0, s>>>(p)
-            if (mb == 8) {
-                if (p.mask) { if (vec) DCN2_GRADW(8, true, true); else DCN2_GRADW(8, true, false); }
-                else { if (vec) DCN2_GRADW(8, false, true); else DCN2_GRADW(8, false, false); }
-            } else {
-                if (p.mask) { if (vec) DCN2_GRADW(4, true, true); else DCN2_GRADW(4, true, false); }
-                else { if (vec) DCN2_GRADW(4, false, true); else DCN2_GRADW(4, false, false); }
+            bool line = false;  // 2-byte type with 16-byte gO rows: whole-line loads
+#define DCN2_GRADW(KERN, MBV, MK) KERN<T, MBV, MK><<<grid, 512, 0, s>>>(p)
+#define DCN2_GRADW_MB(KERN)                                                                      \
+    do {                                                                                         \
+        if (mb == 8) { if (p.mask) DCN2_GRADW(KERN, 8, true); else DCN2_GRADW(KERN, 8, false); } \
+        else { if (p.mask) DCN2_GRADW(KERN, 4, true); else DCN2_GRADW(KERN, 4, false); }         \
+    } while (0)
+            if constexpr (sizeof(T) == 2) {
+                if (p.go_vec && (long long)g.Cout * g.N * (long long)sizeof(T) <= kGoOutOfRange) {
+                    DCN2_GRADW_MB(dcn2_gradw_line_kernel);
+                    line = true;
+                }
             }
+            if (!line) DCN2_GRADW_MB(dcn2_gradw_kernel);
+#undef DCN2_GRADW_MB
 #undef DCN2_GRADW
             if ((e = hipGetLastError()) != hipSuccess) return e;
         }

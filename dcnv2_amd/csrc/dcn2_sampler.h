@@ -61,9 +61,11 @@ struct SampleGeo {
 
 // Raw offset/mask bits and output-pixel coordinates of one chunk for the SPT
 // slots of a thread.  Kept unconverted so that the load can be issued one
-// pipeline step before its first use without forcing an early wait.
+// pipeline step before its first use without forcing an early wait.  A slot
+// past the last pixel has by == kNoPixel.
+constexpr int kNoPixel = -2147483647 - 1;
 template <typename T, int SPT> struct SlotOM {
-    int n[SPT], by[SPT], bx[SPT];
+    int by[SPT], bx[SPT];
     T dy[SPT], dx[SPT], m[SPT];
 };
 
@@ -96,10 +98,9 @@ template <typename T, int SPT, bool MASK> struct Sampler {
 #pragma unroll
         for (int s = 0; s < SPT; ++s) {
             const int n = n0 + ((tid + s * 512) >> 2);
-            om.n[s] = n;
             const int nn = n < sg.N ? n : 0;
             const int oy = nn / sg.Wo, ox = nn - oy * sg.Wo;
-            om.by[s] = oy * sg.sh - sg.ph;
+            om.by[s] = n < sg.N ? oy * sg.sh - sg.ph : kNoPixel;
             om.bx[s] = ox * sg.sw - sg.pw;
             const size_t ob = (size_t)plane * 2 * sg.N + nn;
             om.dy[s] = offs[ob];
@@ -117,7 +118,7 @@ template <typename T, int SPT, bool MASK> struct Sampler {
             const float x = (float)(om.bx[s] + e.z) + to_f32(om.dx[s]);
             float mv = 1.0f;
             if constexpr (MASK) mv = mask_value(to_f32(om.m[s]), sg.msk_logit);
-            mv = om.n[s] < sg.N ? mv : 0.0f;  // pixels past N sample 0
+            mv = om.by[s] != kNoPixel ? mv : 0.0f;  // pixels past N sample 0
             const Corners c = make_corners(sample_pos(y, x, sg.H, sg.W), mv, sg.W, sg.cs);
             const int cbase = e.w + q * CPS;
 #pragma unroll

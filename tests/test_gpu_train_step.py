@@ -110,14 +110,28 @@ def test_train_step_matches_gridsample_network():
     our fp32 gradient must be at most 3x that of the grid_sample network's own
     fp32 run plus 1e-3 of the network's largest gradient.  A plumbing mistake
     (a swapped gradient, a missing sigmoid derivative) is an O(1) error and
-    fails by orders of magnitude; fp32 rounding does not reach 1e-3: the
-    largest measured is 5e-4, in the offset predictor of a 512-channel layer,
-    whose gradient is a difference of two 512-term corner sums.  Errors are absolute
+    fails by orders of magnitude; fp32 rounding stays below the bound (the
+    worst parameter measured sits at 0.66 of it, in every run).  Errors are absolute
     with a network-wide scale because some gradients are ~0 by construction
     (conv biases feeding BatchNorm) or near-cancelling sums, where a
     per-parameter relative error measures nothing; and the yardstick is the
     independent fp32 run because a dozen layers of backward and small-batch
-    BatchNorm amplify fp32 rounding past the per-op 1e-4."""
+    BatchNorm amplify fp32 rounding past the per-op 1e-4.
+
+    The networks' ordinary convolutions (the stem, the 3x3 convs and the
+    offset/mask predictors) run on torch's native kernels, not MIOpen: MIOpen
+    picks its convolution algorithm per run, and in about one run in four it
+    picked one whose rounding alone moved an offset predictor's gradient from
+    0.6x to 1.1x of the bound (measured with this library unchanged)."""
+    prev = torch.backends.cudnn.enabled
+    torch.backends.cudnn.enabled = False
+    try:
+        _train_step_vs_gridsample()
+    finally:
+        torch.backends.cudnn.enabled = prev
+
+
+def _train_step_vs_gridsample():
     torch.manual_seed(0)
     net = build_net((1, 1, 1, 1)).to(DEV)
     for m in net.modules():
