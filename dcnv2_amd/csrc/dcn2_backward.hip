@@ -52,6 +52,10 @@ struct BwdParams {
     int msk_logit;
 };
 
+// Buffer offset at or past one image's gO bytes (a load there reads 0); the
+// kernels that read gO through it require Cout*N*sizeof(T) <= kGoOutOfRange.
+constexpr int kGoOutOfRange = 0x7ffffff0;
+
 // Cell tiles of the grad_input gather: a sample with floor corner (y0, x0)
 // belongs to cell (y0+1, x0+1) of the (H+1) x (W+1) cell grid, and cells are
 // grouped in kCellTile x kCellTile tiles, one bucket per (image, group, tile).
@@ -314,6 +318,62 @@ __global__ __launch_bounds__(512) void dcn2_colgrad_kernel(const BwdParams p) {
                 const int m = mc * MCH + wr * MPW + s * KSTEP + (lane >> 5) * KPL + e;
                 const T v = (n < N && m < p.Cout) ? go[(size_t)m * N + n] : (T)0.0f;
                 FragSet<T, KPL>::set(gfr[s], e, v);
+            }
+        }
+    };
+    // The same fragments for 2-byte types with 16-byte gO rows (one M chunk):
+    // the block's gO tile [MCH][BN] is read with 16-byte buffer loads, 16
+    // consecutive lanes per row (the element loads above cost one instruction
+    // per value), issued before the sampling of chunk 0 and stored into the
+    // column-gradient area of the LDS after it; then every fragment is two
+    // transposing LDS reads (ds_read_b64_tr_b16: within 16 lanes, lane i
+    // receives element i%4 of the 4-element pieces that lanes i/4, 4 + i/4,
+    // 8 + i/4 and 12 + i/4 point at).  Lane L of a 16-lane group points at 4
+    // consecutive pixels of row L/4 of the fragment's 4-row half, so lane i
+    // receives rows 0..3 of that half at pixel i.  Row m keeps its 32-byte
+    // blocks XOR-permuted by m%4, which puts the 4 rows of one read on
+    // distinct banks.  Rows past Cout and pixels past N read 0 (buffer range).
+    constexpr int GQ = (sizeof(T) == 2 ? MCH * (BN / 8) : 512) / 512;  // 16-byte pieces per thread
+    const bool go_stage = ONEM && sizeof(T) == 2 && p.go_vec &&
+                          (size_t)p.Cout * N * sizeof(T) <= (size_t)kGoOutOfRange;
+    uint4 gst[GQ];
+    auto go_stage_issue = [&]() __attribute__((always_inline)) {
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<T *>(go), (short)0, (int)((size_t)p.Cout * N * sizeof(T)), 0x00020000);
+#pragma unroll
+        for (int q = 0; q < GQ; ++q) {
+            const int idx = tid + 512 * q, m = idx / (BN / 8), n = n0 + (idx % (BN / 8)) * 8;
+            const int off = (int)(((unsigned)m * (unsigned)N + (unsigned)n) * sizeof(T));
+            gst[q] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                   rs, n < N ? off : kGoOutOfRange, 0, 0));
+        }
+    };
+    T *const gstg = reinterpret_cast<T *>(smem);  // [MCH][BN], inside the sCG area
+    static_assert(sizeof(T) * MCH * BN <= kCGBytes * 2, "gO stage fits the column-gradient area");
+    auto go_stage_store = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int q = 0; q < GQ; ++q) {
+            const int idx = tid + 512 * q, m = idx / (BN / 8), n = (idx % (BN / 8)) * 8;
+            *reinterpret_cast<uint4 *>(gstg + m * BN + (n ^ ((m & 3) << 4))) = gst[q];
+        }
+    };
+    auto go_stage_read = [&]() __attribute__((always_inline)) {
+        if constexpr (sizeof(T) == 2) {
+            typedef short s16x4 __attribute__((ext_vector_type(4)));
+            const int g = lane >> 4, li = lane & 15;
+#pragma unroll
+            for (int s = 0; s < NMS; ++s) {
+                s16x4 h[2];
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    const int m = wr * MPW + s * KSTEP + 8 * (g >> 1) + 4 * hh + (li >> 2);
+                    const int nl = nb * 32 + 16 * (g & 1) + 4 * (li & 3);
+                    h[hh] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (__attribute__((address_space(3))) s16x4 *)(gstg + m * BN +
+                                                                    (nl ^ ((m & 3) << 4))));
+                }
+                gfr[s] = __builtin_bit_cast(frag, __builtin_shufflevector(h[0], h[1], 0, 1, 2, 3, 4, 5,
+                                                                           6, 7));
             }
         }
     };
@@ -587,14 +647,22 @@ __global__ __launch_bounds__(512) void dcn2_colgrad_kernel(const BwdParams p) {
     // than sitting in a branch: with every memory operation of a step issued
     // unconditionally the compiler's load counting stays exact across steps.
     const int last = nch - 1;
-    if constexpr (ONEM) load_go(0);
+    if constexpr (ONEM) {
+        if (go_stage) go_stage_issue();
+        else load_go(0);
+    }
     load_om(0, om_c);
     a_prefetch(0);
     load_om(min(1, last), om_n);
     sample(0, 0, om_c);
+    if (go_stage) go_stage_store();
     a_commit(0);
     a_prefetch(min(1, last));
     __syncthreads();
+    if (go_stage) {
+        go_stage_read();
+        __syncthreads();  // colgrad(0) writes the column-gradient area
+    }
     colgrad(0, 0);
     a_commit(1);
     om_c = om_n;
@@ -853,10 +921,6 @@ __global__ __launch_bounds__(512) void dcn2_gradw_kernel(const BwdParams p) {
         if (lane < 32 && mrow < p.Cout) unsafeAtomicAdd(p.gb_acc + mrow, bsum);
     }
 }
-
-// Buffer offset at or past one image's gO bytes for dcn2_gradw_line_kernel
-// (a load there reads 0).
-constexpr int kGoOutOfRange = 0x7ffffff0;
 
 // grad_weight for 2-byte types whose gO rows take 16-byte loads (N % 8 == 0,
 // aligned base, at most kGoOutOfRange bytes per image): the work items,
