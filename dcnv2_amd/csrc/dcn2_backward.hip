@@ -934,8 +934,11 @@ __global__ __launch_bounds__(512) void dcn2_gradw_kernel(const BwdParams p) {
 // of row r at 16-byte slot 17*r + c (the padding keeps both the stores and
 // the reads of 8 consecutive lanes on distinct banks, and every address is a
 // per-lane base plus a constant).  For K step i lane l reads chunk c = 2i +
-// l/32 of row l%32: its A fragment, whose B fragment is LDS block c.  K steps 0..3 only need line 0, so they are read back after the
-// first four loads.  Rows past Cout and pixels past N read 0 (buffer range).
+// l/32 of row l%32: its A fragment, whose B fragment is LDS block c.  The
+// loads of the next tile are stored at the end of the step that issued them
+// (they have had its MFMA phase to land), so the MFMAs only wait for LDS
+// reads, and one register set holds the loads in flight.  Rows past Cout and
+// pixels past N read 0 (buffer range).
 // Every stage runs unconditionally on a clamped tile index, so no load sits
 // in a divergent branch and the compiler's count of outstanding loads stays
 // exact across steps.
@@ -981,8 +984,8 @@ __global__ __launch_bounds__(512) void dcn2_gradw_line_kernel(const BwdParams p)
     sg.Wo = p.Wo; sg.N = N; sg.cs = cs; sg.KK = KK; sg.msk_logit = p.msk_logit;
     const ChunkEnt cp = ((const ChunkEnt *)p.tab)[ch];
     // offset/mask loads 3 tiles ahead of the MFMA, corner gathers 2 ahead, the
-    // LDS stage and the gO loads 1 ahead; register sets by tile parity (the
-    // loop is unrolled by two, so no register copies)
+    // column stage and the gO loads 1 ahead; sampler register sets by tile
+    // parity (the loop is unrolled by two, so no register copies)
     Sampler<T, 1, MASK> smp[2];
     smp[0].init(tid);
     smp[1].init(tid);
@@ -1016,7 +1019,7 @@ __global__ __launch_bounds__(512) void dcn2_gradw_line_kernel(const BwdParams p)
     // one image's gO rows (the host keeps them within kGoOutOfRange bytes)
     const uint32_t go_bytes = (uint32_t)((size_t)p.Cout * N * sizeof(T));
     const int lg = lane >> 3, lc = lane & 7;
-    uint4 ga[2][NKS];  // gO of a tile, by tile parity: loaded by line, then rearranged
+    uint4 ga[NKS];  // gO of the next tile, loaded by line; stored to LDS at the end of the step
     auto load_a_tile = [&](uint4 (&a)[NKS], int t) __attribute__((always_inline)) {
         const int b = t / p.tiles_per_img, n0 = (t - b * p.tiles_per_img) * BN;
         const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
@@ -1035,14 +1038,9 @@ __global__ __launch_bounds__(512) void dcn2_gradw_line_kernel(const BwdParams p)
     __shared__ uint4 sG[8][32 * 17];
     uint4 *const gw_st = &sG[wave][17 * lg + lc];                     // + 17*8*q + 8*lam
     const uint4 *const gw_ld = &sG[wave][17 * (lane & 31) + (lane >> 5)];  // + 2*i
-    auto rearrange = [&](uint4 (&a)[NKS]) __attribute__((always_inline)) {
+    auto stash = [&]() __attribute__((always_inline)) {
 #pragma unroll
-        for (int hf = 0; hf < 2; ++hf) {
-#pragma unroll
-            for (int j = hf * 4; j < hf * 4 + 4; ++j) gw_st[17 * 8 * (j & 3) + 8 * (j >> 2)] = a[j];
-#pragma unroll
-            for (int i = hf * 4; i < hf * 4 + 4; ++i) a[i] = gw_ld[2 * i];
-        }
+        for (int j = 0; j < NKS; ++j) gw_st[17 * 8 * (j & 3) + 8 * (j >> 2)] = ga[j];
     };
 
     f32x16 acc[BPW];
@@ -1054,10 +1052,12 @@ __global__ __launch_bounds__(512) void dcn2_gradw_line_kernel(const BwdParams p)
 
     auto mfma_tile = [&](auto s_c) __attribute__((always_inline)) {
         constexpr int buf = decltype(s_c)::value;
-        rearrange(ga[buf]);
+        frag af[NKS];
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) af[ks] = __builtin_bit_cast(frag, gw_ld[2 * ks]);
 #pragma unroll
         for (int ks = 0; ks < NKS; ++ks) {
-            const frag a = __builtin_bit_cast(frag, ga[buf][ks]);
+            const frag a = af[ks];
 #pragma unroll
             for (int i = 0; i < BPW; ++i) {
                 const int k = (kblk0 + i) * 32 + (lane & 31);
@@ -1072,9 +1072,8 @@ __global__ __launch_bounds__(512) void dcn2_gradw_line_kernel(const BwdParams p)
         if (do_bias) {
 #pragma unroll
             for (int ks = 0; ks < NKS; ++ks) {
-                const frag a = __builtin_bit_cast(frag, ga[buf][ks]);
 #pragma unroll
-                for (int e = 0; e < 8; ++e) bsum += to_f32(a[e]);
+                for (int e = 0; e < 8; ++e) bsum += to_f32(af[ks][e]);
             }
         }
     };
@@ -1084,21 +1083,23 @@ __global__ __launch_bounds__(512) void dcn2_gradw_line_kernel(const BwdParams p)
         constexpr int S = decltype(s_c)::value;
         constexpr int O = S ^ 1;
         load_om_tile(min(t + 3, t_last), om[O]);
-        load_a_tile(ga[O], min(t + 1, t_last));
+        load_a_tile(ga, min(t + 1, t_last));
         issue_tile(std::integral_constant<int, S>{}, min(t + 2, t_last), om[S]);
         mfma_tile(s_c);
         store_stage(std::integral_constant<int, O>{}, O);
+        stash();  // after this wave's reads of the current tile (LDS is in order per wave)
         __syncthreads();
     };
 
     if (t_begin < t_end) {
         load_om_tile(t_begin, om[0]);
         load_om_tile(min(t_begin + 1, t_last), om[1]);
-        load_a_tile(ga[0], t_begin);
+        load_a_tile(ga, t_begin);
         issue_tile(std::integral_constant<int, 0>{}, t_begin, om[0]);
         load_om_tile(min(t_begin + 2, t_last), om[0]);
         issue_tile(std::integral_constant<int, 1>{}, min(t_begin + 1, t_last), om[1]);
         store_stage(std::integral_constant<int, 0>{}, 0);
+        stash();
     }
     __syncthreads();
     // pairs of steps with no condition inside (a skipped second step would
