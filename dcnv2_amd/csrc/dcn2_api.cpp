@@ -144,6 +144,8 @@ BwdWorkspace bwd_workspace(const Geo &g) {
     o += align256((size_t)gg.nbuckets * sizeof(int) + 16);
     w.sidx = o;
     o += align256((size_t)g.B * g.G * g.KK * g.N * sizeof(int));
+    w.ring = o;
+    o += align256((size_t)gg.nbuckets * kGatherRing * g.Cgp * sizeof(float));
     w.total = o;
     return w;
 }
@@ -209,7 +211,7 @@ static int backward_impl(const Geo &g, const void *input, const void *weight, co
                                         grad_bias, (float *)(base + ws.gi_acc),
                                         (float *)(base + ws.gw_acc), (float *)(base + ws.gb_acc),
                                         base + ws.cgm, base + ws.rec, (int *)(base + ws.cnt),
-                                        (int *)(base + ws.sidx), s),
+                                        (int *)(base + ws.sidx), (float *)(base + ws.ring), s),
                         "backward");
 }
 

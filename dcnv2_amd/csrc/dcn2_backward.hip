@@ -45,6 +45,7 @@ struct BwdParams {
     int *cnt;           // [nbuckets] records appended per bucket
     int *sidx;          // [B][G*KK][N] bucket-slot row of each sample; -1 no corner, -2 bucket full
     int ntx, nty, cap;  // cell tiles per row / column, bucket capacity
+    float *ring;        // [nbuckets][kRing][Cgp] grad_input sums of each window's border ring
     // offset / mask (and grad_offset / grad_mask) elements between images, and
     // whether the mask buffer holds logits (see mask_value; grad_mask is then
     // the gradient of the logits)
@@ -60,6 +61,17 @@ constexpr int kGoOutOfRange = 0x7ffffff0;
 // belongs to cell (y0+1, x0+1) of the (H+1) x (W+1) cell grid, and cells are
 // grouped in kCellTile x kCellTile tiles, one bucket per (image, group, tile).
 constexpr int kCellTile = 16;
+// The pixels a tile's cells reach form a (kCellTile+1)^2 window whose border
+// ring (kRing pixels) it shares with the neighbouring tiles.
+constexpr int kRing = 4 * kCellTile;
+static_assert(kRing == kGatherRing, "workspace sizing uses kGatherRing");
+
+// Position of window pixel (py, px) in its border ring: the top row, the
+// bottom row, then the left and right columns without their corners.
+__device__ __forceinline__ int ring_index(int py, int px) {
+    constexpr int TS = kCellTile, TW = kCellTile + 1;
+    return py == 0 ? px : py == TS ? TW + px : px == 0 ? 2 * TW + py - 1 : 2 * TW + TS - 1 + py - 1;
+}
 
 // Per-pixel sampling record written by the reduction phase for the
 // grad_input phase.  mode 0: no corner inside the image (nothing to add);
@@ -113,6 +125,15 @@ template <typename T> struct FragSet<T, 1> {
 template <typename T> struct FragSet<T, 8> {
     template <typename F> static __device__ __forceinline__ void set(F &f, int e, T v) { f[e] = v; }
 };
+
+// f(integral_constant<int, I>) for I = B .. E-1, unrolled at compile time
+// (for builtins whose operand must be a constant).
+template <int B, int E, typename F> __device__ __forceinline__ void static_for(F &&f) {
+    if constexpr (B < E) {
+        f(std::integral_constant<int, B>{});
+        static_for<B + 1, E>(f);
+    }
+}
 
 __device__ __forceinline__ float shfl_xor_f(float v, int mask) {
     return __shfl_xor(v, mask, 64);
@@ -1137,10 +1158,11 @@ __global__ __launch_bounds__(512) void dcn2_gradw_line_kernel(const BwdParams p)
 // of those four cells of (bilinear corner weight) x (masked column-gradient
 // row), computed in a register with up to two batches of row loads in
 // flight.  Interior pixels (reachable from this tile's cells only) are
-// complete and added by a plain read-modify-write; the one-pixel border ring,
-// shared with the neighbouring tiles, is added with fp32 atomics.  This
-// replaces one global atomic per (sample, corner, channel) -- the reference's
-// col2im scatter, com.cu:553-609 -- by one per border pixel and channel.
+// complete and added by a plain read-modify-write; the sums of the one-pixel
+// border ring, shared with the neighbouring tiles, are stored per bucket
+// (kRing pixels) and added by finalize_gi_kernel.  This replaces the global
+// atomic per (sample, corner, channel) of the reference's col2im scatter
+// (com.cu:553-609) with plain stores.
 constexpr int kGatherCapMax = 4096;  // records of one bucket the LDS sort holds
 // Buffer offset past every bucket's rows (cap * Cgp * esz stays far below it),
 // so a load there reads 0.
@@ -1227,7 +1249,7 @@ __global__ __launch_bounds__(512) void dcn2_gi_gather_kernel(const BwdParams p) 
     //    channels) of all rows of its pixel's records, so one load instruction
     //    reads PPW whole rows.  Pixel (py, px) is corner 00 of cell (py, px),
     //    01 of (py, px-1), 10 of (py-1, px) and 11 of (py-1, px-1).
-    //    Rows come in batches of UNR from buffer loads over the bucket's rows:
+    //    Rows come in batches of 8 from buffer loads over the bucket's rows:
     //    a row index past the pixel's count reads 0 through an out-of-range
     //    offset, so no load sits in a branch, the compiler's load counting
     //    stays exact, and the next batch is in flight while one is summed
@@ -1235,8 +1257,7 @@ __global__ __launch_bounds__(512) void dcn2_gi_gather_kernel(const BwdParams p) 
     constexpr int EPL = 16 / sizeof(T);  // channels per lane per row
     constexpr int LPR = KC / EPL;        // lanes per row (8)
     constexpr int PPW = 64 / LPR;        // pixels per wave pass (8)
-    constexpr int UNR = 4;
-    static_assert(LPR == 8, "a 16-byte lane slice of a KC-channel row");
+    static_assert(LPR == 8, "a 16-byte lane slice of a KC-channel row; 8-lane swizzle groups");
     typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
     const int co = lane % LPR, ps = lane / LPR;
     const int row_bytes = p.Cgp * (int)sizeof(T);
@@ -1266,64 +1287,91 @@ __global__ __launch_bounds__(512) void dcn2_gi_gather_kernel(const BwdParams p) 
             float sum[EPL];
 #pragma unroll
             for (int e = 0; e < EPL; ++e) sum[e] = 0.0f;
-            // batch j0..j0+UNR-1 of this pixel's rows -> raw, wgt
-            auto fetch = [&](int j0, u32x4 (&raw)[UNR], float (&wgt)[UNR]) __attribute__((always_inline)) {
-#pragma unroll
-                for (int u = 0; u < UNR; ++u) {
-                    // selects only (no branch): record position of row j in the
-                    // corner-ordered ranges, its weight, and its row offset
-                    // (OR-ed out of range past the pixel's count)
-                    const int j = j0 + u;
-                    const bool ok = j < tot, q1 = j >= e1, q2 = j >= e2, q3 = j >= e3;
-                    int pos = beg[0] + j;
-                    pos = q1 ? beg[1] + j - e1 : pos;
-                    pos = q2 ? beg[2] + j - e2 : pos;
-                    pos = q3 ? beg[3] + j - e3 : pos;
-                    pos = ok ? pos : 0;
-                    const float2 f = sfrac[pos];
-                    const int off = (int)sslot[pos] * row_bytes + slice;
-                    const float wy = q2 ? f.x : 1.0f - f.x;             // corners 10, 11
-                    const float wx = (q1 != q2) || q3 ? f.y : 1.0f - f.y;  // corners 01, 11
-                    wgt[u] = ok ? wy * wx : 0.0f;
-                    raw[u] = __builtin_amdgcn_raw_buffer_load_b128(
-                        rrs, off | (ok ? 0 : kGatherOutOfRange), 0, 0);
-                }
+            // Row j of the pixel's corner-ordered record ranges: its record
+            // position, weight and row offset (out of range past the pixel's
+            // count), by selects only.  Lane co of the pixel's 8-lane group
+            // works out row jb + co of a batch of LPR rows; the batch's loads
+            // take each row's offset and weight from its lane (ds_swizzle in
+            // bit mode: lane (l & 0x18) | u of every 32-lane half), so the
+            // index arithmetic is done once per row instead of once per lane.
+            auto row_info = [&](int jb, int &off, float &w) __attribute__((always_inline)) {
+                const int j = jb + co;
+                const bool ok = j < tot, q1 = j >= e1, q2 = j >= e2, q3 = j >= e3;
+                int pos = beg[0] + j;
+                pos = q1 ? beg[1] + j - e1 : pos;
+                pos = q2 ? beg[2] + j - e2 : pos;
+                pos = q3 ? beg[3] + j - e3 : pos;
+                pos = ok ? pos : 0;
+                const float2 f = sfrac[pos];
+                const float wy = q2 ? f.x : 1.0f - f.x;             // corners 10, 11
+                const float wx = (q1 != q2) || q3 ? f.y : 1.0f - f.y;  // corners 01, 11
+                w = ok ? wy * wx : 0.0f;
+                off = ok ? (int)sslot[pos] * row_bytes : kGatherOutOfRange;
             };
-            auto accumulate = [&](const u32x4 (&raw)[UNR], const float (&wgt)[UNR]) __attribute__((always_inline)) {
+            auto fetch = [&](int off, float w, u32x4 (&raw)[LPR], float (&wgt)[LPR]) __attribute__((always_inline)) {
+                static_for<0, LPR>([&](auto uc) __attribute__((always_inline)) {
+                    constexpr int u = decltype(uc)::value;
+                    const int ou = __builtin_amdgcn_ds_swizzle(off, (u << 5) | 0x18);
+                    wgt[u] = __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(w), (u << 5) | 0x18));
+                    // row_bytes is a multiple of 128 and the marker has the low
+                    // bits set, so OR-ing the slice in keeps either in range
+                    raw[u] = __builtin_amdgcn_raw_buffer_load_b128(rrs, ou | slice, 0, 0);
+                });
+            };
+            auto accumulate = [&](const u32x4 (&raw)[LPR], const float (&wgt)[LPR]) __attribute__((always_inline)) {
 #pragma unroll
-                for (int u = 0; u < UNR; ++u) {
+                for (int u = 0; u < LPR; ++u) {
                     float v[EPL];
                     Unpack<T>::run(make_uint4(raw[u].x, raw[u].y, raw[u].z, raw[u].w), v);
 #pragma unroll
                     for (int e = 0; e < EPL; ++e) sum[e] = fmaf(wgt[u], v[e], sum[e]);
                 }
             };
-            u32x4 ra[UNR], rb[UNR];
-            float wa[UNR], wb[UNR];
+            u32x4 ra[LPR], rb[LPR];
+            float wa[LPR], wb[LPR];
+            int oa, ob;
+            float xa, xb;
             // (scheduling barriers keep each batch's loads ahead of the sums of
             // the previous one; left alone the scheduler groups the fetches)
-            fetch(0, ra, wa);
-            for (int j0 = 0; j0 < tot; j0 += 2 * UNR) {
-                fetch(j0 + UNR, rb, wb);
+            row_info(0, oa, xa);
+            fetch(oa, xa, ra, wa);
+            for (int j0 = 0; j0 < tot; j0 += 2 * LPR) {
+                row_info(j0 + LPR, ob, xb);
+                fetch(ob, xb, rb, wb);
                 __builtin_amdgcn_sched_barrier(0);
                 accumulate(ra, wa);
                 __builtin_amdgcn_sched_barrier(0);
-                fetch(j0 + 2 * UNR, ra, wa);
+                row_info(j0 + 2 * LPR, oa, xa);
+                fetch(oa, xa, ra, wa);
                 __builtin_amdgcn_sched_barrier(0);
                 accumulate(rb, wb);
                 __builtin_amdgcn_sched_barrier(0);
             }
-            if (tot == 0) continue;
-            float *dst = gi + ((size_t)Y * p.W + X) * cs + cc * KC + co * EPL;
-            const int cvalid = min(EPL, p.Cg - (cc * KC + co * EPL));
+            // Interior pixels (reachable from this tile's cells only) are this
+            // block's alone: a plain read-modify-write.  The accumulator's
+            // padding channels (Cg..Cgp of a group) are never read back (and
+            // receive zeros), so whole 16-byte pieces are updated (a guarded
+            // update per channel made every channel a separate round trip).
             if (py >= 1 && py <= TS - 1 && px >= 1 && px <= TS - 1) {
+                if (tot == 0) continue;
+                f32x4 *d4 = reinterpret_cast<f32x4 *>(gi + ((size_t)Y * p.W + X) * cs + cc * KC + co * EPL);
+                f32x4 acc4[EPL / 4];
 #pragma unroll
-                for (int e = 0; e < EPL; ++e)
-                    if (e < cvalid) dst[e] += sum[e];
-            } else {
+                for (int i = 0; i < EPL / 4; ++i) acc4[i] = d4[i];
 #pragma unroll
-                for (int e = 0; e < EPL; ++e)
-                    if (e < cvalid && sum[e] != 0.0f) unsafeAtomicAdd(dst + e, sum[e]);
+                for (int i = 0; i < EPL / 4; ++i) {
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) acc4[i][k] += sum[4 * i + k];
+                    d4[i] = acc4[i];
+                }
+            } else if (pl < TW * TW) {
+                // border ring: written in full every call (zeros included) and
+                // added by finalize_gi_kernel, no atomics
+                f32x4 *r4 = reinterpret_cast<f32x4 *>(
+                    p.ring + ((size_t)bucket * kRing + ring_index(py, px)) * p.Cgp + cc * KC + co * EPL);
+#pragma unroll
+                for (int i = 0; i < EPL / 4; ++i)
+                    r4[i] = f32x4{sum[4 * i], sum[4 * i + 1], sum[4 * i + 2], sum[4 * i + 3]};
             }
         }
     }
@@ -1333,6 +1381,54 @@ __global__ __launch_bounds__(512) void dcn2_gi_gather_kernel(const BwdParams p) 
 __global__ __launch_bounds__(256) void fill_zero_kernel(float4 *__restrict__ p, size_t n4) {
     for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (size_t)gridDim.x * 256)
         p[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+}
+
+// Adds the gather's border-ring partials into gi_acc.  The tile-boundary
+// pixels are those with (Y+1) % TS == 0 or (X+1) % TS == 0: the whole rows
+// Y = TS*k + TS-1 (nrow of them) first, then the columns X = TS*k + TS-1
+// (ncol) without those rows.  Pixel (Y, X) is (py, px) = ((Y+1) % TS,
+// (X+1) % TS) of the window of tile ((Y+1) / TS, (X+1) / TS), and also row TS
+// of the tile above when py == 0 and column TS of the tile to the left when
+// px == 0; it is on the ring of each of those windows.  One thread per pixel
+// and 4 padded channels; every pixel has exactly one thread, so the update is
+// a plain read-modify-write.
+__global__ __launch_bounds__(256) void ring_merge_kernel(float *__restrict__ gi_acc,
+                                                         const float *__restrict__ ring, int H,
+                                                         int W, int cs, int Cgp, int G, int nty,
+                                                         int ntx, int nrow, int ncol) {
+    constexpr int TS = kCellTile;
+    const int q4 = cs / 4, b = blockIdx.y;
+    const long npix = (long)nrow * W + (long)(H - nrow) * ncol;
+    const long item = (long)blockIdx.x * 256 + threadIdx.x;
+    if (item >= npix * q4) return;
+    const long k = item / q4;
+    const int cp = (int)(item - k * q4) * 4;
+    int Y, X;
+    if (k < (long)nrow * W) {
+        Y = TS * (int)(k / W) + TS - 1;
+        X = (int)(k % W);
+    } else {
+        const long k2 = k - (long)nrow * W;
+        const int c = (int)(k2 / (H - nrow)), j = (int)(k2 % (H - nrow));
+        Y = j + j / (TS - 1);  // the j-th row that is not a boundary row
+        X = TS * c + TS - 1;
+    }
+    const int g = cp / Cgp, ci = cp - g * Cgp;
+    const int py = (Y + 1) % TS, ty = (Y + 1) / TS, px = (X + 1) % TS, tx = (X + 1) / TS;
+    f32x4 *dst = reinterpret_cast<f32x4 *>(gi_acc + (((size_t)b * H + Y) * W + X) * cs + cp);
+    f32x4 v = *dst;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        if (i == 1 && (py != 0 || ty == 0)) continue;
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) {
+            if (jj == 1 && (px != 0 || tx == 0)) continue;
+            const long bucket = (((long)b * G + g) * nty + (ty - i)) * ntx + (tx - jj);
+            v += *reinterpret_cast<const f32x4 *>(
+                ring + (bucket * kRing + ring_index(i ? TS : py, jj ? TS : px)) * Cgp + ci);
+        }
+    }
+    *dst = v;
 }
 
 // gi_acc [B][HW][cs] fp32 -> grad_input [B][C][HW] T; 64 pixels x 32 padded
@@ -1453,6 +1549,15 @@ static hipError_t backward_t(const Geo &g, const BwdParams &p0, void *grad_input
                 lds_cu = 0;
             const int pad = std::max(0, lds_cu / 3 + 256 - kGatherStaticLds);
             dcn2_gi_gather_kernel<T><<<g.B * g.G * p.nty * p.ntx, 512, pad, s>>>(p);
+            if ((e = hipGetLastError()) != hipSuccess) return e;
+            // the windows' border rings into gi_acc (tile-boundary pixels only)
+            const int nrow = g.H / kCellTile, ncol = g.W / kCellTile;
+            const long items = ((long)nrow * g.W + (long)(g.H - nrow) * ncol) * (g.cs / 4);
+            if (items > 0) {
+                dim3 rgrid((unsigned)((items + 255) / 256), g.B);
+                ring_merge_kernel<<<rgrid, 256, 0, s>>>(p.gi_acc, p.ring, g.H, g.W, g.cs, g.Cgp, g.G,
+                                                        p.nty, p.ntx, nrow, ncol);
+            }
         }
         if ((e = hipGetLastError()) != hipSuccess) return e;
         prof_end(DCN2_STAGE_BWD_GATHER, s);
@@ -1536,7 +1641,7 @@ hipError_t launch_backward(const Geo &g, const void *xt, const void *wt, const v
                            const void *mask, const void *grad_out, void *grad_input,
                            void *grad_offset, void *grad_mask, void *grad_weight, void *grad_bias,
                            float *gi_acc, float *gw_acc, float *gb_acc, void *cgm, void *rec,
-                           int *cnt, int *sidx, hipStream_t s) {
+                           int *cnt, int *sidx, float *ring, hipStream_t s) {
     BwdParams p;
     p.xt = xt;
     p.wt = wt;
@@ -1582,6 +1687,7 @@ hipError_t launch_backward(const Geo &g, const void *xt, const void *wt, const v
     p.ntx = gg.ntx;
     p.nty = gg.nty;
     p.cap = gg.cap;
+    p.ring = ring;
     switch (g.dtype) {
     case DCN2_F16: return backward_t<f16>(g, p, grad_input, grad_weight, grad_bias, s);
     case DCN2_BF16: return backward_t<bf16>(g, p, grad_input, grad_weight, grad_bias, s);

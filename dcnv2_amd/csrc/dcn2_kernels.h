@@ -36,8 +36,10 @@ struct FwdWorkspace {
 FwdWorkspace fwd_workspace(const Geo &g);
 
 struct BwdWorkspace {
-    size_t xt, wt, tab, gi_acc, gw_acc, gb_acc, cgm, rec, cnt, sidx, total;
+    size_t xt, wt, tab, gi_acc, gw_acc, gb_acc, cgm, rec, cnt, sidx, ring, total;
 };
+// Border-ring pixels of one grad_input gather window (4 x the cell tile side).
+constexpr int kGatherRing = 64;
 BwdWorkspace bwd_workspace(const Geo &g);
 
 // Bucket geometry of the grad_input gather (dcn2_backward.hip).
@@ -63,6 +65,6 @@ hipError_t launch_backward(const Geo &g, const void *xt, const void *wt, const v
                            const void *mask, const void *grad_out, void *grad_input,
                            void *grad_offset, void *grad_mask, void *grad_weight, void *grad_bias,
                            float *gi_acc, float *gw_acc, float *gb_acc, void *cgm, void *rec,
-                           int *cnt, int *sidx, hipStream_t s);
+                           int *cnt, int *sidx, float *ring, hipStream_t s);
 
 }  // namespace dcn2

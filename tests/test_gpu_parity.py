@@ -9,8 +9,9 @@ fp16/bf16 and <= 1e-4 for fp32, for the output and all five gradients.
   image against the CPU oracle, forward+backward of one image against the
   oracle in the config dtype and in an fp32 rerun, and the whole batch against
   the independent grid_sample formulation evaluated in fp32 on the GPU;
-* edge cases: mask/bias None, Cout > 256 (two M tiles), every sample outside
-  the image, non-contiguous inputs, an empty batch.
+* edge cases: mask/bias None, Cout > 256 (two M tiles), grad_input across the
+  gather's cell-tile boundaries, every sample outside the image, non-contiguous
+  inputs, an empty batch.
 """
 from __future__ import annotations
 
@@ -181,6 +182,20 @@ def test_cout_beyond_one_tile(dtype):
     grads = gpu_backward(t, w.geometry())
     torch.cuda.synchronize()
     check("output", out, oracle_forward(t, w.geometry()), TOL[dtype])
+    for name, g, r in zip(GRADS, grads, oracle_backward(t, w.geometry())):
+        check(name, g, r, TOL[dtype])
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+def test_grad_input_tile_boundaries(dtype):
+    """grad_input where the gather's 16x16 cell tiles meet: images of 37x45
+    (not multiples of 16, so the last tiles are partial) and two deformable
+    groups.  The pixels of rows and columns 15 and 31 are shared by two or four
+    tiles' windows, whose partial sums are merged after the gather; offsets of
+    +-3 pixels spread every tile's samples over its neighbours' cells."""
+    w, t = _small(dtype, B=2, C=24, H=37, W=45, Cout=20, G=2, osc=3.0)
+    grads = gpu_backward(t, w.geometry())
+    torch.cuda.synchronize()
     for name, g, r in zip(GRADS, grads, oracle_backward(t, w.geometry())):
         check(name, g, r, TOL[dtype])
 
