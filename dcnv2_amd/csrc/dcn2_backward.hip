@@ -440,14 +440,35 @@ __global__ __launch_bounds__(512) void dcn2_colgrad_kernel(const BwdParams p) {
         }
     };
 
+    // Chunk c = (tap*G + g)*cpg + cc, tap = ki*kw + kj.  The steps walk the
+    // chunks in order, so the ids are advanced with compares instead of being
+    // divided out of c (runtime divisors expand to long scalar sequences, and
+    // the scalar unit is shared by the CU's waves).
+    struct ChunkId {
+        int cc, g, tap, ki, kj;
+    };
+    auto chunk_next = [&](ChunkId r) __attribute__((always_inline)) {
+        if (++r.cc == cpg) {
+            r.cc = 0;
+            if (++r.g == p.G) {
+                r.g = 0;
+                ++r.tap;
+                if (++r.kj == p.kw) {
+                    r.kj = 0;
+                    ++r.ki;
+                }
+            }
+        }
+        return r;
+    };
+
     // Offsets, mask and bucket row of (pr, chunk), loaded two steps ahead.
     struct OM {
         T dy, dx, m;
         int sx;
     };
-    auto load_om = [&](int c, OM &o) __attribute__((always_inline)) {
-        const int tg = c / cpg, tap = tg / p.G, g = tg - tap * p.G;
-        const int plane = g * KK + tap;
+    auto load_om = [&](const ChunkId &id, OM &o) __attribute__((always_inline)) {
+        const int plane = id.g * KK + id.tap;
         const int nn = live ? nr : 0;
         const size_t ob = (size_t)plane * 2 * N + nn;
         o.dy = offs[ob];
@@ -455,18 +476,6 @@ __global__ __launch_bounds__(512) void dcn2_colgrad_kernel(const BwdParams p) {
         o.m = msk ? msk[(size_t)plane * N + nn] : (T)1.0f;
         o.sx = sidx[(size_t)plane * N + nn];
     };
-    struct ChunkId {
-        int cc, tap, g;
-    };
-    auto chunk_id = [&](int c) __attribute__((always_inline)) {
-        ChunkId r;
-        const int tg = c / cpg;
-        r.cc = c - tg * cpg;
-        r.tap = tg / p.G;
-        r.g = tg - r.tap * p.G;
-        return r;
-    };
-
     // This thread's corner gathers of the chunk sampled last.
     uint4 raw[4][2];
     // this lane's 16 bytes of dcn2_trash
@@ -476,9 +485,8 @@ __global__ __launch_bounds__(512) void dcn2_colgrad_kernel(const BwdParams p) {
 
     // Sampling of chunk c (offsets o): corner gathers, and the descriptor of
     // pixel pr into sD[X].
-    auto sample = [&](int X, int c, const OM &o) __attribute__((always_inline)) {
-        const ChunkId id = chunk_id(c);
-        const int ki = id.tap / p.kw, kj = id.tap - ki * p.kw;
+    auto sample = [&](int X, const ChunkId &id, const OM &o) __attribute__((always_inline)) {
+        const int ki = id.ki, kj = id.kj;
         SamplePos sp;
         float mv = 0.0f;
         if (live) {
@@ -564,8 +572,7 @@ __global__ __launch_bounds__(512) void dcn2_colgrad_kernel(const BwdParams p) {
     // lane's channels.  The shuffles leave the sums in all QPP lanes of the
     // pixel, which all store the same values at the last chunk of its (tap,
     // group) (the lanes of a dead pixel store to dcn2_trash).
-    auto reduce_corners = [&](int X, int c) __attribute__((always_inline)) {
-        const ChunkId id = chunk_id(c);
+    auto reduce_corners = [&](int X, const ChunkId &id) __attribute__((always_inline)) {
         float cgv[CPL];
 #pragma unroll
         for (int c4 = 0; c4 < CPL / 4; ++c4) {
@@ -622,8 +629,7 @@ __global__ __launch_bounds__(512) void dcn2_colgrad_kernel(const BwdParams p) {
     // column-gradient row (8 rows of 16-byte pieces per wave instruction) for
     // the gather kernel; a sample of a full bucket adds to grad_input here
     // with fp32 atomics (the one conditional memory operation of the step).
-    auto handoff = [&](int X, int c) __attribute__((always_inline)) {
-        const ChunkId id = chunk_id(c);
+    auto handoff = [&](int X, const ChunkId &id) __attribute__((always_inline)) {
         constexpr int EPL = 16 / sizeof(T), LPP = KC / EPL, PPI = 64 / LPP;
         static_assert(LPP == 8, "8 lanes cover one chunk row");
         const int co = lane % LPP, r = lane / LPP;
@@ -672,10 +678,14 @@ __global__ __launch_bounds__(512) void dcn2_colgrad_kernel(const BwdParams p) {
         if (go_stage) go_stage_issue();
         else load_go(0);
     }
-    load_om(0, om_c);
+    // ids of chunks c, c+1 and min(c+2, last) of the step
+    ChunkId id0 = {0, 0, 0, 0, 0};
+    ChunkId id1 = last >= 1 ? chunk_next(id0) : id0;
+    ChunkId id2 = last >= 2 ? chunk_next(id1) : id1;
+    load_om(id0, om_c);
     a_prefetch(0);
-    load_om(min(1, last), om_n);
-    sample(0, 0, om_c);
+    load_om(id1, om_n);
+    sample(0, id0, om_c);
     if (go_stage) go_stage_store();
     a_commit(0);
     a_prefetch(min(1, last));
@@ -691,18 +701,21 @@ __global__ __launch_bounds__(512) void dcn2_colgrad_kernel(const BwdParams p) {
 
     for (int c = 0; c < last; ++c) {
         const int X = c & 1, Y = X ^ 1;
-        reduce_corners(X, c);
+        reduce_corners(X, id0);
         a_prefetch(min(c + 2, last));
-        load_om(min(c + 2, last), om_n);
-        sample(Y, c + 1, om_c);
+        load_om(id2, om_n);
+        sample(Y, id1, om_c);
         colgrad(Y, c + 1);
-        handoff(X, c);
+        handoff(X, id0);
         a_commit(X);  // chunk c+2 has chunk c's parity, and MFMA(c) is done
         om_c = om_n;
+        id0 = id1;
+        id1 = id2;
+        if (c + 3 <= last) id2 = chunk_next(id2);
         __syncthreads();
     }
-    reduce_corners(last & 1, last);
-    handoff(last & 1, last);
+    reduce_corners(last & 1, id0);
+    handoff(last & 1, id0);
 }
 
 // ---------------------------------------------------------------------------
