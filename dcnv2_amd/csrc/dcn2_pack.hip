@@ -35,7 +35,10 @@ template <typename T>
 __device__ __forceinline__ void pack_input_block(const PackParams &p, int blk) {
     constexpr int E = 16 / sizeof(T);     // elements per 16-byte vector
     constexpr int CT = 128 / sizeof(T);   // channels per block (128 bytes of a pixel)
-    constexpr int LDP = 64 + E;           // LDS pitch (elements) of one channel row
+    // LDS tile [channel][pixel], the 16-byte blocks of channel row c XOR-permuted
+    // by (c / E) % 8: the transposed reads (the E channels of one pixel, for 8
+    // consecutive channel blocks across lanes) then hit 8 distinct banks.
+    constexpr int LDP = 64;               // LDS pitch (elements) of one channel row
     __shared__ __attribute__((aligned(16))) T tile[CT][LDP];
     const T *__restrict__ in = (const T *)p.in;
     T *__restrict__ xt = (T *)p.xt;
@@ -55,11 +58,11 @@ __device__ __forceinline__ void pack_input_block(const PackParams &p, int blk) {
         if (p.in_vec) {
             uint4 v = make_uint4(0, 0, 0, 0);
             if (live && px0 + po < p.HW) v = *reinterpret_cast<const uint4 *>(src);
-            *reinterpret_cast<uint4 *>(&tile[cl][po]) = v;
+            *reinterpret_cast<uint4 *>(&tile[cl][((po / E) ^ ((cl / E) & 7)) * E]) = v;
         } else {
 #pragma unroll
             for (int e = 0; e < E; ++e)
-                tile[cl][po + e] = (live && px0 + po + e < p.HW) ? src[e] : (T)0.0f;
+                tile[cl][((po / E) ^ ((cl / E) & 7)) * E + e] = (live && px0 + po + e < p.HW) ? src[e] : (T)0.0f;
         }
     }
     __syncthreads();
@@ -72,7 +75,7 @@ __device__ __forceinline__ void pack_input_block(const PackParams &p, int blk) {
         if (px0 + pl >= p.HW) continue;
         T v[E];
 #pragma unroll
-        for (int e = 0; e < E; ++e) v[e] = tile[cg + e][pl];
+        for (int e = 0; e < E; ++e) v[e] = tile[cg + e][((pl / E) ^ (((cg + e) / E) & 7)) * E + pl % E];
         *reinterpret_cast<uint4 *>(xt + ((size_t)b * p.HW + px0 + pl) * p.cs + cp0 + cg) =
             __builtin_bit_cast(uint4, v);
     }
