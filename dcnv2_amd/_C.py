@@ -12,7 +12,8 @@ the current stream; all arithmetic runs in the gfx950 kernels of the library.
 Extensions over the reference, all trailing and optional: ``dilation_h``,
 ``dilation_w`` and ``deformable_groups`` (the reference's Python module accepts
 them but never forwards them, ``dcn_v2_mm.py:67-68, 94-102``); fp16/bf16 as
-well as fp32 tensors; ``mask`` and ``bias`` may be ``None``.
+well as fp32 tensors; ``mask`` and ``bias`` may be ``None``; a weight of shape
+``[Cout, C/groups, kh, kw]`` selects torchvision's weight groups.
 
 Errors: any invalid device, dtype, shape or launch failure raises
 ``RuntimeError``, as the reference's ``AT_ASSERTM`` checks do
@@ -38,7 +39,7 @@ class Desc(ctypes.Structure):
     _fields_ = [(name, ctypes.c_int32) for name in (
         "batch", "in_channels", "height", "width", "out_channels", "kernel_h", "kernel_w",
         "stride_h", "stride_w", "pad_h", "pad_w", "dilation_h", "dilation_w",
-        "deformable_groups", "dtype")]
+        "deformable_groups", "dtype", "weight_groups")]
 
 
 def library_path() -> str:
@@ -97,9 +98,11 @@ def _ptr(t):
 def make_desc(input, weight, stride_h, stride_w, pad_h, pad_w, dilation_h, dilation_w,
               deformable_groups) -> Desc:
     B, C, H, W = (int(v) for v in input.shape)
-    Cout, _, kh, kw = (int(v) for v in weight.shape)
+    Cout, Cw, kh, kw = (int(v) for v in weight.shape)
+    # weight groups follow from weight.shape[1], as in torchvision's deform_conv2d
     return Desc(B, C, H, W, Cout, kh, kw, int(stride_h), int(stride_w), int(pad_h), int(pad_w),
-                int(dilation_h), int(dilation_w), int(deformable_groups), _DTYPES[input.dtype])
+                int(dilation_h), int(dilation_w), int(deformable_groups), _DTYPES[input.dtype],
+                C // Cw)
 
 
 def _validate(name, input, weight, mask, offset, bias, extra=()):
@@ -125,9 +128,12 @@ def _validate(name, input, weight, mask, offset, bias, extra=()):
                            "(float32, float16 and bfloat16 are supported)")
     if input.dim() != 4 or weight.dim() != 4 or offset.dim() != 4:
         raise RuntimeError(f"{name}: input, weight and offset must be 4-D")
-    if weight.shape[1] != input.shape[1]:  # reference com.cu:760-761
-        raise RuntimeError(f"{name}: input has {input.shape[1]} channels, "
-                           f"weight expects {weight.shape[1]}")
+    # reference com.cu:760-761 requires weight.shape[1] == C; torchvision's weight
+    # groups (C / weight.shape[1] of them) must also split Cout evenly
+    C, Cw, Cout = int(input.shape[1]), int(weight.shape[1]), int(weight.shape[0])
+    if Cw <= 0 or C % Cw != 0 or Cout % (C // Cw) != 0:
+        raise RuntimeError(f"{name}: input has {C} channels, weight expects {Cw} per group "
+                           f"with {Cout} output channels")
     if bias is not None and tuple(bias.shape) != (weight.shape[0],):
         raise RuntimeError(f"{name}: bias shape {tuple(bias.shape)} != ({weight.shape[0]},)")
 

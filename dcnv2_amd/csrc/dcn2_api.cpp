@@ -50,6 +50,7 @@ static int make_geo(const dcn2_desc *d, Geo &g) {
     g.dw = d->dilation_w;
     g.G = d->deformable_groups;
     g.dtype = d->dtype;
+    g.WG = d->weight_groups == 0 ? 1 : d->weight_groups;
     if (g.dtype != DCN2_F32 && g.dtype != DCN2_F16 && g.dtype != DCN2_BF16)
         return fail(DCN2_EINVAL, "dcn2: unsupported dtype code %d", g.dtype);
     if (g.B < 0 || g.C <= 0 || g.H <= 0 || g.W <= 0 || g.Cout <= 0)
@@ -63,6 +64,11 @@ static int make_geo(const dcn2_desc *d, Geo &g) {
     if (g.G <= 0 || g.C % g.G != 0)
         return fail(DCN2_EINVAL, "dcn2: in_channels %d not divisible by deformable_groups %d",
                     g.C, g.G);
+    if (g.WG <= 0 || g.C % g.WG != 0 || g.Cout % g.WG != 0)
+        return fail(DCN2_EINVAL,
+                    "dcn2: in_channels %d and out_channels %d not divisible by weight_groups %d",
+                    g.C, g.Cout, g.WG);
+    g.Cw = g.C / g.WG;
     g.Ho = (g.H + 2 * g.ph - (g.dh * (g.kh - 1) + 1)) / g.sh + 1;
     g.Wo = (g.W + 2 * g.pw - (g.dw * (g.kw - 1) + 1)) / g.sw + 1;
     if (g.H + 2 * g.ph < g.dh * (g.kh - 1) + 1 || g.W + 2 * g.pw < g.dw * (g.kw - 1) + 1 ||
@@ -297,6 +303,6 @@ int dcn2_backward_om(const dcn2_desc *d, const void *input, const void *weight, 
 
 const char *dcn2_last_error(void) { return g_last_error.c_str(); }
 
-const char *dcn2_version(void) { return "dcnv2_amd 1 gfx950"; }
+const char *dcn2_version(void) { return "dcnv2_amd 2 gfx950"; }
 
 }  // extern "C"

@@ -1476,14 +1476,17 @@ template <typename T>
 __global__ __launch_bounds__(256) void finalize_gw_kernel(const float *__restrict__ gwa,
                                                           const float *__restrict__ gba,
                                                           T *__restrict__ gw, T *__restrict__ gb,
-                                                          int Cout, int C, int KK, int Cg,
-                                                          int Cgp, int G, int Kp) {
+                                                          int Cout, int Cw, int mpg, int KK,
+                                                          int Cg, int Cgp, int G, int Kp) {
+    // grad_weight [Cout][Cw][KK]: row m's channel cl is input channel
+    // (m / mpg) * Cw + cl, the diagonal block of the block-diagonal W'.
     const long idx = (long)blockIdx.x * 256 + threadIdx.x;
-    const long total = (long)Cout * C * KK;
+    const long total = (long)Cout * Cw * KK;
     if (idx < total) {
-        const int m = (int)(idx / ((long)C * KK));
-        const int r = (int)(idx - (long)m * C * KK);
-        const int c = r / KK, tap = r - c * KK;
+        const int m = (int)(idx / ((long)Cw * KK));
+        const int r = (int)(idx - (long)m * Cw * KK);
+        const int cl = r / KK, tap = r - cl * KK;
+        const int c = (m / mpg) * Cw + cl;
         const int g = c / Cg, ci = c - g * Cg;
         gw[idx] = (T)gwa[(size_t)m * Kp + ((size_t)tap * G + g) * Cgp + ci];
     }
@@ -1626,10 +1629,10 @@ static hipError_t backward_t(const Geo &g, const BwdParams &p0, void *grad_input
     // 5. grad_weight / grad_bias to the caller's layout
     prof_begin(DCN2_STAGE_BWD_FINAL, s);
     {
-        const long total = std::max<long>((long)g.Cout * g.C * g.KK, g.Cout);
+        const long total = std::max<long>((long)g.Cout * g.Cw * g.KK, g.Cout);
         finalize_gw_kernel<T><<<(unsigned)((total + 255) / 256), 256, 0, s>>>(
-            p.gw_acc, p.gb_acc, (T *)grad_weight, (T *)grad_bias, g.Cout, g.C, g.KK, g.Cg, g.Cgp,
-            g.G, g.Kp);
+            p.gw_acc, p.gb_acc, (T *)grad_weight, (T *)grad_bias, g.Cout, g.Cw, g.Cout / g.WG,
+            g.KK, g.Cg, g.Cgp, g.G, g.Kp);
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }
     prof_end(DCN2_STAGE_BWD_FINAL, s);

@@ -14,6 +14,7 @@ struct Geo {
     int dtype;      // enum dcn2_dtype
     int esz;        // element size in bytes
     int Cg;         // channels per deformable group
+    int WG, Cw;     // weight groups and input channels per weight group (C / WG)
     int KC;         // channel chunk of one LDS stage (64 for f16/bf16, 32 for f32)
     int Cgp;        // Cg rounded up to KC
     int cs;         // channels-last pixel stride of xt: G*Cgp

@@ -4,9 +4,11 @@
 //         channels, so a bilinear corner is one contiguous channel vector
 //         (16-byte loads) instead of C scattered scalars.  The reference
 //         samples NCHW directly, one scalar per thread (com.cu:151-195).
-// weight: [Cout][C][kh][kw] -> MFMA fragment order of W' [Mp][Kp] (or of its
-//         transpose) with K ordered (tap, group, channel) and zero padding,
-//         plus the chunk table.
+// weight: [Cout][C/WG][kh][kw] -> MFMA fragment order of W' [Mp][Kp] (or of
+//         its transpose) with K ordered (tap, group, channel) and zero padding,
+//         plus the chunk table.  With WG weight groups W' is block diagonal:
+//         row m holds its group's C/WG channels and zeros for all others, so
+//         the GEMMs need no notion of groups.
 //
 // Blocks [0, nin) transpose 64 pixels x CT channels of the input each (CT*esz
 // = 128 bytes, one channel chunk of a pixel); blocks [nin, nin + nw) pack 256
@@ -26,6 +28,7 @@ struct PackParams {
     int pxt, cht, nin;             // pixel tiles, channel tiles per image, input blocks
     int in_vec;                    // HW % E == 0 and 16-byte aligned input: vector loads
     int Cout, KK, kw, dh, dw, G;   // weight geometry
+    int Cw, mpg;                   // channels and output channels per weight group
     int kc, kstep, kpl, Mp, Kp;    // MFMA packing
     int transpose;                 // 0: forward A fragments, 1: backward W'^T fragments
 };
@@ -135,7 +138,10 @@ __device__ __forceinline__ void pack_weight_block(const PackParams &p, int blk) 
     const int tap = k / gc, r = k - tap * gc;
     const int g = r / p.Cgp, c = r - g * p.Cgp;
     T v = (T)0.0f;
-    if (m < p.Cout && c < p.Cg) v = w[((size_t)m * p.C + g * p.Cg + c) * p.KK + tap];
+    // input channel g*Cg + c, as channel cl of row m's weight group
+    const int cl = g * p.Cg + c - (m / p.mpg) * p.Cw;
+    if (m < p.Cout && c < p.Cg && (unsigned)cl < (unsigned)p.Cw)
+        v = w[((size_t)m * p.Cw + cl) * p.KK + tap];
     dst[idx] = v;
 }
 
@@ -174,6 +180,8 @@ static hipError_t pack_t(const Geo &g, const void *input, void *xt, const void *
     p.dh = g.dh;
     p.dw = g.dw;
     p.G = g.G;
+    p.Cw = g.Cw;
+    p.mpg = g.Cout / g.WG;
     p.kc = g.KC;
     p.kstep = g.dtype == DCN2_F32 ? 2 : 16;
     p.kpl = g.dtype == DCN2_F32 ? 1 : 8;

@@ -23,7 +23,10 @@ Differences from the reference, by design:
   ``2*G*kh*kw`` channels and apply ``sigmoid`` to the rest while loading, and
   the backward returns the gradient of that tensor, so the ``chunk`` / ``cat`` /
   ``sigmoid`` passes (``:133-137``) and their backward are not materialised.
-  ``DCN(..., fused_offset_mask=False)`` keeps the reference's separate steps.
+  ``DCN(..., fused_offset_mask=False)`` keeps the reference's separate steps;
+* a trailing ``groups=1`` on ``DCNv2`` / ``DCN`` gives torchvision's weight
+  groups (weight ``[Cout, C/groups, kh, kw]``); the operator infers them from
+  the weight's shape, as ``torchvision.ops.deform_conv2d`` does.
 """
 from __future__ import annotations
 
@@ -102,7 +105,7 @@ dcn_v2_conv_om = _DCNv2OM.apply
 
 class DCNv2(nn.Module):
     def __init__(self, in_channels, out_channels, kernel_size, stride, padding, dilation=1,
-                 deformable_groups=1):
+                 deformable_groups=1, groups=1):
         super().__init__()
         self.in_channels = in_channels
         self.out_channels = out_channels
@@ -111,15 +114,21 @@ class DCNv2(nn.Module):
         self.padding = _pair(padding)
         self.dilation = _pair(dilation)
         self.deformable_groups = deformable_groups
+        # groups: torchvision's weight groups (DeformConv2d(groups=...)); the
+        # reference's module has none, and groups=1 is its behaviour
+        self.groups = groups
         if in_channels % deformable_groups != 0:
             raise ValueError("in_channels must be divisible by deformable_groups")
-        self.weight = nn.Parameter(torch.Tensor(out_channels, in_channels, *self.kernel_size))
+        if in_channels % groups != 0 or out_channels % groups != 0:
+            raise ValueError("in_channels and out_channels must be divisible by groups")
+        self.weight = nn.Parameter(torch.Tensor(out_channels, in_channels // groups,
+                                                *self.kernel_size))
         self.bias = nn.Parameter(torch.Tensor(out_channels))
         self.reset_parameters()
 
     def reset_parameters(self):
         # reference dcn_v2_mm.py:83-89: U(+-1/sqrt(fan_in)), zero bias
-        n = self.in_channels
+        n = self.in_channels // self.groups
         for k in self.kernel_size:
             n *= k
         stdv = 1.0 / math.sqrt(n)
@@ -136,9 +145,9 @@ class DCNv2(nn.Module):
 
 class DCN(DCNv2):
     def __init__(self, in_channels, out_channels, kernel_size, stride=1, padding=0,
-                 dilation=1, deformable_groups=1, fused_offset_mask=True):
+                 dilation=1, deformable_groups=1, fused_offset_mask=True, groups=1):
         super().__init__(in_channels, out_channels, kernel_size, stride, padding, dilation,
-                         deformable_groups)
+                         deformable_groups, groups)
         self.fused_offset_mask = fused_offset_mask
         channels_ = self.deformable_groups * 3 * self.kernel_size[0] * self.kernel_size[1]
         # The offset/mask predictor sees the same sampling grid as the DCN

@@ -11,16 +11,17 @@
  *
  * Semantics are those of torchvision.ops.deform_conv2d(input, offset, weight,
  * bias, stride, padding, dilation, mask), the comparator the reference names:
- *   output[b, m, oy, ox] = bias[m] + sum_{c, i, j} weight[m, c, i, j]
+ *   output[b, m, oy, ox] = bias[m] + sum_{c in group(m), i, j} weight[m, c - c0(m), i, j]
  *                          * mask[b, g*kh*kw + k, oy, ox]
  *                          * bilinear(input[b, c], y, x)
  *   k = i*kw + j,  g = c / (C / deformable_groups),
+ *   group(m) = [c0(m), c0(m) + C/weight_groups),  c0(m) = (m / (Cout/weight_groups)) * C/weight_groups,
  *   y = oy*stride_h - pad_h + i*dilation_h + offset[b, 2*(g*kh*kw + k),     oy, ox]
  *   x = ox*stride_w - pad_w + j*dilation_w + offset[b, 2*(g*kh*kw + k) + 1, oy, ox]
  * with bilinear() reading 0 outside the image (reference com.cu:119-148, 187).
  *
  * Tensor layouts are contiguous NCHW in the caller's dtype:
- *   input  [B, C, H, W]            weight [Cout, C, kh, kw]       bias [Cout]
+ *   input  [B, C, H, W]            weight [Cout, C/weight_groups, kh, kw]    bias [Cout]
  *   offset [B, 2*G*kh*kw, Ho, Wo]  mask   [B, G*kh*kw, Ho, Wo]    output [B, Cout, Ho, Wo]
  *   Ho = (H + 2*pad_h - (dilation_h*(kh-1) + 1)) / stride_h + 1   (likewise Wo)
  * All tensors of one call share the dtype in dcn2_desc.dtype; the GEMM
@@ -41,7 +42,7 @@
 extern "C" {
 #endif
 
-#define DCN2_ABI_VERSION 1
+#define DCN2_ABI_VERSION 2
 #define DCN2_API __attribute__((visibility("default")))
 
 enum dcn2_dtype { DCN2_F32 = 0, DCN2_F16 = 1, DCN2_BF16 = 2 };
@@ -58,13 +59,17 @@ enum dcn2_status {
  * dcn_v2_forward(input, weight, mask, offset, bias, stride_h, stride_w, pad_h,
  * pad_w) (name.h:15-24) with the shapes read off the tensors, extended by
  * dilation and deformable groups, which the reference's Python module accepts
- * but never forwards (dcn_v2_mm.py:67-68, 94-102). */
+ * but never forwards (dcn_v2_mm.py:67-68, 94-102), and by torchvision's weight
+ * groups (its deform_conv2d infers them from weight.shape[1]; the reference has
+ * none).  weight_groups 0 means 1, so a zero-initialised descriptor is
+ * ungrouped; in_channels and out_channels must both divide by it. */
 typedef struct dcn2_desc {
     int32_t batch, in_channels, height, width;
     int32_t out_channels, kernel_h, kernel_w;
     int32_t stride_h, stride_w, pad_h, pad_w, dilation_h, dilation_w;
     int32_t deformable_groups;
     int32_t dtype; /* enum dcn2_dtype */
+    int32_t weight_groups;
 } dcn2_desc;
 
 /* Output spatial size for `d`; DCN2_EINVAL if it would be empty. */

@@ -14,13 +14,15 @@
  *
  * Layouts (all NCHW, contiguous):
  *   input  [B, C, H, W]
- *   weight [Cout, C, kh, kw]
+ *   weight [Cout, C/WG, kh, kw]          WG weight groups (torchvision groups)
  *   offset [B, G*kh*kw*2, Hout, Wout]   channel (g*kh*kw + k)*2 + {0: dy, 1: dx}
  *   mask   [B, G*kh*kw, Hout, Wout]     channel  g*kh*kw + k   (may be NULL = all 1)
  *   bias   [Cout]                       (may be NULL = all 0)
  *   output [B, Cout, Hout, Wout]
  * with Hout = (H + 2*ph - (dh*(kh-1)+1)) / sh + 1 (likewise Wout), tap
- * k = i*kw + j, and input channel c belonging to offset group g = c / (C/G).
+ * k = i*kw + j, input channel c belonging to offset group g = c / (C/G), and
+ * output channel m reading only the C/WG input channels of its weight group
+ * m / (Cout/WG), as torchvision's deform_conv2d splits its GEMM per group.
  *
  * Function-by-function provenance (reference = /root/reference):
  *   bilinear()        com.cu:119-148 (dcn_bilinear_cuda) plus the in-range test
@@ -113,13 +115,14 @@ static int FN(out_size_)(int in, int k, int s, int p, int d) {
 int FN(oracle_dcn_forward)(const REAL *input, const REAL *weight, const REAL *offset,
                            const REAL *mask, const REAL *bias, int B, int C, int H, int W,
                            int Cout, int kh, int kw, int sh, int sw, int ph, int pw, int dh,
-                           int dw, int G, REAL *out, int pos_f32, int nthreads) {
+                           int dw, int G, int WG, REAL *out, int pos_f32, int nthreads) {
     if (B < 0 || C <= 0 || H <= 0 || W <= 0 || Cout <= 0 || kh <= 0 || kw <= 0 || sh <= 0 ||
-        sw <= 0 || ph < 0 || pw < 0 || dh <= 0 || dw <= 0 || G <= 0 || C % G)
+        sw <= 0 || ph < 0 || pw < 0 || dh <= 0 || dw <= 0 || G <= 0 || C % G || WG <= 0 ||
+        C % WG || Cout % WG)
         return -1;
     const int Ho = FN(out_size_)(H, kh, sh, ph, dh), Wo = FN(out_size_)(W, kw, sw, pw, dw);
     if (Ho <= 0 || Wo <= 0) return -1;
-    const int KK = kh * kw, CK = C * KK, Cg = C / G;
+    const int KK = kh * kw, CK = C * KK, Cg = C / G, CKw = (C / WG) * KK;
     const long N = (long)Ho * Wo;
 #ifdef _OPENMP
     if (nthreads > 0) omp_set_num_threads(nthreads);
@@ -152,8 +155,10 @@ int FN(oracle_dcn_forward)(const REAL *input, const REAL *weight, const REAL *of
                 REAL *o = out + (((size_t)b * Cout + m) * Ho + oy) * Wo;
                 const REAL bv = bias ? bias[m] : 0;
                 for (int ox = 0; ox < Wo; ++ox) o[ox] = bv;
-                const REAL *wr = weight + (size_t)m * CK;
-                for (int ck = 0; ck < CK; ++ck) {
+                /* weight group of m: columns [ck0, ck0 + CKw) */
+                const int ck0 = (m / (Cout / WG)) * CKw;
+                const REAL *wr = weight + (size_t)m * CKw - ck0;
+                for (int ck = ck0; ck < ck0 + CKw; ++ck) {
                     const REAL wv = wr[ck];
                     const REAL *cr = col + (size_t)ck * Wo;
                     for (int ox = 0; ox < Wo; ++ox) o[ox] += wv * cr[ox];
@@ -171,18 +176,19 @@ int FN(oracle_dcn_forward)(const REAL *input, const REAL *weight, const REAL *of
 int FN(oracle_dcn_backward)(const REAL *input, const REAL *weight, const REAL *offset,
                             const REAL *mask, const REAL *grad_out, int B, int C, int H, int W,
                             int Cout, int kh, int kw, int sh, int sw, int ph, int pw, int dh,
-                            int dw, int G, REAL *grad_input, REAL *grad_weight,
+                            int dw, int G, int WG, REAL *grad_input, REAL *grad_weight,
                             REAL *grad_bias, REAL *grad_offset, REAL *grad_mask,
                             int ref_boundary, int pos_f32, int nthreads) {
     if (B < 0 || C <= 0 || H <= 0 || W <= 0 || Cout <= 0 || kh <= 0 || kw <= 0 || sh <= 0 ||
-        sw <= 0 || ph < 0 || pw < 0 || dh <= 0 || dw <= 0 || G <= 0 || C % G)
+        sw <= 0 || ph < 0 || pw < 0 || dh <= 0 || dw <= 0 || G <= 0 || C % G || WG <= 0 ||
+        C % WG || Cout % WG)
         return -1;
     const int Ho = FN(out_size_)(H, kh, sh, ph, dh), Wo = FN(out_size_)(W, kw, sw, pw, dw);
     if (Ho <= 0 || Wo <= 0) return -1;
-    const int KK = kh * kw, CK = C * KK, Cg = C / G;
+    const int KK = kh * kw, CK = C * KK, Cg = C / G, CKw = (C / WG) * KK, mpg = Cout / WG;
     const long N = (long)Ho * Wo;
     memset(grad_input, 0, sizeof(REAL) * (size_t)B * C * H * W);
-    memset(grad_weight, 0, sizeof(REAL) * (size_t)Cout * CK);
+    memset(grad_weight, 0, sizeof(REAL) * (size_t)Cout * CKw);
     memset(grad_offset, 0, sizeof(REAL) * (size_t)B * G * KK * 2 * N);
     if (grad_mask) memset(grad_mask, 0, sizeof(REAL) * (size_t)B * G * KK * N);
     if (grad_bias) {
@@ -201,7 +207,7 @@ int FN(oracle_dcn_backward)(const REAL *input, const REAL *weight, const REAL *o
     if (nthreads > 0) omp_set_num_threads(nthreads);
     nt = omp_get_max_threads();
 #endif
-    REAL *gw_part = (REAL *)calloc((size_t)nt * Cout * CK, sizeof(REAL));
+    REAL *gw_part = (REAL *)calloc((size_t)nt * Cout * CKw, sizeof(REAL));
     if (!gw_part) return -2;
     /* one image per task: grad_input of image b is written by one thread only */
 #pragma omp parallel
@@ -210,7 +216,7 @@ int FN(oracle_dcn_backward)(const REAL *input, const REAL *weight, const REAL *o
 #ifdef _OPENMP
         tid = omp_get_thread_num();
 #endif
-        REAL *gw = gw_part + (size_t)tid * Cout * CK;
+        REAL *gw = gw_part + (size_t)tid * Cout * CKw;
         REAL *cg = (REAL *)malloc(sizeof(REAL) * (size_t)CK * Wo);  /* column gradient */
         REAL *cs = (REAL *)malloc(sizeof(REAL) * (size_t)CK * Wo);  /* re-sampled columns */
 #pragma omp for schedule(dynamic)
@@ -220,8 +226,9 @@ int FN(oracle_dcn_backward)(const REAL *input, const REAL *weight, const REAL *o
                 memset(cg, 0, sizeof(REAL) * (size_t)CK * Wo);
                 for (int m = 0; m < Cout; ++m) {
                     const REAL *go = grad_out + (((size_t)b * Cout + m) * Ho + oy) * Wo;
-                    const REAL *wr = weight + (size_t)m * CK;
-                    for (int ck = 0; ck < CK; ++ck) {
+                    const int ck0 = (m / mpg) * CKw; /* m's weight group */
+                    const REAL *wr = weight + (size_t)m * CKw - ck0;
+                    for (int ck = ck0; ck < ck0 + CKw; ++ck) {
                         const REAL wv = wr[ck];
                         REAL *d = cg + (size_t)ck * Wo;
                         for (int ox = 0; ox < Wo; ++ox) d[ox] += wv * go[ox];
@@ -268,8 +275,9 @@ int FN(oracle_dcn_backward)(const REAL *input, const REAL *weight, const REAL *o
                 /* grad_weight, com.cu:829-830: gW[m][ck] += sum_ox gO[m][ox] * cols[ck][ox] */
                 for (int m = 0; m < Cout; ++m) {
                     const REAL *go = grad_out + (((size_t)b * Cout + m) * Ho + oy) * Wo;
-                    REAL *gwr = gw + (size_t)m * CK;
-                    for (int ck = 0; ck < CK; ++ck) {
+                    const int ck0 = (m / mpg) * CKw;
+                    REAL *gwr = gw + (size_t)m * CKw - ck0;
+                    for (int ck = ck0; ck < ck0 + CKw; ++ck) {
                         const REAL *csr = cs + (size_t)ck * Wo;
                         REAL s = 0;
                         for (int ox = 0; ox < Wo; ++ox) s += go[ox] * csr[ox];
@@ -282,8 +290,8 @@ int FN(oracle_dcn_backward)(const REAL *input, const REAL *weight, const REAL *o
         free(cs);
     }
     for (int t = 0; t < nt; ++t) {
-        const REAL *src = gw_part + (size_t)t * Cout * CK;
-        for (size_t e = 0; e < (size_t)Cout * CK; ++e) grad_weight[e] += src[e];
+        const REAL *src = gw_part + (size_t)t * Cout * CKw;
+        for (size_t e = 0; e < (size_t)Cout * CKw; ++e) grad_weight[e] += src[e];
     }
     free(gw_part);
     return 0;

@@ -42,10 +42,10 @@ def _load():
             p = ctypes.POINTER(ct)
             i = ctypes.c_int
             fwd = getattr(lib, "oracle_dcn_forward" + suffix)
-            fwd.argtypes = [p] * 5 + [i] * 14 + [p, i, i]
+            fwd.argtypes = [p] * 5 + [i] * 15 + [p, i, i]
             fwd.restype = i
             bwd = getattr(lib, "oracle_dcn_backward" + suffix)
-            bwd.argtypes = [p] * 5 + [i] * 14 + [p] * 5 + [i, i, i]
+            bwd.argtypes = [p] * 5 + [i] * 15 + [p] * 5 + [i, i, i]
             bwd.restype = i
         _lib = lib
     return _lib
@@ -78,8 +78,10 @@ def out_size(n, k, s, p, d):
 def _geometry(input, weight, offset, mask, stride, padding, dilation, deformable_groups):
     B, C, H, W = input.shape
     Cout, Cw, kh, kw = weight.shape
-    if Cw != C:
-        raise ValueError(f"weight has {Cw} input channels, input has {C}")
+    # torchvision's weight groups: C / weight.shape[1] of them
+    if Cw <= 0 or C % Cw or Cout % (C // Cw):
+        raise ValueError(f"weight has {Cw} input channels per group, input has {C}, "
+                         f"output {Cout}")
     sh, sw = _pair(stride)
     ph, pw = _pair(padding)
     dh, dw = _pair(dilation)
@@ -89,7 +91,7 @@ def _geometry(input, weight, offset, mask, stride, padding, dilation, deformable
         raise ValueError(f"offset shape {offset.shape} != {(B, 2 * G * kh * kw, Ho, Wo)}")
     if mask is not None and mask.shape != (B, G * kh * kw, Ho, Wo):
         raise ValueError(f"mask shape {mask.shape} != {(B, G * kh * kw, Ho, Wo)}")
-    return (B, C, H, W, Cout, kh, kw, sh, sw, ph, pw, dh, dw, G), (Ho, Wo)
+    return (B, C, H, W, Cout, kh, kw, sh, sw, ph, pw, dh, dw, G, C // Cw), (Ho, Wo)
 
 
 def dcn_forward(input, weight, mask, offset, bias, stride=1, padding=0, dilation=1,
@@ -125,7 +127,7 @@ def dcn_backward(input, weight, mask, offset, bias, grad_output, stride=1, paddi
     x, w, o, m, go = (_arr(t, dt) for t in (input, weight, offset, mask, grad_output))
     geo, (Ho, Wo) = _geometry(x, w, o, m, stride, padding, dilation, deformable_groups)
     B, C, H, W, Cout, kh, kw = geo[:7]
-    G = geo[-1]
+    G = geo[13]
     if go.shape != (B, Cout, Ho, Wo):
         raise ValueError(f"grad_output shape {go.shape} != {(B, Cout, Ho, Wo)}")
     gi = np.empty_like(x)

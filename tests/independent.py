@@ -22,9 +22,12 @@ def _pair(v):
 
 def deform_conv2d_gs(input, weight, offset, mask, bias, stride=1, padding=0, dilation=1,
                      deformable_groups=1):
-    """Modulated deformable conv by grid_sample, differentiable in all inputs."""
+    """Modulated deformable conv by grid_sample, differentiable in all inputs.
+    A weight of shape [Cout, C/WG, kh, kw] gives WG weight groups, contracted
+    group by group (torchvision's deform_conv2d semantics)."""
     B, C, H, W = input.shape
-    Cout, _, kh, kw = weight.shape
+    Cout, Cw, kh, kw = weight.shape
+    WG = C // Cw
     sh, sw = _pair(stride)
     ph, pw = _pair(padding)
     dh, dw = _pair(dilation)
@@ -54,8 +57,8 @@ def deform_conv2d_gs(input, weight, offset, mask, bias, stride=1, padding=0, dil
         if mask is not None:
             s = s * mask.view(B, G, KK, Ho, Wo)[:, g].unsqueeze(1)
         cols.append(s)
-    cols = torch.cat(cols, dim=1).reshape(B, C * KK, Ho * Wo)
-    out = torch.matmul(weight.reshape(Cout, C * KK), cols).view(B, Cout, Ho, Wo)
+    cols = torch.cat(cols, dim=1).reshape(B, WG, Cw * KK, Ho * Wo)
+    out = torch.matmul(weight.reshape(WG, Cout // WG, Cw * KK), cols).view(B, Cout, Ho, Wo)
     if bias is not None:
         out = out + bias.view(1, Cout, 1, 1)
     return out

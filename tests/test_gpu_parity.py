@@ -239,3 +239,26 @@ def test_forward_deterministic():
     b = gpu_forward(t, w.geometry())
     torch.cuda.synchronize()
     assert torch.equal(a, b)
+
+
+# --------------------------------------------------------------------------- weight groups
+@pytest.mark.parametrize("case", [
+    # C, Cout, deformable groups, weight groups, H, W
+    (24, 36, 2, 3, 11, 13),
+    (128, 128, 1, 2, 17, 15),    # 64 channels per weight group: one f16 chunk each
+    (16, 32, 1, 16, 9, 10),      # one input channel per weight group
+], ids=["wg3_dg2", "wg2_c128", "wg16_c16"])
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+def test_weight_groups(dtype, case):
+    """torchvision's weight groups (weight [Cout, C/WG, kh, kw]): forward and all
+    five gradients against the oracle's grouped loops."""
+    C, Cout, G, WG, H, W = case
+    w, t = _small(dtype, B=2, C=C, H=H, W=W, Cout=Cout, G=G, osc=2.0)
+    t["weight"] = t["weight"][:, : C // WG].contiguous()
+    out = gpu_forward(t, w.geometry())
+    grads = gpu_backward(t, w.geometry())
+    torch.cuda.synchronize()
+    assert tuple(grads[3].shape) == tuple(t["weight"].shape)
+    check("output", out, oracle_forward(t, w.geometry()), TOL[dtype])
+    for name, g, r in zip(GRADS, grads, oracle_backward(t, w.geometry())):
+        check(name, g, r, TOL[dtype])

@@ -49,8 +49,8 @@ def header_functions():
 
 
 def desc(B=2, C=8, H=9, W=10, Co=5, kh=3, kw=3, sh=1, sw=1, ph=1, pw=1, dh=1, dw=1, G=1,
-         dtype=0):
-    return _C.Desc(B, C, H, W, Co, kh, kw, sh, sw, ph, pw, dh, dw, G, dtype)
+         dtype=0, WG=0):
+    return _C.Desc(B, C, H, W, Co, kh, kw, sh, sw, ph, pw, dh, dw, G, dtype, WG)
 
 
 def out_hw(L, d):
@@ -90,6 +90,9 @@ def test_output_shape_matches_formula(L, geo):
 
 @pytest.mark.parametrize("bad,code,msg", [
     (dict(G=3), 1, "divisible"),
+    (dict(WG=3), 1, "weight_groups"),
+    (dict(C=8, Co=6, WG=4), 1, "weight_groups"),
+    (dict(WG=-1), 1, "weight_groups"),
     (dict(dtype=7), 1, "dtype"),
     (dict(C=0), 1, "shape"),
     (dict(sh=0), 1, "stride"),
@@ -304,3 +307,30 @@ def test_workload_flops_and_determinism():
         if a[k] is not None:
             assert torch.equal(a[k], b[k]), k
     assert np.isfinite(a["offset"].numpy()).all()
+
+
+def test_dcnv2_module_weight_groups(oracle_C):
+    """DCNv2(groups=2): weight [Cout, C/2, kh, kw], fan-in init over C/2*kh*kw,
+    and the autograd plumbing carries the grouped weight through unchanged
+    (values and gradients against the grid_sample formulation)."""
+    torch.manual_seed(2)
+    mod = dcnv2_amd.DCNv2(6, 4, 3, stride=1, padding=1, deformable_groups=3, groups=2).double()
+    assert tuple(mod.weight.shape) == (4, 3, 3, 3)
+    assert float(mod.weight.detach().abs().max()) <= 1.0 / (3 * 9) ** 0.5
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(2, 6, 7, 6, generator=g, dtype=torch.float64)
+    off = torch.randn(2, 2 * 3 * 9, 7, 6, generator=g, dtype=torch.float64) * 1.2
+    m = torch.rand(2, 3 * 9, 7, 6, generator=g, dtype=torch.float64)
+    go = torch.randn(2, 4, 7, 6, generator=g, dtype=torch.float64)
+    with torch.no_grad():
+        mod.bias.normal_()
+    y = mod(x, off, m)
+    y.backward(go)
+    w = mod.weight.detach().clone().requires_grad_(True)
+    y_ref = deform_conv2d_gs(x, w, off, m, mod.bias.detach(), stride=1, padding=1,
+                             dilation=1, deformable_groups=3)
+    y_ref.backward(go)
+    assert rel_err(y, y_ref) < 1e-12
+    assert rel_err(mod.weight.grad, w.grad) < 1e-12
+    with pytest.raises(ValueError):
+        dcnv2_amd.DCNv2(6, 5, 3, 1, 1, groups=2)

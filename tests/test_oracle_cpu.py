@@ -298,3 +298,83 @@ def test_backward_rejects_bad_shapes():
                            **geo)
     with pytest.raises(ValueError):
         oracle.dcn_backward(*(t[k] for k in IN5), t["grad_output"][:, :1], **geo)
+
+
+# -- torchvision weight groups -------------------------------------------------------
+WG_GEOMS = [
+    # B, C, H, W, Co, kh, kw, s, p, d, G, WG
+    (1, 4, 7, 7, 6, 3, 3, 1, 1, 1, 1, 2),
+    (2, 6, 8, 9, 9, 3, 3, 2, 1, 1, 2, 3),
+    (1, 4, 9, 8, 8, 3, 3, 1, 2, 2, 4, 4),   # depthwise-like: one input channel per group
+    (1, 6, 6, 7, 4, 3, 2, 1, 1, 1, 3, 2),   # deformable groups cut across weight groups
+]
+
+
+def _grouped_case(geom, seed, osc=1.0):
+    *g11, WG = geom
+    t, geo = rand_case(*g11, seed=seed, osc=osc)
+    C = g11[1]
+    t["weight"] = t["weight"][:, : C // WG].contiguous()
+    return t, geo, WG
+
+
+@pytest.mark.parametrize("geom", WG_GEOMS)
+def test_weight_groups_zero_offset_is_grouped_conv2d(geom):
+    """Zero offset, mask 1: exactly F.conv2d(groups=WG), forward and the
+    grad_input / grad_weight / grad_bias of its autograd."""
+    t, geo, WG = _grouped_case(geom, seed=3)
+    t["offset"].zero_()
+    t["mask"].fill_(1.0)
+    x = t["input"].clone().requires_grad_(True)
+    w = t["weight"].clone().requires_grad_(True)
+    b = t["bias"].clone().requires_grad_(True)
+    ref = F.conv2d(x, w, b, stride=geo["stride"], padding=geo["padding"],
+                   dilation=geo["dilation"], groups=WG)
+    ref.backward(t["grad_output"])
+    assert rel_err(fwd(t, geo), ref) < 1e-13
+    gi, goff, gm, gw, gb = bwd(t, geo)
+    assert gw.shape == tuple(w.shape)
+    assert rel_err(gi, x.grad) < 1e-13
+    assert rel_err(gw, w.grad) < 1e-13
+    assert rel_err(gb, b.grad) < 1e-13
+
+
+@pytest.mark.parametrize("geom", WG_GEOMS)
+def test_weight_groups_match_independent_formulation(geom):
+    """Random fractional offsets: the oracle's grouped loops against the
+    grid_sample formulation, which contracts each weight group with its own
+    matmul and takes every gradient from autograd."""
+    from independent import forward_backward_gs
+    t, geo, WG = _grouped_case(geom, seed=4, osc=1.3)
+    out, *grads = forward_backward_gs(t["input"], t["weight"], t["offset"], t["mask"],
+                                      t["bias"], t["grad_output"], **geo)
+    assert rel_err(fwd(t, geo), out) < 1e-12
+    for name, a, r in zip(GRADS, bwd(t, geo), grads):
+        assert rel_err(a, r) < 1e-10, name
+
+
+def test_weight_groups_are_block_diagonal():
+    """A grouped weight equals the full weight that is zero outside each output
+    channel's group (forward and grad_input), and its grad_weight is that full
+    weight's grad_weight restricted to the group blocks."""
+    t, geo, WG = _grouped_case(WG_GEOMS[1], seed=5, osc=2.0)
+    Co, Cw = t["weight"].shape[:2]
+    full = torch.zeros(Co, Cw * WG, *t["weight"].shape[2:], dtype=f64)
+    mpg = Co // WG
+    for gw in range(WG):
+        full[gw * mpg:(gw + 1) * mpg, gw * Cw:(gw + 1) * Cw] = t["weight"][gw * mpg:(gw + 1) * mpg]
+    tf = dict(t, weight=full)
+    assert rel_err(fwd(t, geo), fwd(tf, geo)) < 1e-13
+    g_grp, g_full = bwd(t, geo), bwd(tf, geo)
+    for i in (0, 1, 2, 4):
+        assert rel_err(g_grp[i], g_full[i]) < 1e-12
+    blocks = np.concatenate([g_full[3][gw * mpg:(gw + 1) * mpg, gw * Cw:(gw + 1) * Cw]
+                             for gw in range(WG)])
+    assert rel_err(g_grp[3], blocks) < 1e-13
+
+
+def test_weight_groups_reject_bad_split():
+    t, geo, _ = _grouped_case(WG_GEOMS[0], seed=6)
+    t["weight"] = t["weight"][:5]   # Cout 5 does not split over 2 groups
+    with pytest.raises(ValueError):
+        fwd(t, geo)
