@@ -248,6 +248,32 @@ def main():
             "kernel_ms": round(kern_ms, 5),
         },
     }
+    # The same two workloads with a channels_last input: the kernels read it in
+    # place (C = 64 needs no channel padding), so the repacking pass drops out,
+    # and grad_input is written channels-last directly.
+    x_cl = t["input"].to(memory_format=torch.channels_last)
+    x2_cl = t2["input"].to(memory_format=torch.channels_last)
+
+    def fwd_cl():
+        return _C.dcn_v2_forward(x_cl, *fargs[1:], *geo)
+
+    def fwd_bwd_cl():
+        _C.dcn_v2_forward(x2_cl, *b_args[1:], *geo)
+        return _C.dcn_v2_backward(x2_cl, *b_args[1:], t2["grad_output"], *geo)
+
+    for _ in range(50):
+        fwd_cl()
+    cl_fwd_ms = _events_ms(fwd_cl, args.steps, torch)
+    for _ in range(5):
+        fwd_bwd_cl()
+    result["channels_last_input"] = {
+        "fwd_ms": round(cl_fwd_ms, 5),
+        "fwd_readme_tflops": round(fwd_w.readme_flops() / (cl_fwd_ms * 1e-3) / 1e12, 2),
+        "fwd_bwd_ms": round(_events_ms(fwd_bwd_cl, fb_steps, torch), 5),
+        "note": "input (and grad_input) channels_last, read in place; output NCHW",
+    }
+    del x_cl, x2_cl
+
     # The DCN module (offset/mask predictor conv + operator) at the same shape,
     # forward + backward: the fused path hands the predictor output to the
     # kernels; the separate path materialises chunk / cat / sigmoid as the

@@ -13,7 +13,9 @@ Extensions over the reference, all trailing and optional: ``dilation_h``,
 ``dilation_w`` and ``deformable_groups`` (the reference's Python module accepts
 them but never forwards them, ``dcn_v2_mm.py:67-68, 94-102``); fp16/bf16 as
 well as fp32 tensors; ``mask`` and ``bias`` may be ``None``; a weight of shape
-``[Cout, C/groups, kh, kw]`` selects torchvision's weight groups.
+``[Cout, C/groups, kh, kw]`` selects torchvision's weight groups; a
+``channels_last`` input is read without a layout copy, and its ``grad_input``
+comes back channels_last (the output stays contiguous NCHW).
 
 Errors: any invalid device, dtype, shape or launch failure raises
 ``RuntimeError``, as the reference's ``AT_ASSERTM`` checks do
@@ -39,7 +41,7 @@ class Desc(ctypes.Structure):
     _fields_ = [(name, ctypes.c_int32) for name in (
         "batch", "in_channels", "height", "width", "out_channels", "kernel_h", "kernel_w",
         "stride_h", "stride_w", "pad_h", "pad_w", "dilation_h", "dilation_w",
-        "deformable_groups", "dtype", "weight_groups")]
+        "deformable_groups", "dtype", "weight_groups", "input_layout")]
 
 
 def library_path() -> str:
@@ -95,14 +97,27 @@ def _ptr(t):
     return None if t is None else ctypes.c_void_p(t.data_ptr())
 
 
+def _input_layout(input):
+    """(input, layout): a channels_last input (one that is not also contiguous
+    NCHW) is handed over as it is, with layout 1 (``DCN2_NHWC``); the kernels
+    read it in place when its channels need no padding.  Anything else becomes
+    contiguous NCHW, layout 0.  grad_input is returned in the same layout."""
+    cl = torch.channels_last
+    if input.dim() == 4 and not input.is_contiguous() and input.is_contiguous(memory_format=cl):
+        if input.data_ptr() % 16:  # in-place reads use 16-byte loads
+            input = input.clone(memory_format=cl)
+        return input, 1
+    return input.contiguous(), 0
+
+
 def make_desc(input, weight, stride_h, stride_w, pad_h, pad_w, dilation_h, dilation_w,
-              deformable_groups) -> Desc:
+              deformable_groups, input_layout=0) -> Desc:
     B, C, H, W = (int(v) for v in input.shape)
     Cout, Cw, kh, kw = (int(v) for v in weight.shape)
     # weight groups follow from weight.shape[1], as in torchvision's deform_conv2d
     return Desc(B, C, H, W, Cout, kh, kw, int(stride_h), int(stride_w), int(pad_h), int(pad_w),
                 int(dilation_h), int(dilation_w), int(deformable_groups), _DTYPES[input.dtype],
-                C // Cw)
+                C // Cw, int(input_layout))
 
 
 def _validate(name, input, weight, mask, offset, bias, extra=()):
@@ -166,11 +181,12 @@ def dcn_v2_forward(input, weight, mask, offset, bias, stride_h, stride_w, pad_h,
     ``[B, Cout, Ho, Wo]`` in the input dtype."""
     name = "dcn_v2_forward"
     _validate(name, input, weight, mask, offset, bias)
-    input, weight, offset = input.contiguous(), weight.contiguous(), offset.contiguous()
+    input, layout = _input_layout(input)
+    weight, offset = weight.contiguous(), offset.contiguous()
     mask = mask.contiguous() if mask is not None else None
     bias = bias.contiguous() if bias is not None else None
     desc = make_desc(input, weight, stride_h, stride_w, pad_h, pad_w, dilation_h, dilation_w,
-                     deformable_groups)
+                     deformable_groups, layout)
     ho, wo = _geometry(name, desc, input, mask, offset)
     L = lib()
     out = torch.empty((desc.batch, desc.out_channels, ho, wo), dtype=input.dtype,
@@ -196,17 +212,18 @@ def dcn_v2_backward(input, weight, mask, offset, bias, grad_output, stride_h, st
     ``mask``/``bias`` is."""
     name = "dcn_v2_backward"
     _validate(name, input, weight, mask, offset, bias, extra=[("grad_output", grad_output)])
-    input, weight, offset = input.contiguous(), weight.contiguous(), offset.contiguous()
+    input, layout = _input_layout(input)
+    weight, offset = weight.contiguous(), offset.contiguous()
     mask = mask.contiguous() if mask is not None else None
     grad_output = grad_output.contiguous()
     desc = make_desc(input, weight, stride_h, stride_w, pad_h, pad_w, dilation_h, dilation_w,
-                     deformable_groups)
+                     deformable_groups, layout)
     ho, wo = _geometry(name, desc, input, mask, offset)
     if tuple(grad_output.shape) != (desc.batch, desc.out_channels, ho, wo):
         raise RuntimeError(f"{name}: grad_output shape {tuple(grad_output.shape)} != "
                            f"{(desc.batch, desc.out_channels, ho, wo)}")
     L = lib()
-    grad_input = torch.empty_like(input)
+    grad_input = torch.empty_like(input)  # keeps the channels_last layout of layout 1
     grad_offset = torch.empty_like(offset)
     grad_mask = torch.empty_like(mask) if mask is not None else None
     grad_weight = torch.empty_like(weight)
@@ -247,10 +264,11 @@ def dcn_v2_forward_om(input, weight, om, bias, stride_h, stride_w, pad_h, pad_w,
     (``dcn_v2_mm.py:133-137``), done inside the kernels."""
     name = "dcn_v2_forward_om"
     _validate(name, input, weight, None, om, bias)
-    input, weight, om = input.contiguous(), weight.contiguous(), om.contiguous()
+    input, layout = _input_layout(input)
+    weight, om = weight.contiguous(), om.contiguous()
     bias = bias.contiguous() if bias is not None else None
     desc = make_desc(input, weight, stride_h, stride_w, pad_h, pad_w, dilation_h, dilation_w,
-                     deformable_groups)
+                     deformable_groups, layout)
     ho, wo = _om_geometry(name, desc, om)
     L = lib()
     out = torch.empty((desc.batch, desc.out_channels, ho, wo), dtype=input.dtype,
@@ -275,16 +293,17 @@ def dcn_v2_backward_om(input, weight, om, bias, grad_output, stride_h, stride_w,
     gradient of the mask logits (``grad_mask * mask * (1 - mask)``)."""
     name = "dcn_v2_backward_om"
     _validate(name, input, weight, None, om, bias, extra=[("grad_output", grad_output)])
-    input, weight, om = input.contiguous(), weight.contiguous(), om.contiguous()
+    input, layout = _input_layout(input)
+    weight, om = weight.contiguous(), om.contiguous()
     grad_output = grad_output.contiguous()
     desc = make_desc(input, weight, stride_h, stride_w, pad_h, pad_w, dilation_h, dilation_w,
-                     deformable_groups)
+                     deformable_groups, layout)
     ho, wo = _om_geometry(name, desc, om)
     if tuple(grad_output.shape) != (desc.batch, desc.out_channels, ho, wo):
         raise RuntimeError(f"{name}: grad_output shape {tuple(grad_output.shape)} != "
                            f"{(desc.batch, desc.out_channels, ho, wo)}")
     L = lib()
-    grad_input = torch.empty_like(input)
+    grad_input = torch.empty_like(input)  # keeps the channels_last layout of layout 1
     grad_om = torch.empty_like(om)
     grad_weight = torch.empty_like(weight)
     grad_bias = torch.empty((desc.out_channels,), dtype=input.dtype, device=input.device) \

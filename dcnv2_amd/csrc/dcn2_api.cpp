@@ -51,6 +51,9 @@ static int make_geo(const dcn2_desc *d, Geo &g) {
     g.G = d->deformable_groups;
     g.dtype = d->dtype;
     g.WG = d->weight_groups == 0 ? 1 : d->weight_groups;
+    g.nhwc = d->input_layout;
+    if (g.nhwc != DCN2_NCHW && g.nhwc != DCN2_NHWC)
+        return fail(DCN2_EINVAL, "dcn2: unsupported input_layout %d", g.nhwc);
     if (g.dtype != DCN2_F32 && g.dtype != DCN2_F16 && g.dtype != DCN2_BF16)
         return fail(DCN2_EINVAL, "dcn2: unsupported dtype code %d", g.dtype);
     if (g.B < 0 || g.C <= 0 || g.H <= 0 || g.W <= 0 || g.Cout <= 0)
@@ -79,6 +82,7 @@ static int make_geo(const dcn2_desc *d, Geo &g) {
     g.Cg = g.C / g.G;
     g.Cgp = round_up(g.Cg, g.KC);
     g.cs = g.G * g.Cgp;
+    g.xt_direct = g.nhwc && g.cs == g.C;
     g.N = g.Ho * g.Wo;
     g.KK = g.kh * g.kw;
     g.BM = g.Cout > 128 ? 256 : 128;
@@ -117,7 +121,7 @@ FwdWorkspace fwd_workspace(const Geo &g) {
     FwdWorkspace w;
     size_t o = 0;
     w.xt = o;
-    o += align256((size_t)g.B * g.H * g.W * g.cs * g.esz);
+    if (!g.xt_direct) o += align256((size_t)g.B * g.H * g.W * g.cs * g.esz);
     w.wp = o;
     o += align256((size_t)g.Mp * g.Kp * g.esz);
     w.tab = o;
@@ -130,7 +134,7 @@ BwdWorkspace bwd_workspace(const Geo &g) {
     BwdWorkspace w;
     size_t o = 0;
     w.xt = o;
-    o += align256((size_t)g.B * g.H * g.W * g.cs * g.esz);
+    if (!g.xt_direct) o += align256((size_t)g.B * g.H * g.W * g.cs * g.esz);
     w.wt = o;
     o += align256((size_t)g.Mp * g.Kp * g.esz);
     w.tab = o;
@@ -175,11 +179,16 @@ static int forward_impl(const Geo &g, const void *input, const void *weight, con
                     "dcn2_forward: workspace needs %zu bytes at 256-byte alignment (got %zu)",
                     ws.total, workspace_bytes);
     if (g.B == 0) return DCN2_OK;
+    if (g.xt_direct && ((uintptr_t)input & 15))
+        return fail(DCN2_EINVAL, "dcn2_forward: a channels-last input must be 16-byte aligned");
     hipStream_t s = (hipStream_t)stream;
     char *base = (char *)workspace;
-    void *xt = base + ws.xt, *wp = base + ws.wp, *tab = base + ws.tab;
+    // a channels-last input whose channels need no padding is read in place
+    const void *xt = g.xt_direct ? input : base + ws.xt;
+    void *wp = base + ws.wp, *tab = base + ws.tab;
     prof_begin(DCN2_STAGE_FWD_PACK, s);
-    if ((rc = check_launch(launch_pack(g, input, xt, weight, wp, tab, false, s), "pack")))
+    if ((rc = check_launch(launch_pack(g, g.xt_direct ? nullptr : input, (void *)xt, weight, wp,
+                                       tab, false, s), "pack")))
         return rc;
     prof_end(DCN2_STAGE_FWD_PACK, s);
     prof_begin(DCN2_STAGE_FWD_MAIN, s);
@@ -205,11 +214,15 @@ static int backward_impl(const Geo &g, const void *input, const void *weight, co
         return fail(DCN2_EWORKSPACE,
                     "dcn2_backward: workspace needs %zu bytes at 256-byte alignment (got %zu)",
                     ws.total, workspace_bytes);
+    if (g.B > 0 && g.xt_direct && ((uintptr_t)input & 15))
+        return fail(DCN2_EINVAL, "dcn2_backward: a channels-last input must be 16-byte aligned");
     hipStream_t s = (hipStream_t)stream;
     char *base = (char *)workspace;
-    void *xt = base + ws.xt, *wt = base + ws.wt, *tab = base + ws.tab;
+    const void *xt = g.xt_direct ? input : base + ws.xt;
+    void *wt = base + ws.wt, *tab = base + ws.tab;
     prof_begin(DCN2_STAGE_BWD_PACK, s);
-    if ((rc = check_launch(launch_pack(g, input, xt, weight, wt, tab, true, s), "pack")))
+    if ((rc = check_launch(launch_pack(g, g.xt_direct ? nullptr : input, (void *)xt, weight, wt,
+                                       tab, true, s), "pack")))
         return rc;
     prof_end(DCN2_STAGE_BWD_PACK, s);
     return check_launch(launch_backward(g, xt, wt, tab, offset, mask, grad_output,

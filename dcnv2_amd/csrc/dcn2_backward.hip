@@ -1470,6 +1470,21 @@ __global__ __launch_bounds__(256) void finalize_gi_kernel(const float *__restric
     }
 }
 
+// gi_acc [B][HW][cs] fp32 -> channels-last grad_input [B][HW][C] T: one
+// element per thread, contiguous on both sides.
+template <typename T>
+__global__ __launch_bounds__(256) void finalize_gi_nhwc_kernel(const float *__restrict__ acc,
+                                                               T *__restrict__ gi, long total,
+                                                               int C, int Cg, int Cgp, int cs) {
+    for (long idx = (long)blockIdx.x * 256 + threadIdx.x; idx < total;
+         idx += (long)gridDim.x * 256) {
+        const long px = idx / C;
+        const int c = (int)(idx - px * C);
+        const int g = c / Cg, ci = c - g * Cg;
+        gi[idx] = (T)acc[px * cs + g * Cgp + ci];
+    }
+}
+
 // gw_acc [Mp][Kp] (K order tap, group, channel) -> grad_weight [Cout][C][kh][kw];
 // gb_acc -> grad_bias.
 template <typename T>
@@ -1619,9 +1634,16 @@ static hipError_t backward_t(const Geo &g, const BwdParams &p0, void *grad_input
         prof_begin(DCN2_STAGE_BWD_FINAL, s);
         {
             const int HW = g.H * g.W;
-            dim3 grid(ceil_div(HW, 64), g.cs / 32, g.B);
-            finalize_gi_kernel<T><<<grid, 256, 0, s>>>(p.gi_acc, (T *)grad_input, g.C, HW, g.Cg,
-                                                       g.Cgp, g.cs);
+            if (g.nhwc) {
+                const long total = (long)g.B * HW * g.C;
+                const unsigned blocks = (unsigned)std::min<long>((total + 255) / 256, 16384);
+                finalize_gi_nhwc_kernel<T><<<blocks, 256, 0, s>>>(
+                    p.gi_acc, (T *)grad_input, total, g.C, g.Cg, g.Cgp, g.cs);
+            } else {
+                dim3 grid(ceil_div(HW, 64), g.cs / 32, g.B);
+                finalize_gi_kernel<T><<<grid, 256, 0, s>>>(p.gi_acc, (T *)grad_input, g.C, HW,
+                                                           g.Cg, g.Cgp, g.cs);
+            }
             if ((e = hipGetLastError()) != hipSuccess) return e;
         }
         prof_end(DCN2_STAGE_BWD_FINAL, s);

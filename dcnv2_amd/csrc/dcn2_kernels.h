@@ -15,6 +15,8 @@ struct Geo {
     int esz;        // element size in bytes
     int Cg;         // channels per deformable group
     int WG, Cw;     // weight groups and input channels per weight group (C / WG)
+    int nhwc;       // input / grad_input are channels-last [B][H][W][C]
+    int xt_direct;  // nhwc and cs == C: the input itself serves as xt (no repacking)
     int KC;         // channel chunk of one LDS stage (64 for f16/bf16, 32 for f32)
     int Cgp;        // Cg rounded up to KC
     int cs;         // channels-last pixel stride of xt: G*Cgp
@@ -50,8 +52,9 @@ struct GatherGeo {
 };
 GatherGeo gather_geometry(const Geo &g);
 
-// dcn2_pack.hip: input -> xt (skipped when B == 0) and weight -> wp + chunk
-// table in one launch; transpose selects the backward's W'^T fragment order.
+// dcn2_pack.hip: input -> xt (skipped when input is null) and weight -> wp +
+// chunk table in one launch; transpose selects the backward's W'^T fragment
+// order.  The input is NCHW, or channels-last when g.nhwc.
 hipError_t launch_pack(const Geo &g, const void *input, void *xt, const void *weight, void *wp,
                        void *tab, bool transpose, hipStream_t s);
 

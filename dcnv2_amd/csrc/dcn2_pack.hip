@@ -31,7 +31,33 @@ struct PackParams {
     int Cw, mpg;                   // channels and output channels per weight group
     int kc, kstep, kpl, Mp, Kp;    // MFMA packing
     int transpose;                 // 0: forward A fragments, 1: backward W'^T fragments
+    int nhwc;                      // input is channels-last [B][HW][C]
 };
+
+// Channels-last input [B][HW][C] -> xt [B][HW][cs]: the same tile of 64
+// pixels x CT padded channels, one element per thread and step (consecutive
+// threads take consecutive channels of a pixel, so both sides are contiguous).
+// Only used when the padding makes xt differ from the input; otherwise the
+// kernels read the input in place.
+template <typename T>
+__device__ __forceinline__ void pack_input_block_nhwc(const PackParams &p, int blk) {
+    constexpr int CT = 128 / sizeof(T);
+    const T *__restrict__ in = (const T *)p.in;
+    T *__restrict__ xt = (T *)p.xt;
+    const int pt = blk % p.pxt, ct = (blk / p.pxt) % p.cht, b = blk / (p.pxt * p.cht);
+    const int px0 = pt * 64, cp0 = ct * CT;
+#pragma unroll
+    for (int k = 0; k < 64 * CT / 256; ++k) {
+        const int idx = threadIdx.x + k * 256;
+        const int pl = idx / CT, cl = idx - pl * CT;
+        const int px = px0 + pl, cp = cp0 + cl;
+        if (px >= p.HW) continue;
+        const int g = cp / p.Cgp, ci = cp - g * p.Cgp;
+        T v = (T)0.0f;
+        if (ci < p.Cg) v = in[((size_t)b * p.HW + px) * p.C + g * p.Cg + ci];
+        xt[((size_t)b * p.HW + px) * p.cs + cp] = v;
+    }
+}
 
 // Input transpose: 64 pixels x CT padded channels per block, 256 threads.
 template <typename T>
@@ -148,9 +174,12 @@ __device__ __forceinline__ void pack_weight_block(const PackParams &p, int blk) 
 template <typename T>
 __global__ __launch_bounds__(256) void pack_kernel(const PackParams p) {
     const int blk = blockIdx.x;
-    if (blk < p.nin)
-        pack_input_block<T>(p, blk);
-    else
+    if (blk < p.nin) {
+        if (p.nhwc)
+            pack_input_block_nhwc<T>(p, blk);
+        else
+            pack_input_block<T>(p, blk);
+    } else
         pack_weight_block<T>(p, blk - p.nin);
 }
 
@@ -188,6 +217,7 @@ static hipError_t pack_t(const Geo &g, const void *input, void *xt, const void *
     p.Mp = g.Mp;
     p.Kp = g.Kp;
     p.transpose = transpose ? 1 : 0;
+    p.nhwc = g.nhwc;
     const long nw = ((long)g.Mp * g.Kp + 255) / 256;
     const long blocks = p.nin + nw;
     pack_kernel<T><<<(unsigned)blocks, 256, 0, s>>>(p);
@@ -196,7 +226,7 @@ static hipError_t pack_t(const Geo &g, const void *input, void *xt, const void *
 
 hipError_t launch_pack(const Geo &g, const void *input, void *xt, const void *weight, void *wp,
                        void *tab, bool transpose, hipStream_t s) {
-    if (g.B == 0) input = nullptr;  // weight packing only
+    if (g.B == 0) input = nullptr;  // weight packing only (also for an input read in place)
     switch (g.dtype) {
     case DCN2_F16: return pack_t<f16>(g, input, xt, weight, wp, tab, transpose, s);
     case DCN2_BF16: return pack_t<bf16>(g, input, xt, weight, wp, tab, transpose, s);

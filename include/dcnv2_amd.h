@@ -47,6 +47,14 @@ extern "C" {
 
 enum dcn2_dtype { DCN2_F32 = 0, DCN2_F16 = 1, DCN2_BF16 = 2 };
 
+/* Memory layout of `input` and `grad_input` (every other tensor is NCHW).
+ * DCN2_NHWC is torch's channels_last: [B][H][W][C].  When C/deformable_groups
+ * is a multiple of 64 (fp16/bf16) or 32 (fp32) the kernels read such an input
+ * in place (it must then be 16-byte aligned) and the forward workspace holds
+ * no repacked copy; otherwise it is repacked like an NCHW input.  No
+ * counterpart in the reference, which takes contiguous NCHW only. */
+enum dcn2_layout { DCN2_NCHW = 0, DCN2_NHWC = 1 };
+
 enum dcn2_status {
     DCN2_OK = 0,
     DCN2_EINVAL = 1,     /* bad geometry, dtype, null pointer or group split     */
@@ -62,7 +70,8 @@ enum dcn2_status {
  * but never forwards (dcn_v2_mm.py:67-68, 94-102), and by torchvision's weight
  * groups (its deform_conv2d infers them from weight.shape[1]; the reference has
  * none).  weight_groups 0 means 1, so a zero-initialised descriptor is
- * ungrouped; in_channels and out_channels must both divide by it. */
+ * ungrouped; in_channels and out_channels must both divide by it.
+ * input_layout is an enum dcn2_layout (0 = NCHW). */
 typedef struct dcn2_desc {
     int32_t batch, in_channels, height, width;
     int32_t out_channels, kernel_h, kernel_w;
@@ -70,6 +79,7 @@ typedef struct dcn2_desc {
     int32_t deformable_groups;
     int32_t dtype; /* enum dcn2_dtype */
     int32_t weight_groups;
+    int32_t input_layout;
 } dcn2_desc;
 
 /* Output spatial size for `d`; DCN2_EINVAL if it would be empty. */

@@ -262,3 +262,52 @@ def test_weight_groups(dtype, case):
     check("output", out, oracle_forward(t, w.geometry()), TOL[dtype])
     for name, g, r in zip(GRADS, grads, oracle_backward(t, w.geometry())):
         check(name, g, r, TOL[dtype])
+
+
+# --------------------------------------------------------------------------- channels_last
+@pytest.mark.parametrize("case", [
+    # dtype, C, deformable groups: in place when C/G is a multiple of the channel chunk
+    (torch.float16, 64, 1),      # read in place
+    (torch.bfloat16, 128, 2),    # read in place, two groups
+    (torch.float32, 64, 2),      # read in place (fp32 chunk is 32 channels)
+    (torch.float16, 24, 2),      # padded: repacked from channels-last
+], ids=["f16_c64", "bf16_c128_dg2", "f32_c64_dg2", "f16_c24_dg2_padded"])
+def test_channels_last_input(case):
+    """A channels_last input gives the same forward, bit for bit, as its NCHW
+    copy (the kernels see the same channels-last data), and a backward within
+    tolerance of the oracle whose grad_input is channels_last."""
+    dtype, C, G = case
+    w, t = _small(dtype, B=2, C=C, H=13, W=11, Cout=40, G=G, osc=2.0)
+    geo = w.geometry()
+    x_cl = t["input"].to(DEV).to(memory_format=torch.channels_last)
+    assert not x_cl.is_contiguous()
+    args = [None if t[k] is None else t[k].to(DEV) for k in IN5]
+    out_nchw = _C.dcn_v2_forward(*args, *_args(geo))
+    out_cl = _C.dcn_v2_forward(x_cl, *args[1:], *_args(geo))
+    grads = _C.dcn_v2_backward(x_cl, *args[1:], t["grad_output"].to(DEV), *_args(geo))
+    torch.cuda.synchronize()
+    assert torch.equal(out_cl, out_nchw)
+    assert grads[0].is_contiguous(memory_format=torch.channels_last)
+    for name, g, r in zip(GRADS, grads, oracle_backward(t, geo)):
+        check(name, g, r, TOL[dtype])
+
+
+def test_channels_last_predictor_output_path():
+    """dcn_v2_forward_om / dcn_v2_backward_om with a channels_last input match
+    the same calls on the NCHW copy."""
+    w, t = _small(torch.float16, B=2, C=64, H=10, W=12, Cout=32, G=1, osc=1.5)
+    geo = w.geometry()
+    x = t["input"].to(DEV)
+    om = torch.cat([t["offset"], torch.logit(t["mask"].float().clamp(1e-3, 1 - 1e-3)).to(
+        t["offset"].dtype)], 1).to(DEV)
+    wt, b, go = t["weight"].to(DEV), t["bias"].to(DEV), t["grad_output"].to(DEV)
+    x_cl = x.to(memory_format=torch.channels_last)
+    ref = _C.dcn_v2_forward_om(x, wt, om, b, *_args(geo))
+    got = _C.dcn_v2_forward_om(x_cl, wt, om, b, *_args(geo))
+    g_ref = _C.dcn_v2_backward_om(x, wt, om, b, go, *_args(geo))
+    g_cl = _C.dcn_v2_backward_om(x_cl, wt, om, b, go, *_args(geo))
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref)
+    assert g_cl[0].is_contiguous(memory_format=torch.channels_last)
+    for a, r in zip(g_cl, g_ref):
+        check("grad", a, r, TOL[torch.float16])

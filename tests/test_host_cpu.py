@@ -49,8 +49,8 @@ def header_functions():
 
 
 def desc(B=2, C=8, H=9, W=10, Co=5, kh=3, kw=3, sh=1, sw=1, ph=1, pw=1, dh=1, dw=1, G=1,
-         dtype=0, WG=0):
-    return _C.Desc(B, C, H, W, Co, kh, kw, sh, sw, ph, pw, dh, dw, G, dtype, WG)
+         dtype=0, WG=0, layout=0):
+    return _C.Desc(B, C, H, W, Co, kh, kw, sh, sw, ph, pw, dh, dw, G, dtype, WG, layout)
 
 
 def out_hw(L, d):
@@ -93,6 +93,7 @@ def test_output_shape_matches_formula(L, geo):
     (dict(WG=3), 1, "weight_groups"),
     (dict(C=8, Co=6, WG=4), 1, "weight_groups"),
     (dict(WG=-1), 1, "weight_groups"),
+    (dict(layout=2), 1, "input_layout"),
     (dict(dtype=7), 1, "dtype"),
     (dict(C=0), 1, "shape"),
     (dict(sh=0), 1, "stride"),
@@ -334,3 +335,17 @@ def test_dcnv2_module_weight_groups(oracle_C):
     assert rel_err(mod.weight.grad, w.grad) < 1e-12
     with pytest.raises(ValueError):
         dcnv2_amd.DCNv2(6, 5, 3, 1, 1, groups=2)
+
+
+def test_channels_last_workspace(L):
+    """A channels-last input whose channels need no padding is read in place:
+    the workspace drops exactly the repacked copy; with padding it keeps it."""
+    for dtype, esz, C in ((1, 2, 64), (2, 2, 128), (0, 4, 32)):
+        nchw, nhwc = desc(C=C, dtype=dtype), desc(C=C, dtype=dtype, layout=1)
+        copy = 2 * 9 * 10 * C * esz
+        for fn in (L.dcn2_forward_workspace_bytes, L.dcn2_backward_workspace_bytes):
+            a, b = fn(ctypes.byref(nchw)), fn(ctypes.byref(nhwc))
+            assert 0 < b < a and a - b == (copy + 255) // 256 * 256
+    padded_cl, padded = desc(C=24, dtype=1, layout=1), desc(C=24, dtype=1)
+    assert L.dcn2_forward_workspace_bytes(ctypes.byref(padded_cl)) == \
+        L.dcn2_forward_workspace_bytes(ctypes.byref(padded))
