@@ -6,6 +6,6 @@ native module ``Conv2d._C`` and ``dcnv2_amd.dcn_v2_mm`` mirrors
 ``include/dcnv2_amd.h``); build them with ``python -m dcnv2_amd.build``.
 """
 from . import _C  # noqa: F401
-from .dcn_v2_mm import DCN, DCNv2, _DCNv2, dcn_v2_conv  # noqa: F401
+from .dcn_v2_mm import DCN, DCNv2, _DCNv2, dcn_v2_conv, deform_conv2d  # noqa: F401
 
-__all__ = ["DCN", "DCNv2", "dcn_v2_conv", "_C"]
+__all__ = ["DCN", "DCNv2", "dcn_v2_conv", "deform_conv2d", "_C"]

@@ -71,6 +71,24 @@ class _DCNv2(Function):
 dcn_v2_conv = _DCNv2.apply
 
 
+def deform_conv2d(input, offset, weight, bias=None, stride=(1, 1), padding=(0, 0),
+                  dilation=(1, 1), mask=None):
+    """``torchvision.ops.deform_conv2d``'s signature on these kernels, the
+    comparator the reference names: deformable groups follow from
+    ``offset.shape[1] // (2*kh*kw)`` and weight groups from ``weight.shape[1]``,
+    as torchvision infers them; ``mask=None`` is DCNv1.  Differentiable in
+    input, offset, weight, bias and mask (through :func:`dcn_v2_conv`)."""
+    kh, kw = int(weight.shape[-2]), int(weight.shape[-1])
+    if offset.dim() != 4 or offset.shape[1] % (2 * kh * kw) or offset.shape[1] == 0:
+        raise RuntimeError(f"deform_conv2d: offset channels {tuple(offset.shape)[1:2]} are not a "
+                           f"positive multiple of 2*kh*kw = {2 * kh * kw}")
+    dg = offset.shape[1] // (2 * kh * kw)
+    if mask is not None and (mask.dim() != 4 or mask.shape[1] != dg * kh * kw):
+        raise RuntimeError(f"deform_conv2d: mask has {mask.shape[1]} channels, "
+                           f"offset implies {dg * kh * kw}")
+    return dcn_v2_conv(input, weight, mask, offset, bias, stride, padding, dilation, dg)
+
+
 class _DCNv2OM(Function):
     """``dcn_v2_conv`` on the offset-and-mask predictor's raw output ``om``
     ``[B, 3*G*kh*kw, Ho, Wo]``: equal to ``dcn_v2_conv(input, weight,

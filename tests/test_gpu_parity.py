@@ -311,3 +311,33 @@ def test_channels_last_predictor_output_path():
     assert g_cl[0].is_contiguous(memory_format=torch.channels_last)
     for a, r in zip(g_cl, g_ref):
         check("grad", a, r, TOL[torch.float16])
+
+
+# --------------------------------------------------------------------------- torchvision signature
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+def test_torchvision_signature_nonsquare(dtype):
+    """dcnv2_amd.deform_conv2d (torchvision's argument order) with stride (2, 1),
+    padding (1, 2), dilation (1, 2), a 3x2 kernel, 2 deformable groups inferred
+    from the offset and 2 weight groups inferred from the weight; forward and
+    autograd gradients against the oracle."""
+    import dcnv2_amd
+    g = torch.Generator().manual_seed(11)
+    B, C, H, W, Co, kh, kw, dg, wg = 2, 32, 15, 12, 24, 3, 2, 2, 2
+    Ho, Wo = (H + 2 - (kh - 1) - 1) // 2 + 1, (W + 4 - 2 * (kw - 1) - 1) + 1
+    t = {"input": torch.randn(B, C, H, W, generator=g),
+         "weight": torch.randn(Co, C // wg, kh, kw, generator=g) * 0.2,
+         "offset": torch.randn(B, 2 * dg * kh * kw, Ho, Wo, generator=g) * 1.5,
+         "mask": torch.rand(B, dg * kh * kw, Ho, Wo, generator=g),
+         "bias": torch.randn(Co, generator=g) * 0.1,
+         "grad_output": torch.randn(B, Co, Ho, Wo, generator=g)}
+    t = {k: v.to(dtype) for k, v in t.items()}
+    dev = {k: t[k].to(DEV).requires_grad_(k != "grad_output") for k in t}
+    y = dcnv2_amd.deform_conv2d(dev["input"], dev["offset"], dev["weight"], dev["bias"],
+                                stride=(2, 1), padding=(1, 2), dilation=(1, 2), mask=dev["mask"])
+    y.backward(dev["grad_output"])
+    torch.cuda.synchronize()
+    geo = dict(stride=(2, 1), padding=(1, 2), dilation=(1, 2), deformable_groups=dg)
+    check("output", y.detach(), oracle_forward(t, geo), TOL[dtype])
+    got = [dev[k].grad for k in ("input", "offset", "mask", "weight", "bias")]
+    for name, a, r in zip(GRADS, got, oracle_backward(t, geo)):
+        check(name, a, r, TOL[dtype])

@@ -196,15 +196,14 @@ def test_module_without_gpu_raises_not_falls_back():
 
 # -- autograd plumbing with _C replaced by the CPU oracle -------------------------
 def _oracle_forward(input, weight, mask, offset, bias, sh, sw, ph, pw, dh=1, dw=1, G=1):
-    assert sh == sw and ph == pw and dh == dw
-    out = oracle.dcn_forward(input, weight, mask, offset, bias, sh, ph, dh, G)
+    out = oracle.dcn_forward(input, weight, mask, offset, bias, (sh, sw), (ph, pw), (dh, dw), G)
     return torch.from_numpy(out)
 
 
 def _oracle_backward(input, weight, mask, offset, bias, grad_output, sh, sw, ph, pw, dh=1,
                      dw=1, G=1):
     gi, goff, gm, gw, gb = oracle.dcn_backward(input, weight, mask, offset, bias, grad_output,
-                                               sh, ph, dh, G)
+                                               (sh, sw), (ph, pw), (dh, dw), G)
     gb = torch.from_numpy(gb) if bias is not None else None
     gm = torch.from_numpy(gm) if mask is not None else None
     return [torch.from_numpy(gi), torch.from_numpy(goff), gm, torch.from_numpy(gw), gb]
@@ -349,3 +348,34 @@ def test_channels_last_workspace(L):
     padded_cl, padded = desc(C=24, dtype=1, layout=1), desc(C=24, dtype=1)
     assert L.dcn2_forward_workspace_bytes(ctypes.byref(padded_cl)) == \
         L.dcn2_forward_workspace_bytes(ctypes.byref(padded))
+
+
+def test_torchvision_signature(oracle_C):
+    """deform_conv2d(input, offset, weight, bias, stride, padding, dilation,
+    mask): deformable groups from the offset's channels, weight groups from the
+    weight's shape, non-square geometry passed through, all five gradients."""
+    g = torch.Generator().manual_seed(4)
+    f64 = torch.float64
+    x = torch.randn(2, 6, 9, 8, generator=g, dtype=f64)
+    w = torch.randn(4, 3, 3, 2, generator=g, dtype=f64)        # 2 weight groups, 3x2 kernel
+    Ho, Wo = (9 + 2 * 1 - (1 * 2 + 1)) // 2 + 1, (8 + 2 * 2 - (2 * 1 + 1)) // 1 + 1
+    off = torch.randn(2, 2 * 3 * 6, Ho, Wo, generator=g, dtype=f64) * 1.3   # 3 deformable groups
+    m = torch.rand(2, 3 * 6, Ho, Wo, generator=g, dtype=f64)
+    b = torch.randn(4, generator=g, dtype=f64)
+    go = torch.randn(2, 4, Ho, Wo, generator=g, dtype=f64)
+    ours = [t.clone().requires_grad_(True) for t in (x, off, w, b, m)]
+    y = dcnv2_amd.deform_conv2d(ours[0], ours[1], ours[2], ours[3], stride=(2, 1),
+                                padding=(1, 2), dilation=(1, 2), mask=ours[4])
+    y.backward(go)
+    ref = [t.clone().requires_grad_(True) for t in (x, off, w, b, m)]
+    y_ref = deform_conv2d_gs(ref[0], ref[2], ref[1], ref[4], ref[3], stride=(2, 1),
+                             padding=(1, 2), dilation=(1, 2), deformable_groups=3)
+    y_ref.backward(go)
+    assert y.shape == (2, 4, Ho, Wo)
+    assert rel_err(y, y_ref) < 1e-12
+    for a, r in zip(ours, ref):
+        assert rel_err(a.grad, r.grad) < 1e-11
+    with pytest.raises(RuntimeError):
+        dcnv2_amd.deform_conv2d(x, off[:, :5], w)
+    with pytest.raises(RuntimeError):
+        dcnv2_amd.deform_conv2d(x, off, w, mask=m[:, :4])
