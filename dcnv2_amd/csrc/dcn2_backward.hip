@@ -1445,28 +1445,50 @@ __global__ __launch_bounds__(256) void ring_merge_kernel(float *__restrict__ gi_
 }
 
 // gi_acc [B][HW][cs] fp32 -> grad_input [B][C][HW] T; 64 pixels x 32 padded
-// channels per block, transposed through LDS.
+// channels per block, transposed through LDS.  Loads: 8 lanes per pixel, 16
+// bytes (4 channels) each.  Stores: 8 lanes per channel row, 8 consecutive
+// pixels each (one 16-byte store for 2-byte T) when vec (HW % 8 == 0 and a
+// 16-byte aligned grad_input); otherwise one element per store.
 template <typename T>
 __global__ __launch_bounds__(256) void finalize_gi_kernel(const float *__restrict__ acc,
                                                           T *__restrict__ gi, int C, int HW,
-                                                          int Cg, int Cgp, int cs) {
+                                                          int Cg, int Cgp, int cs, int vec) {
     __shared__ float tile[64][33];
     const int px0 = blockIdx.x * 64, cp0 = blockIdx.y * 32, b = blockIdx.z;
     const int tid = threadIdx.x;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int pl = (tid >> 5) + 8 * i, cl = tid & 31;
+    for (int i = 0; i < 2; ++i) {
+        const int pl = (tid >> 3) + 32 * i, c4 = (tid & 7) * 4;
         const int px = px0 + pl;
-        tile[pl][cl] = px < HW ? acc[((size_t)b * HW + px) * cs + cp0 + cl] : 0.0f;
+        f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (px < HW)  // cs % 32 == 0 and cp0 % 32 == 0: the 16-byte load stays in the pixel
+            v = *reinterpret_cast<const f32x4 *>(acc + ((size_t)b * HW + px) * cs + cp0 + c4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) tile[pl][c4 + e] = v[e];
     }
     __syncthreads();
-    const int pl = tid & 63;
+    const int cl = tid >> 3, p8 = (tid & 7) * 8;
+    const int cp = cp0 + cl, g = cp / Cgp, ci = cp - g * Cgp;
+    if (ci >= Cg) return;
+    T *row = gi + ((size_t)b * C + g * Cg + ci) * HW + px0 + p8;
+    T v[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int cl = (tid >> 6) + 4 * i;
-        const int cp = cp0 + cl, g = cp / Cgp, ci = cp - g * Cgp;
-        const int px = px0 + pl;
-        if (ci < Cg && px < HW) gi[((size_t)b * C + g * Cg + ci) * HW + px] = (T)tile[pl][cl];
+    for (int e = 0; e < 8; ++e) v[e] = (T)tile[p8 + e][cl];
+    if (vec && px0 + p8 + 8 <= HW) {
+        if constexpr (sizeof(T) == 2) {
+            *reinterpret_cast<uint4 *>(row) = __builtin_bit_cast(uint4, v);
+        } else {
+            reinterpret_cast<uint4 *>(row)[0] = make_uint4(__builtin_bit_cast(unsigned, v[0]),
+                __builtin_bit_cast(unsigned, v[1]), __builtin_bit_cast(unsigned, v[2]),
+                __builtin_bit_cast(unsigned, v[3]));
+            reinterpret_cast<uint4 *>(row)[1] = make_uint4(__builtin_bit_cast(unsigned, v[4]),
+                __builtin_bit_cast(unsigned, v[5]), __builtin_bit_cast(unsigned, v[6]),
+                __builtin_bit_cast(unsigned, v[7]));
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            if (px0 + p8 + e < HW) row[e] = v[e];
     }
 }
 
@@ -1641,8 +1663,9 @@ static hipError_t backward_t(const Geo &g, const BwdParams &p0, void *grad_input
                     p.gi_acc, (T *)grad_input, total, g.C, g.Cg, g.Cgp, g.cs);
             } else {
                 dim3 grid(ceil_div(HW, 64), g.cs / 32, g.B);
+                const int vec = HW % 8 == 0 && ((uintptr_t)grad_input & 15) == 0;
                 finalize_gi_kernel<T><<<grid, 256, 0, s>>>(p.gi_acc, (T *)grad_input, g.C, HW,
-                                                           g.Cg, g.Cgp, g.cs);
+                                                           g.Cg, g.Cgp, g.cs, vec);
             }
             if ((e = hipGetLastError()) != hipSuccess) return e;
         }
