@@ -1492,14 +1492,34 @@ __global__ __launch_bounds__(256) void finalize_gi_kernel(const float *__restric
     }
 }
 
-// gi_acc [B][HW][cs] fp32 -> channels-last grad_input [B][HW][C] T: one
-// element per thread, contiguous on both sides.
+// gi_acc [B][HW][cs] fp32 -> channels-last grad_input [B][HW][C] T, contiguous
+// on both sides.  With vec4 (C and C/G multiples of 4, grad_input aligned to 4
+// elements) each thread moves 4 channels: one 16-byte load and one 8- or
+// 16-byte store; otherwise one element per thread.
 template <typename T>
 __global__ __launch_bounds__(256) void finalize_gi_nhwc_kernel(const float *__restrict__ acc,
                                                                T *__restrict__ gi, long total,
-                                                               int C, int Cg, int Cgp, int cs) {
-    for (long idx = (long)blockIdx.x * 256 + threadIdx.x; idx < total;
-         idx += (long)gridDim.x * 256) {
+                                                               int C, int Cg, int Cgp, int cs,
+                                                               int vec4) {
+    const long stride = (long)gridDim.x * 256;
+    if (vec4) {
+        for (long i4 = (long)blockIdx.x * 256 + threadIdx.x; i4 < total / 4; i4 += stride) {
+            const long idx = i4 * 4;
+            const long px = idx / C;
+            const int c = (int)(idx - px * C);
+            const int g = c / Cg, ci = c - g * Cg;  // c..c+3 lie in one group
+            const f32x4 v = *reinterpret_cast<const f32x4 *>(acc + px * cs + g * Cgp + ci);
+            T o[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[e] = (T)v[e];
+            if constexpr (sizeof(T) == 2)
+                *reinterpret_cast<uint2 *>(gi + idx) = __builtin_bit_cast(uint2, o);
+            else
+                *reinterpret_cast<uint4 *>(gi + idx) = __builtin_bit_cast(uint4, o);
+        }
+        return;
+    }
+    for (long idx = (long)blockIdx.x * 256 + threadIdx.x; idx < total; idx += stride) {
         const long px = idx / C;
         const int c = (int)(idx - px * C);
         const int g = c / Cg, ci = c - g * Cg;
@@ -1658,9 +1678,12 @@ static hipError_t backward_t(const Geo &g, const BwdParams &p0, void *grad_input
             const int HW = g.H * g.W;
             if (g.nhwc) {
                 const long total = (long)g.B * HW * g.C;
-                const unsigned blocks = (unsigned)std::min<long>((total + 255) / 256, 16384);
+                const int vec4 = g.C % 4 == 0 && g.Cg % 4 == 0 &&
+                                 ((uintptr_t)grad_input % (4 * sizeof(T))) == 0;
+                const long work = vec4 ? total / 4 : total;
+                const unsigned blocks = (unsigned)std::min<long>((work + 255) / 256, 16384);
                 finalize_gi_nhwc_kernel<T><<<blocks, 256, 0, s>>>(
-                    p.gi_acc, (T *)grad_input, total, g.C, g.Cg, g.Cgp, g.cs);
+                    p.gi_acc, (T *)grad_input, total, g.C, g.Cg, g.Cgp, g.cs, vec4);
             } else {
                 dim3 grid(ceil_div(HW, 64), g.cs / 32, g.B);
                 const int vec = HW % 8 == 0 && ((uintptr_t)grad_input & 15) == 0;

@@ -271,7 +271,8 @@ def test_weight_groups(dtype, case):
     (torch.bfloat16, 128, 2),    # read in place, two groups
     (torch.float32, 64, 2),      # read in place (fp32 chunk is 32 channels)
     (torch.float16, 24, 2),      # padded: repacked from channels-last
-], ids=["f16_c64", "bf16_c128_dg2", "f32_c64_dg2", "f16_c24_dg2_padded"])
+    (torch.bfloat16, 18, 2),     # padded, 9 channels per group: element-wise grad_input stores
+], ids=["f16_c64", "bf16_c128_dg2", "f32_c64_dg2", "f16_c24_dg2_padded", "bf16_c18_dg2_padded"])
 def test_channels_last_input(case):
     """A channels_last input gives the same forward, bit for bit, as its NCHW
     copy (the kernels see the same channels-last data), and a backward within
