@@ -7,20 +7,27 @@ B8 C64 128x128 Cout256 3x3 fp16, plus forward+backward
 milliseconds at the same shape (config 2).
 
 A step is one forward over one batch of synthetic inputs already resident in
-HBM.  W untimed warm-up steps, then K steps bracketed by device
-synchronisation and HIP events on the stream the kernels run on.  The
-``roofline`` object covers the dominant kernel (the fused forward kernel):
-achieved = algorithmic GEMM FLOPs per launch (2*B*Cout*Hout*Wout*C*kh*kw) /
-its average duration, measured with the library's per-stage HIP events over a
-second timed loop.  ``cpu_baseline`` times the float32 CPU oracle
-(oracle/dcn_oracle.c, OpenMP) on a bounded sample of the same workload.
+HBM.  The warm-up runs W untimed steps and keeps going until at least
+--settle-ms of forward work has run (the GPU reaches its steady shader clock
+only after some tens of milliseconds of load; the count actually run is
+reported as ``warmup_steps_run``), then K steps are timed, bracketed by device
+synchronisation and HIP events on the stream the kernels run on.
+
+The ``roofline`` object covers the dominant kernel (the fused forward
+kernel): achieved = algorithmic GEMM FLOPs per launch (2*B*Cout*Hout*Wout*C*
+kh*kw) / its average duration, measured with the library's per-stage HIP
+events (recorded on the launch stream) over a second timed loop.  The other
+configurations (c2 forward+backward, c3, c4) are reported beside it with the
+same per-stage timing and fractions.  ``cpu_baseline`` times the float32 CPU
+oracle (oracle/dcn_oracle.c, OpenMP) on bounded samples of c0, c1 and c2.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 
 Profiling aids (not part of the headline line's workload): ``--mode fwd`` runs
-only the forward loops (for ``rocprofv3 --pmc`` passes), ``--copy-mib N``
-first runs one plain device-to-device copy of N MiB, the calibration kernel
-whose FETCH_SIZE/WRITE_SIZE readings scale the forward kernel's.
+only the c1 forward loops (for ``rocprofv3 --pmc`` passes), ``--mode c2``
+only the c2 forward+backward loop, ``--copy-mib N`` first runs one plain
+device-to-device copy of N MiB, the calibration kernel whose FETCH_SIZE /
+WRITE_SIZE readings scale the kernels' counters.
 """
 from __future__ import annotations
 
@@ -35,8 +42,12 @@ sys.path.insert(0, ROOT)
 
 PEAK_FP16_TFLOPS = 2500.0   # MI355X dense fp16/bf16 MFMA
 PEAK_FP32_TFLOPS = 157.3
+PEAK_HBM_GBS = 8000.0
 REF_README_TFLOPS = 90.2    # reference README.md:14 (RTX 3090, com_2buffer_cpasyc.cu)
 METRIC = "DCNv2 fwd TFLOPS (README formula) @B8 C64 128² Co256 3×3 fp16; fwd+bwd ms"
+# Forward floors of BASELINE.md section 2 (us): c3 MFMA-bound, c4 HBM/gather-bound.
+FWD_FLOOR_US = {"c1_readme_fwd": 15.4, "c3_neck_bf16_dg4": 30.7, "c4_stress_s2_d2": 5.5}
+MFMA_STAGES = ("fwd_main", "bwd_colgrad", "bwd_gradw")
 
 
 def _events_ms(fn, steps, torch):
@@ -71,6 +82,18 @@ def _median_ms(fn, steps, torch, scrub=None):
     return ts[len(ts) // 2]
 
 
+def _warm(fn, steps, settle_ms, torch):
+    """At least `steps` calls and at least `settle_ms` of wall time."""
+    n, t0 = 0, time.perf_counter()
+    while n < steps or (time.perf_counter() - t0) * 1e3 < settle_ms:
+        fn()
+        n += 1
+        if n % 16 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    return n
+
+
 def _stage_avgs(_C, names):
     out = {}
     for s in names:
@@ -95,42 +118,100 @@ def _traffic():
     return None
 
 
-def cpu_baseline(w, seconds, threads):
-    """Times the float32 oracle forward on image 0 of workload `w`."""
-    import numpy as np  # noqa: F401
-    from dcnv2_amd.workloads import make_inputs
+def _stage_report(w, stages):
+    """Per-stage ms; for the MFMA stages also TFLOP/s and fraction of the dense
+    fp16/bf16 (fp32) peak on the algorithmic GEMM FLOPs of one pass."""
+    import torch
+    peak = PEAK_FP32_TFLOPS if w.dtype == torch.float32 else PEAK_FP16_TFLOPS
+    out = {}
+    for k, ms in stages.items():
+        e = {"ms": round(ms, 5)}
+        if k in MFMA_STAGES:
+            tf = w.gemm_flops() / (ms * 1e-3) / 1e12
+            e.update(tflops=round(tf, 1), frac=round(tf / peak, 4))
+        out[k] = e
+    return out
+
+
+def _geo(w):
+    return (w.stride, w.stride, w.pad, w.pad, w.dil, w.dil, w.groups)
+
+
+def cpu_baseline(seconds, threads):
+    """The float32 oracle (C, OpenMP) on bounded samples: c1 forward on image
+    0 (the metric), c0 forward, and c2 forward + backward on image 0."""
+    import torch
+
+    from dcnv2_amd.workloads import CONFIGS, make_inputs
     from oracle import oracle
 
-    one = w.with_(B=1)
-    t = make_inputs(one, dtype=None)
-    args = [t[k].float().numpy() for k in ("input", "weight", "mask", "offset", "bias")]
-    geo = one.geometry()
-    oracle.dcn_forward(*args, **geo, precision="f32", nthreads=threads)  # warm-up
-    reps, t0 = 0, time.perf_counter()
-    while True:
-        oracle.dcn_forward(*args, **geo, precision="f32", nthreads=threads)
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= seconds or reps >= 200:
-            break
-    return {
-        "value": one.readme_flops() * reps / el / 1e12,
+    def timed(fn, budget):
+        fn()  # warm-up
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            fn()
+            reps += 1
+            el = time.perf_counter() - t0
+            if el >= budget or reps >= 500:
+                return reps, el
+
+    def arrays(w):
+        t = make_inputs(w, dtype=torch.float32, with_grad=True)
+        return {k: v.numpy() for k, v in t.items()}
+
+    names = ("input", "weight", "mask", "offset", "bias")
+    res = {}
+    # c1 forward, image 0 (the headline's unit: README-formula TFLOPS)
+    c1 = CONFIGS[1].with_(B=1)
+    a = arrays(c1)
+    r1, e1 = timed(lambda: oracle.dcn_forward(*(a[k] for k in names), **c1.geometry(),
+                                              precision="f32", nthreads=threads), seconds * 0.5)
+    # c0 forward (the CPU plumbing workload)
+    c0 = CONFIGS[0]
+    a0 = arrays(c0)
+    r0, e0 = timed(lambda: oracle.dcn_forward(*(a0[k] for k in names), **c0.geometry(),
+                                              precision="f32", nthreads=threads), seconds * 0.1)
+    # c2 forward + backward, image 0
+    c2 = CONFIGS[2].with_(B=1)
+    a2 = arrays(c2)
+
+    def fb():
+        oracle.dcn_forward(*(a2[k] for k in names), **c2.geometry(), precision="f32",
+                           nthreads=threads)
+        oracle.dcn_backward(*(a2[k] for k in names), a2["grad_output"], **c2.geometry(),
+                            precision="f32", nthreads=threads)
+
+    r2, e2 = timed(fb, seconds * 0.4)
+    res = {
+        "value": c1.readme_flops() * r1 / e1 / 1e12,
         "unit": "TFLOPS (README formula)",
         "cores": threads,
         "kind": "port",
-        "sample": f"{reps} x forward of image 0 of {w.name} (B=1 of {w.B}), float32, "
-                  f"{el:.1f} s, C oracle with OpenMP",
+        "sample": f"{r1} x forward of image 0 of c1_readme_fwd (B=1 of 8), float32, {e1:.1f} s; "
+                  f"{r0} x c0 forward, {e0:.1f} s; {r2} x forward+backward of image 0 of "
+                  f"c2_readme_fwd_bwd, {e2:.1f} s; C oracle with OpenMP",
+        "c1_fwd_ms_full_batch": round(e1 / r1 * 1e3 * CONFIGS[1].B, 3),
+        "c0_fwd_ms": round(e0 / r0 * 1e3, 4),
+        "c2_fwd_bwd_ms_full_batch": round(e2 / r2 * 1e3 * CONFIGS[2].B, 3),
+        "os_cpu_count": os.cpu_count(),
+        "affinity_cpus": len(os.sched_getaffinity(0)),
+        "torch_num_threads": torch.get_num_threads(),
+        "threads_note": "OpenMP threads of the oracle = OMP_NUM_THREADS when set (the GPU "
+                        "box's CPU share per GPU), else the affinity mask; full-batch ms are "
+                        "image 0 times the batch",
     }
+    return res
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
-    ap.add_argument("--warmup", type=int, default=500)
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--settle-ms", type=float, default=400.0)
+    ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--mode", choices=("full", "fwd"), default="full")
+    ap.add_argument("--mode", choices=("full", "fwd", "c2"), default="full")
     ap.add_argument("--copy-mib", type=int, default=0)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -141,22 +222,25 @@ def main():
     import torch
 
     from dcnv2_amd import _C
-    from dcnv2_amd.workloads import CONFIGS
+    from dcnv2_amd.workloads import CONFIGS, make_inputs
 
     dev = torch.device("cuda:0")
-    fwd_w, fb_w = CONFIGS[1], CONFIGS[2]
+    c1, c2 = CONFIGS[1], CONFIGS[2]
 
     def load(w):
-        from dcnv2_amd.workloads import make_inputs
-        return {k: v.to(dev) for k, v in make_inputs(w).items()}
+        return {k: v.to(dev) for k, v in make_inputs(w, with_grad=True).items()}
 
-    t = load(fwd_w)
-    geo = (fwd_w.stride, fwd_w.stride, fwd_w.pad, fwd_w.pad, fwd_w.dil, fwd_w.dil,
-           fwd_w.groups)
-    fargs = (t["input"], t["weight"], t["mask"], t["offset"], t["bias"])
+    def fwd_fn(w, t):
+        args5 = (t["input"], t["weight"], t["mask"], t["offset"], t["bias"])
+        return lambda: _C.dcn_v2_forward(*args5, *_geo(w))
 
-    def fwd():
-        return _C.dcn_v2_forward(*fargs, *geo)
+    def fwd_bwd_fn(w, t):
+        args5 = (t["input"], t["weight"], t["mask"], t["offset"], t["bias"])
+
+        def f():
+            _C.dcn_v2_forward(*args5, *_geo(w))
+            return _C.dcn_v2_backward(*args5, t["grad_output"], *_geo(w))
+        return f
 
     if args.copy_mib:
         n = args.copy_mib << 20
@@ -166,17 +250,25 @@ def main():
         torch.cuda.synchronize()
         del src, dst
 
-    for _ in range(args.warmup):
-        fwd()
+    if args.mode == "c2":
+        t2 = load(c2)
+        f = fwd_bwd_fn(c2, t2)
+        _warm(f, args.warmup, args.settle_ms, torch)
+        ms = _events_ms(f, args.steps, torch)
+        print(json.dumps({"mode": "c2", "fwd_bwd_ms": round(ms, 5)}), flush=True)
+        return
+
+    t1 = load(c1)
+    fwd = fwd_fn(c1, t1)
+    warm_run = _warm(fwd, args.warmup, args.settle_ms, torch)
     ms = _events_ms(fwd, args.steps, torch)
-    value = fwd_w.readme_flops() / (ms * 1e-3) / 1e12
+    value = c1.readme_flops() / (ms * 1e-3) / 1e12
     # per-call medians: hot (back to back) and cold (512 MiB scrub before each call)
     hot_med = _median_ms(fwd, args.steps, torch)
     scrub = torch.zeros(128 << 20, dtype=torch.float32, device=dev)
     cold_med = _median_ms(fwd, max(10, args.steps // 4), torch, scrub)
     del scrub
-    for _ in range(50):
-        fwd()
+    _warm(fwd, 20, 100.0, torch)
 
     # second loop with per-stage events for the kernel roofline
     _C.profile_enable(True)
@@ -185,31 +277,13 @@ def main():
     fstages = _stage_avgs(_C, ("fwd_pack", "fwd_main"))
     _C.profile_enable(False)
     kern_ms = fstages["fwd_main"]
-    achieved = fwd_w.gemm_flops() / (kern_ms * 1e-3) / 1e12
+    achieved = c1.gemm_flops() / (kern_ms * 1e-3) / 1e12
 
     if args.mode == "fwd":
         print(json.dumps({"mode": "fwd", "ms_per_step": round(ms, 5),
                           "kernel_ms": round(kern_ms, 5), "fwd_hot_median_ms": round(hot_med, 5),
                           "fwd_cold_median_ms": round(cold_med, 5)}), flush=True)
         return
-
-    # forward + backward at the same shape (config 2)
-    t2 = load(fb_w)
-    b_args = (t2["input"], t2["weight"], t2["mask"], t2["offset"], t2["bias"])
-
-    def fwd_bwd():
-        _C.dcn_v2_forward(*b_args, *geo)
-        return _C.dcn_v2_backward(*b_args, t2["grad_output"], *geo)
-
-    fb_steps = max(5, args.steps // 4)
-    for _ in range(max(2, min(50, args.warmup // 4))):
-        fwd_bwd()
-    fb_ms = _events_ms(fwd_bwd, fb_steps, torch)
-    _C.profile_enable(True)
-    _stage_avgs(_C, _C.STAGES)
-    _events_ms(fwd_bwd, fb_steps, torch)
-    bstages = _stage_avgs(_C, _C.STAGES)
-    _C.profile_enable(False)
 
     result = {
         "metric": METRIC,
@@ -218,24 +292,22 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "warmup_steps_run": warm_run,
         "ms_per_step": round(ms, 5),
         "higher_is_better": True,
         "scaling": "weak",
-        "vs_baseline": round(value / REF_README_TFLOPS, 3),
-        "baseline_note": "90.2 README-formula TFLOPS of com_2buffer_cpasyc.cu on an RTX 3090 "
-                         "(README.md:14); different hardware",
+        "vs_baseline": None,
+        "baseline_note": "no published MI355X number; the reference README's 90.2 README-formula "
+                         "TFLOPS (com_2buffer_cpasyc.cu, RTX 3090, README.md:14) is other "
+                         "hardware",
         "dtype": "fp16",
         "data": "synthetic (seeded, BASELINE.json config distributions; inputs resident in HBM)",
         "config": {"workload": "c1_readme_fwd: B8 C64 H128 W128 Cout256 3x3 s1 p1 d1 dg1 fp16, "
-                               "forward", "global_batch": fwd_w.B, "parallelism": "single GPU"},
-        "fwd_real_tflops": round(fwd_w.gemm_flops() / (ms * 1e-3) / 1e12, 2),
+                               "forward", "global_batch": c1.B, "parallelism": "single GPU"},
+        "fwd_real_tflops": round(c1.gemm_flops() / (ms * 1e-3) / 1e12, 2),
         "fwd_hot_median_ms": round(hot_med, 5),
         "fwd_cold_median_ms": round(cold_med, 5),
         "fwd_cold_note": "median per call after a 512 MiB write that evicts L2 and MALL",
-        "fwd_bwd_ms": round(fb_ms, 5),
-        "fwd_bwd_workload": "c2_readme_fwd_bwd: same shape, forward + all five gradients, fp16",
-        "stages_ms": {"forward": {k: round(v, 5) for k, v in fstages.items()},
-                      "forward_backward": {k: round(v, 5) for k, v in bstages.items()}},
         "roofline": {
             "bound": "mfma",
             "kernel": "dcn2_fwd_ws_kernel (fused bilinear sampling + 32x32x16 f16 MFMA)",
@@ -244,35 +316,81 @@ def main():
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_FP16_TFLOPS, 4),
             "traffic": _traffic(),
-            "algorithmic_flops_per_launch": fwd_w.gemm_flops(),
+            "algorithmic_flops_per_launch": c1.gemm_flops(),
             "kernel_ms": round(kern_ms, 5),
         },
+        "stages_ms": {"c1_forward": {k: round(v, 5) for k, v in fstages.items()}},
     }
-    # The same two workloads with a channels_last input: the kernels read it in
+    del t1
+
+    # forward + backward at the headline shape (c2), and c3 / c4 (forward and
+    # forward + backward each), with per-stage times and MFMA fractions
+    others = {}
+    for w in (c2, CONFIGS[3], CONFIGS[4]):
+        t = load(w)
+        e = {"workload": f"{w.name}: B{w.B} C{w.C} H{w.H} W{w.W} Cout{w.Cout} {w.k}x{w.k} "
+                         f"s{w.stride} p{w.pad} d{w.dil} dg{w.groups} "
+                         f"{str(w.dtype).split('.')[-1]}"}
+        steps = max(5, args.steps // 4)
+        if w is not c2:
+            f = fwd_fn(w, t)
+            _warm(f, 10, 100.0, torch)
+            fms = _events_ms(f, steps, torch)
+            _C.profile_enable(True)
+            _stage_avgs(_C, _C.STAGES)
+            _events_ms(f, steps, torch)
+            st = _stage_avgs(_C, ("fwd_pack", "fwd_main"))
+            _C.profile_enable(False)
+            e["fwd_ms"] = round(fms, 5)
+            e["fwd_readme_tflops"] = round(w.readme_flops() / (fms * 1e-3) / 1e12, 1)
+            e["fwd_real_tflops"] = round(w.gemm_flops() / (fms * 1e-3) / 1e12, 1)
+            e["fwd_stages"] = _stage_report(w, st)
+            floor = FWD_FLOOR_US.get(w.name)
+            if floor:
+                e["fwd_kernel_floor_us"] = floor
+                e["fwd_kernel_frac_of_floor"] = round(floor / (st["fwd_main"] * 1e3), 4)
+        f = fwd_bwd_fn(w, t)
+        _warm(f, 5, 100.0, torch)
+        fbms = _events_ms(f, steps, torch)
+        _C.profile_enable(True)
+        _stage_avgs(_C, _C.STAGES)
+        _events_ms(f, steps, torch)
+        st = _stage_avgs(_C, _C.STAGES)
+        _C.profile_enable(False)
+        e["fwd_bwd_ms"] = round(fbms, 5)
+        e["fwd_bwd_real_tflops"] = round(3 * w.gemm_flops() / (fbms * 1e-3) / 1e12, 1)
+        e["fwd_bwd_stages"] = _stage_report(w, st)
+        others[w.name] = e
+        del t, f
+        torch.cuda.empty_cache()
+    result["fwd_bwd_ms"] = others[c2.name]["fwd_bwd_ms"]
+    result["configs"] = others
+
+    # The c1/c2 workloads with a channels_last input: the kernels read it in
     # place (C = 64 needs no channel padding), so the repacking pass drops out,
     # and grad_input is written channels-last directly.
-    x_cl = t["input"].to(memory_format=torch.channels_last)
-    x2_cl = t2["input"].to(memory_format=torch.channels_last)
+    t2 = load(c2)
+    x_cl = t2["input"].to(memory_format=torch.channels_last)
+    b_args = (t2["weight"], t2["mask"], t2["offset"], t2["bias"])
 
     def fwd_cl():
-        return _C.dcn_v2_forward(x_cl, *fargs[1:], *geo)
+        return _C.dcn_v2_forward(x_cl, *b_args, *_geo(c1))
 
     def fwd_bwd_cl():
-        _C.dcn_v2_forward(x2_cl, *b_args[1:], *geo)
-        return _C.dcn_v2_backward(x2_cl, *b_args[1:], t2["grad_output"], *geo)
+        _C.dcn_v2_forward(x_cl, *b_args, *_geo(c2))
+        return _C.dcn_v2_backward(x_cl, *b_args, t2["grad_output"], *_geo(c2))
 
-    for _ in range(50):
-        fwd_cl()
+    fb_steps = max(5, args.steps // 4)
+    _warm(fwd_cl, 20, 100.0, torch)
     cl_fwd_ms = _events_ms(fwd_cl, args.steps, torch)
-    for _ in range(5):
-        fwd_bwd_cl()
+    _warm(fwd_bwd_cl, 5, 50.0, torch)
     result["channels_last_input"] = {
         "fwd_ms": round(cl_fwd_ms, 5),
-        "fwd_readme_tflops": round(fwd_w.readme_flops() / (cl_fwd_ms * 1e-3) / 1e12, 2),
+        "fwd_readme_tflops": round(c1.readme_flops() / (cl_fwd_ms * 1e-3) / 1e12, 2),
         "fwd_bwd_ms": round(_events_ms(fwd_bwd_cl, fb_steps, torch), 5),
         "note": "input (and grad_input) channels_last, read in place; output NCHW",
     }
-    del x_cl, x2_cl
+    del x_cl
 
     # The DCN module (offset/mask predictor conv + operator) at the same shape,
     # forward + backward: the fused path hands the predictor output to the
@@ -283,7 +401,7 @@ def main():
     x = t2["input"].clone().requires_grad_(True)
     for fused in (True, False):
         torch.manual_seed(0)
-        mod = DCN(fb_w.C, fb_w.Cout, fb_w.k, fb_w.stride, fb_w.pad, fb_w.dil, fb_w.groups,
+        mod = DCN(c2.C, c2.Cout, c2.k, c2.stride, c2.pad, c2.dil, c2.groups,
                   fused_offset_mask=fused).to(dev).half()
         with torch.no_grad():
             mod.conv_offset_mask.weight.normal_(0.0, 0.01)
@@ -292,28 +410,15 @@ def main():
             y = mod(x)
             y.backward(t2["grad_output"])
 
-        for _ in range(5):
-            module_step()
+        _warm(module_step, 5, 50.0, torch)
         mod_ms["fused" if fused else "separate"] = round(_events_ms(module_step, fb_steps, torch), 5)
     result["dcn_module_fwd_bwd_ms"] = dict(mod_ms, workload="DCN module (predictor conv + "
                                            "operator), c2 shape, fp16, forward + backward")
-
-    # Attainable dense fp16 MFMA rate of this GPU (probe in the forward kernel's
-    # issue pattern): the shader clock drops under MFMA work on toggling data.
-    try:
-        from dcnv2_amd.probe import mfma_ceiling
-        mc = mfma_ceiling()
-        result["mfma_ceiling"] = {
-            "unit": "TFLOP/s", "zero_operands": mc["zero"], "normal_operands": mc["normal"],
-            "fwd_kernel_frac_of_normal": round(achieved / mc["normal"]["tflops"], 4),
-            "note": "32x32x16 f16 MFMA, 4 MFMA waves per CU with a barrier per 32 MFMAs; "
-                    "N(0,1) operands lower the shader clock (power limit)",
-        }
-    except (OSError, RuntimeError) as exc:
-        result["mfma_ceiling"] = {"error": str(exc)}
+    del t2, x
     if not args.no_cpu:
-        threads = max(1, min(16, os.cpu_count() or 1))
-        result["cpu_baseline"] = cpu_baseline(fwd_w, args.cpu_seconds, threads)
+        omp = os.environ.get("OMP_NUM_THREADS", "")
+        threads = int(omp) if omp.isdigit() and int(omp) > 0 else len(os.sched_getaffinity(0))
+        result["cpu_baseline"] = cpu_baseline(args.cpu_seconds, threads)
     else:
         result["cpu_baseline"] = None
     print(json.dumps(result), flush=True)

@@ -1,8 +1,7 @@
 """Builds libdcnv2_amd.so (the C-ABI library with the gfx950 kernels) in-tree.
 
 Every source under csrc/ is compiled by hipcc for gfx950 only and linked into
-dcnv2_amd/lib/libdcnv2_amd.so; probe/mfma_ceiling.hip (a measurement tool,
-not part of the C ABI) goes into dcnv2_amd/lib/libdcn2_probe.so.  Packed-FP32 instructions are disabled for all
+dcnv2_amd/lib/libdcnv2_amd.so.  Packed-FP32 instructions are disabled for all
 device code (-Xclang -target-feature -Xclang -packed-fp32-ops).
 Usage: python -m dcnv2_amd.build   (or __graft_entry__.build()).
 """
@@ -19,8 +18,6 @@ CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(ROOT, "_build")
 LIBDIR = os.path.join(HERE, "lib")
 LIB = os.path.join(LIBDIR, "libdcnv2_amd.so")
-PROBE_SRC = os.path.join(HERE, "probe", "mfma_ceiling.hip")
-PROBE_LIB = os.path.join(LIBDIR, "libdcn2_probe.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
@@ -51,13 +48,6 @@ def build(verbose: bool = True) -> str:
     if r.returncode != 0:
         raise RuntimeError("link failed:\n" + r.stdout + r.stderr)
     os.replace(tmp, LIB)
-    # the measurement probe bench.py reports beside the roofline (own library)
-    pobj = _compile(PROBE_SRC)
-    r = subprocess.run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-o", PROBE_LIB + ".tmp", pobj],
-                       capture_output=True, text=True)
-    if r.returncode != 0:
-        raise RuntimeError("probe link failed:\n" + r.stdout + r.stderr)
-    os.replace(PROBE_LIB + ".tmp", PROBE_LIB)
     if verbose:
         print(f"built {LIB}")
     return LIB

@@ -20,7 +20,7 @@ namespace dcn2 {
 
 static thread_local std::string g_last_error;
 
-static int fail(int code, const char *fmt, ...) {
+int fail(int code, const char *fmt, ...) {
     char buf[512];
     va_list ap;
     va_start(ap, fmt);
@@ -33,7 +33,7 @@ static int fail(int code, const char *fmt, ...) {
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 // Validates `d` and derives the packing geometry.  Returns DCN2_OK or an error.
-static int make_geo(const dcn2_desc *d, Geo &g) {
+int make_geo(const dcn2_desc *d, Geo &g) {
     if (!d) return fail(DCN2_EINVAL, "dcn2: null descriptor");
     g.B = d->batch;
     g.C = d->in_channels;
@@ -97,6 +97,12 @@ static int make_geo(const dcn2_desc *d, Geo &g) {
         (long long)g.B * g.G * g.KK * g.Ho * g.Wo >= lim || g.H > 32767 || g.W > 32767)
         return fail(DCN2_ERANGE, "dcn2: problem exceeds the 32-bit per-image index range");
     g.Kp = (int)Kp;
+    {
+        const GatherGeo gg = gather_geometry(g);
+        if (gg.batch_bytes >= gg.max_batch_bytes)
+            return fail(DCN2_ERANGE, "dcn2: %d channels per deformable group exceed the "
+                        "grad_input gather's row range", g.Cg);
+    }
     // separate offset and mask tensors (dcn2_forward / dcn2_backward)
     g.off_bs = 2LL * g.G * g.KK * g.N;
     g.msk_bs = (long long)g.G * g.KK * g.N;
@@ -147,11 +153,15 @@ BwdWorkspace bwd_workspace(const Geo &g) {
     o += align256((size_t)g.Mp * sizeof(float));
     const GatherGeo gg = gather_geometry(g);
     w.cgm = o;
-    o += align256((size_t)gg.nbuckets * gg.cap * g.Cgp * g.esz);
+    o += align256((size_t)gg.rows * g.Cgp * gg.row_esz);
     w.rec = o;
-    o += align256((size_t)gg.nbuckets * gg.cap * 16);
-    w.cnt = o;
+    o += align256((size_t)gg.rows * 16);
+    w.bcnt = o;
     o += align256((size_t)gg.nbuckets * sizeof(int) + 16);
+    w.bstart = o;
+    o += align256((size_t)(gg.nbuckets + 1) * sizeof(int));
+    w.bcur = o;
+    o += align256((size_t)gg.nbuckets * sizeof(int));
     w.sidx = o;
     o += align256((size_t)g.B * g.G * g.KK * g.N * sizeof(int));
     w.ring = o;
@@ -166,9 +176,9 @@ static int check_launch(hipError_t e, const char *what) {
     return DCN2_OK;
 }
 
-static int forward_impl(const Geo &g, const void *input, const void *weight, const void *mask,
-                        const void *offset, const void *bias, void *output, void *workspace,
-                        size_t workspace_bytes, void *stream) {
+int forward_impl(const Geo &g, const void *input, const void *weight, const void *mask,
+                 const void *offset, const void *bias, void *output, void *workspace,
+                 size_t workspace_bytes, void *stream) {
     int rc = DCN2_OK;
     if (g.B > 0 && (!input || !offset || !output))
         return fail(DCN2_EINVAL, "dcn2_forward: null input/offset/output pointer");
@@ -229,7 +239,8 @@ static int backward_impl(const Geo &g, const void *input, const void *weight, co
                                         grad_input, grad_offset, grad_mask, grad_weight,
                                         grad_bias, (float *)(base + ws.gi_acc),
                                         (float *)(base + ws.gw_acc), (float *)(base + ws.gb_acc),
-                                        base + ws.cgm, base + ws.rec, (int *)(base + ws.cnt),
+                                        base + ws.cgm, base + ws.rec, (int *)(base + ws.bcnt),
+                                        (int *)(base + ws.bstart), (int *)(base + ws.bcur),
                                         (int *)(base + ws.sidx), (float *)(base + ws.ring), s),
                         "backward");
 }

@@ -39,12 +39,17 @@ struct BwdParams {
     int B, H, W, Cout, kh, kw, sh, sw, ph, pw, dh, dw, G, Cg, Cgp, Ho, Wo, Kp, Mp;
     int tiles_per_img, splits;
     int go_vec;  // grad_output rows can be read with 16-byte loads (N % 8 == 0, aligned base)
-    // grad_input gather: cell-tile buckets (see dcn2_gi_gather_kernel)
-    void *cgm;          // [nbuckets*cap][Cgp] masked column gradient rows, call dtype
-    int4 *rec;          // [nbuckets][cap] sample records
-    int *cnt;           // [nbuckets] records appended per bucket
-    int *sidx;          // [B][G*KK][N] bucket-slot row of each sample; -1 no corner, -2 bucket full
-    int ntx, nty, cap;  // cell tiles per row / column, bucket capacity
+    // grad_input gather: cell-tile buckets (see dcn2_gi_gather_kernel).  The
+    // rows of all buckets are packed back to back, bucket k owning rows
+    // [bstart[k], bstart[k+1]); there are at most B*G*KK*N of them (one per
+    // sample), so the storage is sized exactly and no bucket can overflow.
+    void *cgm;          // [rows][Cgp] masked column gradient rows, call dtype
+    int4 *rec;          // [rows] sample records, in bucket order
+    int *bcnt;          // [nbuckets] samples per bucket (count pass)
+    int *bstart;        // [nbuckets + 1] first row of each bucket (exclusive scan of bcnt)
+    int *bcur;          // [nbuckets] next free row of each bucket (place pass)
+    int *sidx;          // [B][G*KK][N] bucket row of each sample; -1 no corner inside
+    int ntx, nty;       // cell tiles per row / column
     float *ring;        // [nbuckets][kRing][Cgp] grad_input sums of each window's border ring
     // offset / mask (and grad_offset / grad_mask) elements between images, and
     // whether the mask buffer holds logits (see mask_value; grad_mask is then
@@ -52,6 +57,14 @@ struct BwdParams {
     long long off_bs, msk_bs;
     int msk_logit;
 };
+
+// Element type of the masked column-gradient rows the column-gradient kernel
+// hands to the grad_input gather: fp32 for bf16, whose 8-bit mantissa would
+// add a rounding that the reference's fp32 col2im (com.cu:553-609) does not
+// have, and the call type otherwise.
+template <typename T> struct RowOf { typedef T type; };
+template <> struct RowOf<bf16> { typedef float type; };
+constexpr int row_elem_bytes(int dtype) { return dtype == DCN2_F32 || dtype == DCN2_BF16 ? 4 : 2; }
 
 // Buffer offset at or past one image's gO bytes (a load there reads 0); the
 // kernels that read gO through it require Cout*N*sizeof(T) <= kGoOutOfRange.
@@ -75,12 +88,11 @@ __device__ __forceinline__ int ring_index(int py, int px) {
 
 // Per-pixel sampling record written by the reduction phase for the
 // grad_input phase.  mode 0: no corner inside the image (nothing to add);
-// 1: appended to its cell-tile bucket (write the masked column-gradient row);
-// 2: bucket full (add to grad_input directly with atomics).
+// 1: placed in its cell-tile bucket (write the masked column-gradient row).
 struct Desc {
     int off[4];
     float w[4];  // masked bilinear weight of each corner, 0 outside the image
-    int sidx;    // row of the masked column gradient: bucket*cap + slot
+    int sidx;    // bucket row of the masked column gradient
     int mode;
     int pad0, pad1;
     // the last 16 bytes (DescFrac) are what the corner-sum reduction reads
@@ -95,10 +107,10 @@ struct DescFrac {
 };
 static_assert(sizeof(Desc) == 64 && offsetof(Desc, m) % 16 == 0, "Desc is four 16-byte pieces");
 
-// Appends this lane's record to bucket `key` when `want`; wavefront-aggregated:
-// one atomic per distinct bucket among the wave's lanes.  Returns the slot or
-// -1 when the bucket is full (or !want).
-__device__ __forceinline__ int bucket_append(bool want, int key, int *cnt, int cap) {
+// Claims one entry of counter `key` for this lane when `want`;
+// wavefront-aggregated: one atomic per distinct key among the wave's lanes.
+// Returns the counter's value before this lane's claim, or -1 when !want.
+__device__ __forceinline__ int bucket_append(bool want, int key, int *ctr) {
     const int lane = threadIdx.x & 63;
     unsigned long long active = __ballot(want);
     int slot = -1;
@@ -107,12 +119,9 @@ __device__ __forceinline__ int bucket_append(bool want, int key, int *cnt, int c
         const int lkey = __shfl(key, leader, 64);
         const unsigned long long same = __ballot(want && key == lkey) & active;
         int base = 0;
-        if (lane == leader) base = atomicAdd(cnt + lkey, __popcll(same));
+        if (lane == leader) base = atomicAdd(ctr + lkey, __popcll(same));
         base = __shfl(base, leader, 64);
-        if ((same >> lane) & 1ull) {
-            const int rank = __popcll(same & ((1ull << lane) - 1ull));
-            slot = base + rank < cap ? base + rank : -1;
-        }
+        if ((same >> lane) & 1ull) slot = base + __popcll(same & ((1ull << lane) - 1ull));
         active &= ~same;
     }
     return slot;
@@ -140,19 +149,26 @@ __device__ __forceinline__ float shfl_xor_f(float v, int mask) {
 }
 
 // ---------------------------------------------------------------------------
-// Bucket pre-pass of the grad_input hand-off.  For every sample (image,
-// offset plane g*KK + tap, output pixel) with a corner inside the image it
-// appends the record to the bucket of its cell tile and writes the sample's
-// bucket-slot row to sidx (-1: no corner inside, -2: bucket full), so the
-// column-gradient kernel only reads one int per sample.  The sample position
-// is computed exactly as the column-gradient kernel computes it.
+// Bucket pre-passes of the grad_input hand-off.  Every sample (image, offset
+// plane g*KK + tap, output pixel) with a corner inside the image belongs to
+// the bucket of its cell tile.  Three launches place the samples in exactly
+// sized buckets:
+//   count  samples per bucket -> bcnt;
+//   scan   bstart = exclusive prefix sum of bcnt (and bcur = bstart);
+//   place  each sample claims a row of its bucket from bcur, writes its
+//          record there and its row to sidx (-1: no corner inside),
+// so the column-gradient kernel only reads one int per sample, and the
+// buckets hold any distribution of samples (a learned offset field that pulls
+// every sample into one tile included) in at most B*G*KK*N rows.  Count and
+// place compute the sample position exactly as the column-gradient kernel
+// does, so both passes see the same buckets.
 //
 // A workgroup takes kBucketSPT*256 consecutive pixels of one offset plane and
 // counts its samples per cell tile in LDS (the LDS atomic's return value is
 // the sample's rank inside the workgroup); then one global atomic per
-// (workgroup, cell tile) claims a range of the bucket.  Claiming slots with
-// one global atomic per wave instead serialises thousands of atomics on each
-// bucket counter.
+// (workgroup, cell tile) adds its count (count pass) or claims a range of the
+// bucket's rows (place pass).  Claiming rows with one global atomic per wave
+// instead serialises thousands of atomics on each bucket counter.
 constexpr int kBucketTab = 16384;  // cell tiles of one image the LDS table holds
 constexpr int kBucketSPT = 16;     // samples per thread
 
@@ -192,6 +208,20 @@ __device__ __forceinline__ BucketSample bucket_sample(const BwdParams &p, const 
     return r;
 }
 
+// Record of a placed sample: its floor corner (y0 in the low, x0 in the high
+// 16 bits, both >= -2) and the bilinear fractions.  Row `row` of the bucket
+// storage is written only if it lies inside the bucket's range, so the
+// storage is never written out of bounds, whatever the counts.
+__device__ __forceinline__ int place_sample(const BwdParams &p, const BucketSample &bs, int key,
+                                            int row) {
+    if (row < 0 || row >= p.bstart[key + 1]) return -1;
+    p.rec[row] = make_int4(row, (bs.sp.y0 & 0xffff) | (int)((unsigned)bs.sp.x0 << 16),
+                           __float_as_int(bs.sp.ly), __float_as_int(bs.sp.lx));
+    return row;
+}
+
+// PLACE = false: the count pass (bcnt); true: the place pass (bcur, rec, sidx).
+template <bool PLACE>
 __global__ __launch_bounds__(256) void dcn2_bucket_kernel(const BwdParams p, const void *offset_v,
                                                           int esz_is_f32, int is_bf16) {
     __shared__ int tab[kBucketTab];
@@ -209,35 +239,31 @@ __global__ __launch_bounds__(256) void dcn2_bucket_kernel(const BwdParams p, con
         rank[k] = bs.any ? atomicAdd(tab + bs.tkey, 1) : -1;
     }
     __syncthreads();
-    int *cnt = p.cnt + (size_t)(b * p.G + g) * ntile;
+    int *ctr = (PLACE ? p.bcur : p.bcnt) + (size_t)(b * p.G + g) * ntile;
     for (int i = tid; i < ntile; i += 256) {
         const int c = tab[i];
-        if (c) tab[i] = atomicAdd(cnt + i, c);  // first slot of this workgroup's range
+        if (c) tab[i] = atomicAdd(ctr + i, c);  // first row of this workgroup's range
     }
-    __syncthreads();
+    if constexpr (PLACE) {
+        __syncthreads();
 #pragma unroll
-    for (int k = 0; k < kBucketSPT; ++k) {
-        const int n = n_base + k * 256 + tid;
-        if (n >= N) continue;
-        int sx = -1;
-        if (rank[k] >= 0) {
-            const BucketSample bs = bucket_sample(p, offset_v, esz_is_f32, is_bf16, b, plane, n);
-            const int key = (b * p.G + g) * ntile + bs.tkey;
-            const int slot = tab[bs.tkey] + rank[k];
-            if (slot < p.cap) {
-                sx = key * p.cap + slot;
-                p.rec[sx] = make_int4(sx, (bs.sp.y0 & 0xffff) | (int)((unsigned)bs.sp.x0 << 16),
-                                      __float_as_int(bs.sp.ly), __float_as_int(bs.sp.lx));
-            } else {
-                sx = -2;
+        for (int k = 0; k < kBucketSPT; ++k) {
+            const int n = n_base + k * 256 + tid;
+            if (n >= N) continue;
+            int sx = -1;
+            if (rank[k] >= 0) {
+                const BucketSample bs = bucket_sample(p, offset_v, esz_is_f32, is_bf16, b, plane, n);
+                const int key = (b * p.G + g) * ntile + bs.tkey;
+                sx = place_sample(p, bs, key, tab[bs.tkey] + rank[k]);
             }
+            p.sidx[((size_t)b * p.G * KK + plane) * N + n] = sx;
         }
-        p.sidx[((size_t)b * p.G * KK + plane) * N + n] = sx;
     }
 }
 
 // The same with one global atomic per (wave, bucket), for images with more
 // cell tiles than kBucketTab.
+template <bool PLACE>
 __global__ __launch_bounds__(256) void dcn2_bucket_global_kernel(const BwdParams p,
                                                                  const void *offset_v,
                                                                  int esz_is_f32, int is_bf16) {
@@ -246,17 +272,45 @@ __global__ __launch_bounds__(256) void dcn2_bucket_global_kernel(const BwdParams
     const int plane = blockIdx.y, b = blockIdx.z, g = plane / KK;
     const BucketSample bs = bucket_sample(p, offset_v, esz_is_f32, is_bf16, b, plane, n);
     const int key = (b * p.G + g) * p.nty * p.ntx + bs.tkey;
-    const int slot = bucket_append(bs.any, key, p.cnt, p.cap);
-    const int row = key * p.cap + slot;
-    if (slot >= 0)
-        p.rec[row] = make_int4(row, (bs.sp.y0 & 0xffff) | (int)((unsigned)bs.sp.x0 << 16),
-                               __float_as_int(bs.sp.ly), __float_as_int(bs.sp.lx));
-    if (n < N) p.sidx[((size_t)b * p.G * KK + plane) * N + n] = !bs.any ? -1 : (slot >= 0 ? row : -2);
+    const int row = bucket_append(bs.any, key, PLACE ? p.bcur : p.bcnt);
+    if constexpr (PLACE) {
+        const int sx = bs.any ? place_sample(p, bs, key, row) : -1;
+        if (n < N) p.sidx[((size_t)b * p.G * KK + plane) * N + n] = sx;
+    }
+}
+
+// bstart[i] = bcnt[0] + ... + bcnt[i-1] for i = 0..n, and bcur = bstart:
+// one workgroup; thread t scans a contiguous run of ceil(n / 1024) counts.
+__global__ __launch_bounds__(1024) void dcn2_bucket_scan_kernel(const int *__restrict__ bcnt,
+                                                                int *__restrict__ bstart,
+                                                                int *__restrict__ bcur, int n) {
+    __shared__ int wsum[16];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int per = (n + 1023) / 1024;
+    const int i0 = min(tid * per, n), i1 = min(i0 + per, n);
+    int s = 0;
+    for (int i = i0; i < i1; ++i) s += bcnt[i];
+    int incl = s;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int o = __shfl_up(incl, d, 64);
+        if (lane >= d) incl += o;
+    }
+    if (lane == 63) wsum[wave] = incl;
+    __syncthreads();
+    int run = incl - s;
+    for (int w = 0; w < wave; ++w) run += wsum[w];
+    for (int i = i0; i < i1; ++i) {
+        bstart[i] = run;
+        bcur[i] = run;
+        run += bcnt[i];
+    }
+    if (tid == 1023) bstart[n] = run;  // thread 1023's run ends at n: the total
 }
 
 // Sink of the stores the column-gradient kernel issues with nothing to store
 // (its contents are never read; each device holds its own copy).  Waves of
-// different workgroups use different 1 KiB pieces, so that such stores do
+// different workgroups use different 2 KiB pieces, so that such stores do
 // not all queue on one cache line.
 constexpr int kTrashBytes = 64 * 1024;
 __device__ __attribute__((aligned(16))) unsigned char dcn2_trash[kTrashBytes];
@@ -326,7 +380,6 @@ __global__ __launch_bounds__(512) void dcn2_colgrad_kernel(const BwdParams p) {
     const T *__restrict__ wt = (const T *)p.wt;
     T *__restrict__ goff = (T *)p.goff + (size_t)b * p.off_bs;
     T *__restrict__ gmask = p.gmask ? (T *)p.gmask + (size_t)b * p.msk_bs : nullptr;
-    float *__restrict__ gi = p.gi_acc + (size_t)b * p.H * p.W * cs;
 
     // gO fragments (MFMA B operand, [m][n]): n = this wave's 32-pixel block.
     frag gfr[NMS];
@@ -478,9 +531,9 @@ __global__ __launch_bounds__(512) void dcn2_colgrad_kernel(const BwdParams p) {
     };
     // This thread's corner gathers of the chunk sampled last.
     uint4 raw[4][2];
-    // this lane's 16 bytes of dcn2_trash
+    // this lane's 32 bytes of dcn2_trash (a wave uses one 2 KiB piece)
     uint4 *const trash_v = reinterpret_cast<uint4 *>(dcn2_trash) +
-                           ((blockIdx.x * 8 + wave) % (kTrashBytes / 1024)) * 64 + lane;
+                           ((blockIdx.x * 8 + wave) % (kTrashBytes / 2048)) * 128 + lane * 2;
     T *const trash_t = reinterpret_cast<T *>(trash_v);
 
     // Sampling of chunk c (offsets o): corner gathers, and the descriptor of
@@ -506,7 +559,7 @@ __global__ __launch_bounds__(512) void dcn2_colgrad_kernel(const BwdParams p) {
             raw[q][1] = src[1];
         }
         if (id.cc == 0) {
-            gmode = o.sx == -1 ? 0 : (o.sx >= 0 ? 1 : 2);
+            gmode = o.sx >= 0 ? 1 : 0;
             gsidx = o.sx;
         }
         if (lq == 0) {
@@ -627,10 +680,11 @@ __global__ __launch_bounds__(512) void dcn2_colgrad_kernel(const BwdParams p) {
     // grad_input hand-off of chunk c (parity X): 8 lanes per pixel, 16 bytes
     // (EPL channels) per lane.  A bucketed sample stores its masked
     // column-gradient row (8 rows of 16-byte pieces per wave instruction) for
-    // the gather kernel; a sample of a full bucket adds to grad_input here
-    // with fp32 atomics (the one conditional memory operation of the step).
+    // the gather kernel; a sample with no corner inside stores to dcn2_trash.
     auto handoff = [&](int X, const ChunkId &id) __attribute__((always_inline)) {
+        typedef typename RowOf<T>::type R;
         constexpr int EPL = 16 / sizeof(T), LPP = KC / EPL, PPI = 64 / LPP;
+        constexpr int NST = EPL * sizeof(R) / 16;  // 16-byte stores per lane
         static_assert(LPP == 8, "8 lanes cover one chunk row");
         const int co = lane % LPP, r = lane / LPP;
 #pragma unroll
@@ -651,19 +705,11 @@ __global__ __launch_bounds__(512) void dcn2_colgrad_kernel(const BwdParams p) {
             float mv8[EPL];
 #pragma unroll
             for (int e = 0; e < EPL; ++e) mv8[e] = v[e] * d.m;
-            uint4 *row = reinterpret_cast<uint4 *>((T *)p.cgm + (size_t)d.sidx * p.Cgp + id.cc * KC +
+            uint4 *row = reinterpret_cast<uint4 *>((R *)p.cgm + (size_t)d.sidx * p.Cgp + id.cc * KC +
                                                    co * EPL);
-            *(in && d.mode == 1 ? row : trash_v) = pack16<T>(mv8);
-            if (in && d.mode == 2) {
-                float *gib = gi + id.g * p.Cgp + id.cc * KC + co * EPL;
+            uint4 *dst = in && d.mode == 1 ? row : trash_v;
 #pragma unroll
-                for (int e = 0; e < EPL; ++e) {
-                    if (id.cc * KC + co * EPL + e >= p.Cg) continue;
-#pragma unroll
-                    for (int q = 0; q < 4; ++q)
-                        if (d.w[q] != 0.0f) unsafeAtomicAdd(gib + d.off[q] + e, v[e] * d.w[q]);
-                }
-            }
+            for (int i = 0; i < NST; ++i) dst[i] = pack16<R>(mv8 + i * (16 / sizeof(R)));
         }
     };
 
@@ -1163,36 +1209,38 @@ __global__ __launch_bounds__(512) void dcn2_gradw_line_kernel(const BwdParams p)
 
 // ---------------------------------------------------------------------------
 // grad_input gather.  One block per bucket (image, group, 16x16 cell tile).
-// The records of the bucket are counting-sorted by cell in LDS, together with
-// their fractional sample coordinates.  Then every pixel of the (TS+1)^2 window
-// the tile's corners can reach is pulled by one lane group (lane = channel):
-// pixel (py, px) is corner 00 of cell (py, px), 01 of (py, px-1), 10 of
-// (py-1, px) and 11 of (py-1, px-1), so its value is the sum over the records
-// of those four cells of (bilinear corner weight) x (masked column-gradient
+// The bucket's records are taken in batches of up to kGatherBatch; each
+// batch is counting-sorted by cell in LDS, together with the fractional
+// sample coordinates.  Then every pixel of the (TS+1)^2 window the tile's
+// corners can reach is pulled by one lane group (lane = channel): pixel
+// (py, px) is corner 00 of cell (py, px), 01 of (py, px-1), 10 of (py-1, px)
+// and 11 of (py-1, px-1), so its value is the sum over the batch's records of
+// those four cells of (bilinear corner weight) x (masked column-gradient
 // row), computed in a register with up to two batches of row loads in
-// flight.  Interior pixels (reachable from this tile's cells only) are
-// complete and added by a plain read-modify-write; the sums of the one-pixel
-// border ring, shared with the neighbouring tiles, are stored per bucket
-// (kRing pixels) and added by finalize_gi_kernel.  This replaces the global
-// atomic per (sample, corner, channel) of the reference's col2im scatter
-// (com.cu:553-609) with plain stores.
-constexpr int kGatherCapMax = 4096;  // records of one bucket the LDS sort holds
-// Buffer offset past every bucket's rows (cap * Cgp * esz stays far below it),
-// so a load there reads 0.
+// flight.  Interior pixels (reachable from this tile's cells only) are added
+// by a plain read-modify-write; the sums of the one-pixel border ring, shared
+// with the neighbouring tiles, are stored per bucket (kRing pixels; the first
+// batch stores, later batches add) and merged by ring_merge_kernel.  Every
+// entry of the ring is written on every call, an empty bucket's included.
+// This replaces the global atomic per (sample, corner, channel) of the
+// reference's col2im scatter (com.cu:553-609) with plain stores.
+constexpr int kGatherBatch = 4096;  // records of one batch the LDS sort holds
+// Buffer offset past one batch's rows (the host keeps kGatherBatch * Cgp * esz
+// below it), so a load there reads 0.
 constexpr int kGatherOutOfRange = 0x7ffffff0;
 // static LDS of dcn2_gi_gather_kernel: cell counts and starts, sorted slots and fractions
 constexpr int kGatherStaticLds = kCellTile * kCellTile * 4 + (kCellTile * kCellTile + 1) * 4 +
-                                 kGatherCapMax * 2 + kGatherCapMax * 8;
+                                 kGatherBatch * 2 + kGatherBatch * 8;
 
 template <typename T>
 __global__ __launch_bounds__(512) void dcn2_gi_gather_kernel(const BwdParams p) {
     constexpr int KC = Mma<T>::KC;  // channels per pass
     constexpr int TS = kCellTile, TW = TS + 1, NCELL = TS * TS;
-    constexpr int RPT = kGatherCapMax / 512;
+    constexpr int RPT = kGatherBatch / 512;
     __shared__ int ccnt[NCELL];
     __shared__ int cstart[NCELL + 1];
-    __shared__ unsigned short sslot[kGatherCapMax];   // bucket slot, sorted by cell
-    __shared__ float2 sfrac[kGatherCapMax];           // (ly, lx), sorted by cell
+    __shared__ unsigned short sslot[kGatherBatch];    // row in the batch, sorted by cell
+    __shared__ float2 sfrac[kGatherBatch];            // (ly, lx), sorted by cell
     static_assert(sizeof(ccnt) + sizeof(cstart) + sizeof(sslot) + sizeof(sfrac) == kGatherStaticLds,
                   "the launch's occupancy cap assumes this static LDS");
 
@@ -1201,193 +1249,214 @@ __global__ __launch_bounds__(512) void dcn2_gi_gather_kernel(const BwdParams p) 
     const int bucket = xcd_remap(blockIdx.x, nb);
     const int tx = bucket % p.ntx, ty = (bucket / p.ntx) % p.nty;
     const int bg = bucket / (p.ntx * p.nty), b = bg / p.G, g = bg - b * p.G;
-    const int count = min(p.cnt[bucket], p.cap);
-    const int4 *__restrict__ recs = p.rec + (size_t)bucket * p.cap;
+    const int row0 = p.bstart[bucket], count = p.bstart[bucket + 1] - row0;
     const int oy = ty * TS - 1, ox = tx * TS - 1;  // pixel of local (0, 0)
     const int cs = p.G * p.Cgp, cpg = p.Cgp / KC;
     float *__restrict__ gi = p.gi_acc + (size_t)b * p.H * p.W * cs + g * p.Cgp;
 
-    // 1. counting sort by cell (cell = local row * TS + local column)
-    for (int i = tid; i < NCELL; i += 512) ccnt[i] = 0;
-    __syncthreads();
-    int key[RPT];  // (cell << 16) | rank, or -1
-    float2 fr[RPT];
-#pragma unroll
-    for (int k = 0; k < RPT; ++k) {
-        const int r = tid + k * 512;
-        key[k] = -1;
-        fr[k] = make_float2(0.f, 0.f);
-        if (r < count) {
-            const int4 rc = recs[r];
-            const int cy = (int)(short)(rc.y & 0xffff) - oy, cx = (rc.y >> 16) - ox;  // [0, TS)
-            const int cell = cy * TS + cx;
-            fr[k] = make_float2(__int_as_float(rc.z), __int_as_float(rc.w));
-            key[k] = (cell << 16) | atomicAdd(&ccnt[cell], 1);
-        }
-    }
-    __syncthreads();
-    if (wave == 0) {  // exclusive scan of the 256 counts: 4 per lane + wave scan
-        int v[4], s = 0;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            v[i] = ccnt[lane * 4 + i];
-            s += v[i];
-        }
-        int incl = s;
-#pragma unroll
-        for (int d = 1; d < 64; d <<= 1) {
-            const int o = __shfl_up(incl, d, 64);
-            if (lane >= d) incl += o;
-        }
-        int run = incl - s;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            cstart[lane * 4 + i] = run;
-            run += v[i];
-        }
-        if (lane == 63) cstart[NCELL] = run;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int k = 0; k < RPT; ++k) {
-        if (key[k] < 0) continue;
-        const int pos = cstart[key[k] >> 16] + (key[k] & 0xffff);
-        sslot[pos] = (unsigned short)(tid + k * 512);
-        sfrac[pos] = fr[k];
-    }
-    __syncthreads();
+    // one pass per batch of records; an empty bucket still takes one (with no
+    // records) to write its ring
+    for (int base = 0; base == 0 || base < count; base += kGatherBatch) {
+        const int nrec = min(count - base, kGatherBatch);
+        const int4 *__restrict__ recs = p.rec + (size_t)row0 + base;
+        const bool first = base == 0;
+        if (!first) __syncthreads();  // the previous batch is done with the LDS arrays
 
-    // 2. pull every pixel of the window.  A wave takes PPW pixels at a time;
-    //    lane (pixel slot ps, channel group co) sums the 16-byte slices (EPL
-    //    channels) of all rows of its pixel's records, so one load instruction
-    //    reads PPW whole rows.  Pixel (py, px) is corner 00 of cell (py, px),
-    //    01 of (py, px-1), 10 of (py-1, px) and 11 of (py-1, px-1).
-    //    Rows come in batches of 8 from buffer loads over the bucket's rows:
-    //    a row index past the pixel's count reads 0 through an out-of-range
-    //    offset, so no load sits in a branch, the compiler's load counting
-    //    stays exact, and the next batch is in flight while one is summed
-    //    (two register sets, the loop unrolled by two).
-    constexpr int EPL = 16 / sizeof(T);  // channels per lane per row
-    constexpr int LPR = KC / EPL;        // lanes per row (8)
-    constexpr int PPW = 64 / LPR;        // pixels per wave pass (8)
-    static_assert(LPR == 8, "a 16-byte lane slice of a KC-channel row; 8-lane swizzle groups");
-    typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
-    const int co = lane % LPR, ps = lane / LPR;
-    const int row_bytes = p.Cgp * (int)sizeof(T);
-    for (int cc = 0; cc < cpg; ++cc) {
-        // buffer over the bucket's rows from this chunk's first channel (uniform);
-        // the lane's 16-byte slice goes into the offset
-        const T *rows = (const T *)p.cgm + ((size_t)bucket * p.cap) * p.Cgp + cc * KC;
-        const __amdgpu_buffer_rsrc_t rrs = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<T *>(rows), (short)0, p.cap * row_bytes, 0x00020000);
-        const int slice = co * 16;
-        for (int pl0 = wave * PPW; pl0 < TW * TW; pl0 += 8 * PPW) {
-            const int pl = pl0 + ps;
-            const int py = pl / TW, px = pl - py * TW;
-            const int Y = oy + py, X = ox + px;
-            const bool live = pl < TW * TW && Y >= 0 && Y < p.H && X >= 0 && X < p.W;
-            // record ranges of the four cells whose corner q is this pixel
-            int beg[4], len[4];
+        // 1. counting sort by cell (cell = local row * TS + local column)
+        for (int i = tid; i < NCELL; i += 512) ccnt[i] = 0;
+        __syncthreads();
+        int key[RPT];  // (cell << 16) | rank, or -1
+        float2 fr[RPT];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int cy = py - (q >> 1), cx = px - (q & 1);
-                const bool in = live && cy >= 0 && cy < TS && cx >= 0 && cx < TS;
-                const int cell = in ? cy * TS + cx : 0;
-                beg[q] = in ? cstart[cell] : 0;
-                len[q] = in ? cstart[cell + 1] - beg[q] : 0;
-            }
-            const int e1 = len[0], e2 = e1 + len[1], e3 = e2 + len[2], tot = e3 + len[3];
-            float sum[EPL];
-#pragma unroll
-            for (int e = 0; e < EPL; ++e) sum[e] = 0.0f;
-            // Row j of the pixel's corner-ordered record ranges: its record
-            // position, weight and row offset (out of range past the pixel's
-            // count), by selects only.  Lane co of the pixel's 8-lane group
-            // works out row jb + co of a batch of LPR rows; the batch's loads
-            // take each row's offset and weight from its lane (ds_swizzle in
-            // bit mode: lane (l & 0x18) | u of every 32-lane half), so the
-            // index arithmetic is done once per row instead of once per lane.
-            auto row_info = [&](int jb, int &off, float &w) __attribute__((always_inline)) {
-                const int j = jb + co;
-                const bool ok = j < tot, q1 = j >= e1, q2 = j >= e2, q3 = j >= e3;
-                int pos = beg[0] + j;
-                pos = q1 ? beg[1] + j - e1 : pos;
-                pos = q2 ? beg[2] + j - e2 : pos;
-                pos = q3 ? beg[3] + j - e3 : pos;
-                pos = ok ? pos : 0;
-                const float2 f = sfrac[pos];
-                const float wy = q2 ? f.x : 1.0f - f.x;             // corners 10, 11
-                const float wx = (q1 != q2) || q3 ? f.y : 1.0f - f.y;  // corners 01, 11
-                w = ok ? wy * wx : 0.0f;
-                off = ok ? (int)sslot[pos] * row_bytes : kGatherOutOfRange;
-            };
-            auto fetch = [&](int off, float w, u32x4 (&raw)[LPR], float (&wgt)[LPR]) __attribute__((always_inline)) {
-                static_for<0, LPR>([&](auto uc) __attribute__((always_inline)) {
-                    constexpr int u = decltype(uc)::value;
-                    const int ou = __builtin_amdgcn_ds_swizzle(off, (u << 5) | 0x18);
-                    wgt[u] = __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(w), (u << 5) | 0x18));
-                    // row_bytes is a multiple of 128 and the marker has the low
-                    // bits set, so OR-ing the slice in keeps either in range
-                    raw[u] = __builtin_amdgcn_raw_buffer_load_b128(rrs, ou | slice, 0, 0);
-                });
-            };
-            auto accumulate = [&](const u32x4 (&raw)[LPR], const float (&wgt)[LPR]) __attribute__((always_inline)) {
-#pragma unroll
-                for (int u = 0; u < LPR; ++u) {
-                    float v[EPL];
-                    Unpack<T>::run(make_uint4(raw[u].x, raw[u].y, raw[u].z, raw[u].w), v);
-#pragma unroll
-                    for (int e = 0; e < EPL; ++e) sum[e] = fmaf(wgt[u], v[e], sum[e]);
-                }
-            };
-            u32x4 ra[LPR], rb[LPR];
-            float wa[LPR], wb[LPR];
-            int oa, ob;
-            float xa, xb;
-            // (scheduling barriers keep each batch's loads ahead of the sums of
-            // the previous one; left alone the scheduler groups the fetches)
-            row_info(0, oa, xa);
-            fetch(oa, xa, ra, wa);
-            for (int j0 = 0; j0 < tot; j0 += 2 * LPR) {
-                row_info(j0 + LPR, ob, xb);
-                fetch(ob, xb, rb, wb);
-                __builtin_amdgcn_sched_barrier(0);
-                accumulate(ra, wa);
-                __builtin_amdgcn_sched_barrier(0);
-                row_info(j0 + 2 * LPR, oa, xa);
-                fetch(oa, xa, ra, wa);
-                __builtin_amdgcn_sched_barrier(0);
-                accumulate(rb, wb);
-                __builtin_amdgcn_sched_barrier(0);
-            }
-            // Interior pixels (reachable from this tile's cells only) are this
-            // block's alone: a plain read-modify-write.  The accumulator's
-            // padding channels (Cg..Cgp of a group) are never read back (and
-            // receive zeros), so whole 16-byte pieces are updated (a guarded
-            // update per channel made every channel a separate round trip).
-            if (py >= 1 && py <= TS - 1 && px >= 1 && px <= TS - 1) {
-                if (tot == 0) continue;
-                f32x4 *d4 = reinterpret_cast<f32x4 *>(gi + ((size_t)Y * p.W + X) * cs + cc * KC + co * EPL);
-                f32x4 acc4[EPL / 4];
-#pragma unroll
-                for (int i = 0; i < EPL / 4; ++i) acc4[i] = d4[i];
-#pragma unroll
-                for (int i = 0; i < EPL / 4; ++i) {
-#pragma unroll
-                    for (int k = 0; k < 4; ++k) acc4[i][k] += sum[4 * i + k];
-                    d4[i] = acc4[i];
-                }
-            } else if (pl < TW * TW) {
-                // border ring: written in full every call (zeros included) and
-                // added by finalize_gi_kernel, no atomics
-                f32x4 *r4 = reinterpret_cast<f32x4 *>(
-                    p.ring + ((size_t)bucket * kRing + ring_index(py, px)) * p.Cgp + cc * KC + co * EPL);
-#pragma unroll
-                for (int i = 0; i < EPL / 4; ++i)
-                    r4[i] = f32x4{sum[4 * i], sum[4 * i + 1], sum[4 * i + 2], sum[4 * i + 3]};
+        for (int k = 0; k < RPT; ++k) {
+            const int r = tid + k * 512;
+            key[k] = -1;
+            fr[k] = make_float2(0.f, 0.f);
+            if (r < nrec) {
+                const int4 rc = recs[r];
+                const int cy = (int)(short)(rc.y & 0xffff) - oy, cx = (rc.y >> 16) - ox;  // [0, TS)
+                const int cell = cy * TS + cx;
+                fr[k] = make_float2(__int_as_float(rc.z), __int_as_float(rc.w));
+                key[k] = (cell << 16) | atomicAdd(&ccnt[cell], 1);
             }
         }
-    }
+        __syncthreads();
+        if (wave == 0) {  // exclusive scan of the 256 counts: 4 per lane + wave scan
+            int v[4], s = 0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                v[i] = ccnt[lane * 4 + i];
+                s += v[i];
+            }
+            int incl = s;
+#pragma unroll
+            for (int d = 1; d < 64; d <<= 1) {
+                const int o = __shfl_up(incl, d, 64);
+                if (lane >= d) incl += o;
+            }
+            int run = incl - s;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                cstart[lane * 4 + i] = run;
+                run += v[i];
+            }
+            if (lane == 63) cstart[NCELL] = run;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < RPT; ++k) {
+            if (key[k] < 0) continue;
+            const int pos = cstart[key[k] >> 16] + (key[k] & 0xffff);
+            sslot[pos] = (unsigned short)(tid + k * 512);
+            sfrac[pos] = fr[k];
+        }
+        __syncthreads();
+
+        // 2. pull every pixel of the window.  A wave takes PPW pixels at a time;
+        //    lane (pixel slot ps, channel group co) sums the 16-byte slices (EPL
+        //    channels) of all rows of its pixel's records, so one load instruction
+        //    reads PPW whole rows.  Pixel (py, px) is corner 00 of cell (py, px),
+        //    01 of (py, px-1), 10 of (py-1, px) and 11 of (py-1, px-1).
+        //    Rows come in batches of 8 from buffer loads over the bucket's rows:
+        //    a row index past the pixel's count reads 0 through an out-of-range
+        //    offset, so no load sits in a branch, the compiler's load counting
+        //    stays exact, and the next batch is in flight while one is summed
+        //    (two register sets, the loop unrolled by two).
+        typedef typename RowOf<T>::type R;   // element type of the rows
+        constexpr int EPL = 16 / sizeof(T);  // channels per lane per row
+        constexpr int LPR = KC / EPL;        // lanes per row (8)
+        constexpr int PPW = 64 / LPR;        // pixels per wave pass (8)
+        constexpr int NLD = EPL * sizeof(R) / 16;  // 16-byte loads per lane per row
+        static_assert(LPR == 8, "a lane slice of a KC-channel row; 8-lane swizzle groups");
+        typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+        const int co = lane % LPR, ps = lane / LPR;
+        const int row_bytes = p.Cgp * (int)sizeof(R);
+        for (int cc = 0; cc < cpg; ++cc) {
+            // buffer over the batch's rows from this chunk's first channel (uniform);
+            // the lane's slice goes into the offset
+            const R *rows = (const R *)p.cgm + ((size_t)row0 + base) * p.Cgp + cc * KC;
+            const __amdgpu_buffer_rsrc_t rrs = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<R *>(rows), (short)0, nrec * row_bytes, 0x00020000);
+            const int slice = co * 16 * NLD;
+            for (int pl0 = wave * PPW; pl0 < TW * TW; pl0 += 8 * PPW) {
+                const int pl = pl0 + ps;
+                const int py = pl / TW, px = pl - py * TW;
+                const int Y = oy + py, X = ox + px;
+                const bool live = pl < TW * TW && Y >= 0 && Y < p.H && X >= 0 && X < p.W;
+                // record ranges of the four cells whose corner q is this pixel
+                int beg[4], len[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int cy = py - (q >> 1), cx = px - (q & 1);
+                    const bool in = live && cy >= 0 && cy < TS && cx >= 0 && cx < TS;
+                    const int cell = in ? cy * TS + cx : 0;
+                    beg[q] = in ? cstart[cell] : 0;
+                    len[q] = in ? cstart[cell + 1] - beg[q] : 0;
+                }
+                const int e1 = len[0], e2 = e1 + len[1], e3 = e2 + len[2], tot = e3 + len[3];
+                float sum[EPL];
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) sum[e] = 0.0f;
+                // Row j of the pixel's corner-ordered record ranges: its record
+                // position, weight and row offset (out of range past the pixel's
+                // count), by selects only.  Lane co of the pixel's 8-lane group
+                // works out row jb + co of a batch of LPR rows; the batch's loads
+                // take each row's offset and weight from its lane (ds_swizzle in
+                // bit mode: lane (l & 0x18) | u of every 32-lane half), so the
+                // index arithmetic is done once per row instead of once per lane.
+                auto row_info = [&](int jb, int &off, float &w) __attribute__((always_inline)) {
+                    const int j = jb + co;
+                    const bool ok = j < tot, q1 = j >= e1, q2 = j >= e2, q3 = j >= e3;
+                    int pos = beg[0] + j;
+                    pos = q1 ? beg[1] + j - e1 : pos;
+                    pos = q2 ? beg[2] + j - e2 : pos;
+                    pos = q3 ? beg[3] + j - e3 : pos;
+                    pos = ok ? pos : 0;
+                    const float2 f = sfrac[pos];
+                    const float wy = q2 ? f.x : 1.0f - f.x;             // corners 10, 11
+                    const float wx = (q1 != q2) || q3 ? f.y : 1.0f - f.y;  // corners 01, 11
+                    w = ok ? wy * wx : 0.0f;
+                    off = ok ? (int)sslot[pos] * row_bytes : kGatherOutOfRange;
+                };
+                auto fetch = [&](int off, float w, u32x4 (&raw)[LPR][NLD], float (&wgt)[LPR]) __attribute__((always_inline)) {
+                    static_for<0, LPR>([&](auto uc) __attribute__((always_inline)) {
+                        constexpr int u = decltype(uc)::value;
+                        const int ou = __builtin_amdgcn_ds_swizzle(off, (u << 5) | 0x18);
+                        wgt[u] = __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(w), (u << 5) | 0x18));
+                        // row_bytes is a multiple of 128 * NLD (the slice's range)
+                        // and the marker has the low bits set, so OR-ing the slice
+                        // in keeps either in range
+#pragma unroll
+                        for (int h = 0; h < NLD; ++h)
+                            raw[u][h] = __builtin_amdgcn_raw_buffer_load_b128(rrs, ou | (slice + 16 * h), 0, 0);
+                    });
+                };
+                auto accumulate = [&](const u32x4 (&raw)[LPR][NLD], const float (&wgt)[LPR]) __attribute__((always_inline)) {
+                    constexpr int EU = 16 / sizeof(R);  // channels per 16-byte load
+#pragma unroll
+                    for (int u = 0; u < LPR; ++u) {
+#pragma unroll
+                        for (int h = 0; h < NLD; ++h) {
+                            float v[EU];
+                            Unpack<R>::run(make_uint4(raw[u][h].x, raw[u][h].y, raw[u][h].z, raw[u][h].w), v);
+#pragma unroll
+                            for (int e = 0; e < EU; ++e) sum[h * EU + e] = fmaf(wgt[u], v[e], sum[h * EU + e]);
+                        }
+                    }
+                };
+                u32x4 ra[LPR][NLD], rb[LPR][NLD];
+                float wa[LPR], wb[LPR];
+                int oa, ob;
+                float xa, xb;
+                // (scheduling barriers keep each batch's loads ahead of the sums of
+                // the previous one; left alone the scheduler groups the fetches)
+                row_info(0, oa, xa);
+                fetch(oa, xa, ra, wa);
+                for (int j0 = 0; j0 < tot; j0 += 2 * LPR) {
+                    row_info(j0 + LPR, ob, xb);
+                    fetch(ob, xb, rb, wb);
+                    __builtin_amdgcn_sched_barrier(0);
+                    accumulate(ra, wa);
+                    __builtin_amdgcn_sched_barrier(0);
+                    row_info(j0 + 2 * LPR, oa, xa);
+                    fetch(oa, xa, ra, wa);
+                    __builtin_amdgcn_sched_barrier(0);
+                    accumulate(rb, wb);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                // Interior pixels (reachable from this tile's cells only) are this
+                // block's alone: a plain read-modify-write.  The accumulator's
+                // padding channels (Cg..Cgp of a group) are never read back (and
+                // receive zeros), so whole 16-byte pieces are updated (a guarded
+                // update per channel made every channel a separate round trip).
+                if (py >= 1 && py <= TS - 1 && px >= 1 && px <= TS - 1) {
+                    if (tot == 0) continue;
+                    f32x4 *d4 = reinterpret_cast<f32x4 *>(gi + ((size_t)Y * p.W + X) * cs + cc * KC + co * EPL);
+                    f32x4 acc4[EPL / 4];
+#pragma unroll
+                    for (int i = 0; i < EPL / 4; ++i) acc4[i] = d4[i];
+#pragma unroll
+                    for (int i = 0; i < EPL / 4; ++i) {
+#pragma unroll
+                        for (int k = 0; k < 4; ++k) acc4[i][k] += sum[4 * i + k];
+                        d4[i] = acc4[i];
+                    }
+                } else if (pl < TW * TW) {
+                    // border ring: written in full every call (zeros included) and
+                    // added by ring_merge_kernel, no atomics.  Later batches add to
+                    // it; this lane wrote the same entry in every earlier batch.
+                    f32x4 *r4 = reinterpret_cast<f32x4 *>(
+                        p.ring + ((size_t)bucket * kRing + ring_index(py, px)) * p.Cgp + cc * KC + co * EPL);
+#pragma unroll
+                    for (int i = 0; i < EPL / 4; ++i) {
+                        f32x4 v = f32x4{sum[4 * i], sum[4 * i + 1], sum[4 * i + 2], sum[4 * i + 3]};
+                        if (!first) v += r4[i];
+                        r4[i] = v;
+                    }
+                }
+            }
+        }
+    }  // batches
 }
 
 // ---------------------------------------------------------------------------
@@ -1562,7 +1631,7 @@ static hipError_t backward_t(const Geo &g, const BwdParams &p0, void *grad_input
         const size_t n_gi = (size_t)g.B * g.H * g.W * g.cs;
         const size_t n_gw = (size_t)g.Mp * g.Kp;
         // gb_acc is null when the caller wants no grad_bias; nothing reads it then.
-        float *bufs[4] = {p.gi_acc, p.gw_acc, p.gb_acc, (float *)p.cnt};
+        float *bufs[4] = {p.gi_acc, p.gw_acc, p.gb_acc, (float *)p.bcnt};
         const size_t counts[4] = {n_gi, n_gw, (size_t)g.Mp,
                                   (size_t)g.B * g.G * p.nty * p.ntx};
         for (int i = 0; i < 4; ++i) {
@@ -1578,15 +1647,18 @@ static hipError_t backward_t(const Geo &g, const BwdParams &p0, void *grad_input
         // 2. column gradient: grad_offset, grad_mask, grad_input accumulation
         prof_begin(DCN2_STAGE_BWD_COLGRAD, s);
         {
-            if ((long)p.nty * p.ntx <= kBucketTab) {
-                dim3 bgrid(ceil_div(g.N, 256 * kBucketSPT), g.G * g.KK, g.B);
-                dcn2_bucket_kernel<<<bgrid, 256, 0, s>>>(p, p.offset, sizeof(T) == 4,
-                                                         std::is_same<T, bf16>::value);
-            } else {
-                dim3 bgrid(ceil_div(g.N, 256), g.G * g.KK, g.B);
-                dcn2_bucket_global_kernel<<<bgrid, 256, 0, s>>>(p, p.offset, sizeof(T) == 4,
-                                                                std::is_same<T, bf16>::value);
-            }
+            // buckets: count, scan, place (exact sizes, see dcn2_bucket_kernel)
+            const int f32 = sizeof(T) == 4, isbf = std::is_same<T, bf16>::value;
+            const int nbuckets = g.B * g.G * p.nty * p.ntx;
+            const bool tab = (long)p.nty * p.ntx <= kBucketTab;
+            const dim3 bgrid(ceil_div(g.N, tab ? 256 * kBucketSPT : 256), g.G * g.KK, g.B);
+            if (tab) dcn2_bucket_kernel<false><<<bgrid, 256, 0, s>>>(p, p.offset, f32, isbf);
+            else dcn2_bucket_global_kernel<false><<<bgrid, 256, 0, s>>>(p, p.offset, f32, isbf);
+            if ((e = hipGetLastError()) != hipSuccess) return e;
+            dcn2_bucket_scan_kernel<<<1, 1024, 0, s>>>(p.bcnt, p.bstart, p.bcur, nbuckets);
+            if ((e = hipGetLastError()) != hipSuccess) return e;
+            if (tab) dcn2_bucket_kernel<true><<<bgrid, 256, 0, s>>>(p, p.offset, f32, isbf);
+            else dcn2_bucket_global_kernel<true><<<bgrid, 256, 0, s>>>(p, p.offset, f32, isbf);
             if ((e = hipGetLastError()) != hipSuccess) return e;
             dim3 grid(p.tiles_per_img, g.B);
             // W'^T staged in LDS when a chunk of it fits (Mp <= 256); gO resident
@@ -1712,11 +1784,11 @@ GatherGeo gather_geometry(const Geo &g) {
     gg.ntx = ceil_div(g.W + 1, kCellTile);
     gg.nty = ceil_div(g.H + 1, kCellTile);
     gg.nbuckets = (long)g.B * g.G * gg.ntx * gg.nty;
-    const long samples = (long)g.B * g.G * g.KK * g.N;
-    const long avg = gg.nbuckets ? (samples + gg.nbuckets - 1) / gg.nbuckets : 0;
-    // Room for twice the mean occupancy; a fuller bucket spills its excess to
-    // the direct-atomic path, which is slower but equally exact.
-    gg.cap = (int)std::min<long>(2 * avg + 256, kGatherCapMax);
+    // every sample is placed in at most one bucket
+    gg.rows = (long)g.B * g.G * g.KK * g.N;
+    gg.row_esz = row_elem_bytes(g.dtype);
+    gg.batch_bytes = (long)kGatherBatch * g.Cgp * gg.row_esz;
+    gg.max_batch_bytes = kGatherOutOfRange;
     return gg;
 }
 
@@ -1725,7 +1797,8 @@ hipError_t launch_backward(const Geo &g, const void *xt, const void *wt, const v
                            const void *mask, const void *grad_out, void *grad_input,
                            void *grad_offset, void *grad_mask, void *grad_weight, void *grad_bias,
                            float *gi_acc, float *gw_acc, float *gb_acc, void *cgm, void *rec,
-                           int *cnt, int *sidx, float *ring, hipStream_t s) {
+                           int *bcnt, int *bstart, int *bcur, int *sidx, float *ring,
+                           hipStream_t s) {
     BwdParams p;
     p.xt = xt;
     p.wt = wt;
@@ -1766,11 +1839,12 @@ hipError_t launch_backward(const Geo &g, const void *xt, const void *wt, const v
     const GatherGeo gg = gather_geometry(g);
     p.cgm = cgm;
     p.rec = (int4 *)rec;
-    p.cnt = cnt;
+    p.bcnt = bcnt;
+    p.bstart = bstart;
+    p.bcur = bcur;
     p.sidx = sidx;
     p.ntx = gg.ntx;
     p.nty = gg.nty;
-    p.cap = gg.cap;
     p.ring = ring;
     switch (g.dtype) {
     case DCN2_F16: return backward_t<f16>(g, p, grad_input, grad_weight, grad_bias, s);

@@ -299,9 +299,8 @@ __global__ __launch_bounds__(512) void dcn2_fwd_kernel(const FwdParams p) {
 // ---------------------------------------------------------------------------
 
 // Descriptor of one (pixel, chunk) in the LDS ring: the four corner offsets
-// (elements, 0 outside the image) and the four mask-folded corner weights,
-// as packed (w, w) f16 pairs for f16 and as floats for bf16.  Half h (16
-// bytes) holds corners 2h and 2h+1.
+// (bytes, 0 outside the image) and the four mask-folded corner weights as
+// fp32 bits.  Half h (16 bytes) holds corners 2h and 2h+1.
 struct RingHalf {
     int o0, o1;
     uint32_t w0, w1;
@@ -310,45 +309,16 @@ struct RingDesc {
     RingHalf h[2];
 };
 
-template <typename T> struct Blend8;
-template <> struct Blend8<f16> {
-    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-    static __device__ __forceinline__ uint4 weights(const float (&w)[4]) {
-        uint32_t o[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const _Float16 hw = (_Float16)w[q];
-            o[q] = __builtin_bit_cast(uint32_t, h2{hw, hw});
-        }
-        return make_uint4(o[0], o[1], o[2], o[3]);
-    }
-    // packed f16 FMAs, two channels per instruction, with f16 corner weights
-    // (in [0, 1]); the result is rounded to f16 for the MFMA anyway.
-    static __device__ __forceinline__ uint4 run(const uint4 (&r)[4], uint4 wd) {
-        const h2 wq[4] = {__builtin_bit_cast(h2, wd.x), __builtin_bit_cast(h2, wd.y),
-                          __builtin_bit_cast(h2, wd.z), __builtin_bit_cast(h2, wd.w)};
-        const uint32_t *c0 = reinterpret_cast<const uint32_t *>(&r[0]);
-        const uint32_t *c1 = reinterpret_cast<const uint32_t *>(&r[1]);
-        const uint32_t *c2 = reinterpret_cast<const uint32_t *>(&r[2]);
-        const uint32_t *c3 = reinterpret_cast<const uint32_t *>(&r[3]);
-        uint32_t o[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            h2 a = __builtin_bit_cast(h2, c0[e]) * wq[0];
-            a = __builtin_elementwise_fma(__builtin_bit_cast(h2, c1[e]), wq[1], a);
-            a = __builtin_elementwise_fma(__builtin_bit_cast(h2, c2[e]), wq[2], a);
-            a = __builtin_elementwise_fma(__builtin_bit_cast(h2, c3[e]), wq[3], a);
-            o[e] = __builtin_bit_cast(uint32_t, a);
-        }
-        return make_uint4(o[0], o[1], o[2], o[3]);
-    }
-};
-template <> struct Blend8<bf16> {
+// Bilinear blend of one 16-byte piece (8 channels) of the four corners:
+// fp32 weights, fp32 products and sums, one rounding to T at the end, as the
+// reference's sampler computes in fp32 and rounds its columns once
+// (com.cu:119-148, 83, 87).  For f16 the conversions fold into mixed-precision
+// FMAs (f16 source, fp32 accumulator).
+template <typename T> struct Blend8 {
     static __device__ __forceinline__ uint4 weights(const float (&w)[4]) {
         return make_uint4(__float_as_uint(w[0]), __float_as_uint(w[1]), __float_as_uint(w[2]),
                           __float_as_uint(w[3]));
     }
-    // fp32 blend (bf16 -> fp32 is a shift), rounded to bf16 once.
     static __device__ __forceinline__ uint4 run(const uint4 (&r)[4], uint4 wd) {
         const float w[4] = {__uint_as_float(wd.x), __uint_as_float(wd.y), __uint_as_float(wd.z),
                             __uint_as_float(wd.w)};
@@ -358,11 +328,11 @@ template <> struct Blend8<bf16> {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             float v[8];
-            Unpack<bf16>::run(r[q], v);
+            Unpack<T>::run(r[q], v);
 #pragma unroll
             for (int e = 0; e < 8; ++e) acc[e] = fmaf(w[q], v[e], acc[e]);
         }
-        return pack16<bf16>(acc);
+        return pack16<T>(acc);
     }
 };
 

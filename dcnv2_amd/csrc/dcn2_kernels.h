@@ -6,6 +6,8 @@
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 
+struct dcn2_desc;  // include/dcnv2_amd.h
+
 namespace dcn2 {
 
 // Validated problem geometry plus the derived packing sizes.
@@ -32,6 +34,15 @@ struct Geo {
     int msk_logit;
 };
 
+// dcn2_api.cpp: the descriptor check shared by every entry point, the forward
+// on a given workspace, and the per-thread error message (printf-style; returns
+// `code`).
+int make_geo(const ::dcn2_desc *d, Geo &g);
+int forward_impl(const Geo &g, const void *input, const void *weight, const void *mask,
+                 const void *offset, const void *bias, void *output, void *workspace,
+                 size_t workspace_bytes, void *stream);
+int fail(int code, const char *fmt, ...);
+
 // Workspace carving shared by forward and backward (byte offsets).
 struct FwdWorkspace {
     size_t xt, wp, tab, total;
@@ -39,16 +50,20 @@ struct FwdWorkspace {
 FwdWorkspace fwd_workspace(const Geo &g);
 
 struct BwdWorkspace {
-    size_t xt, wt, tab, gi_acc, gw_acc, gb_acc, cgm, rec, cnt, sidx, ring, total;
+    size_t xt, wt, tab, gi_acc, gw_acc, gb_acc, cgm, rec, bcnt, bstart, bcur, sidx, ring, total;
 };
 // Border-ring pixels of one grad_input gather window (4 x the cell tile side).
 constexpr int kGatherRing = 64;
 BwdWorkspace bwd_workspace(const Geo &g);
 
-// Bucket geometry of the grad_input gather (dcn2_backward.hip).
+// Bucket geometry of the grad_input gather (dcn2_backward.hip): cell tiles
+// per row / column, buckets, rows of all buckets together (one per sample),
+// bytes per row element, and the bytes of one gather batch's rows with the
+// limit they must stay below.
 struct GatherGeo {
-    int ntx, nty, cap;
-    long nbuckets;
+    int ntx, nty, row_esz;
+    long nbuckets, rows;
+    long batch_bytes, max_batch_bytes;
 };
 GatherGeo gather_geometry(const Geo &g);
 
@@ -69,6 +84,7 @@ hipError_t launch_backward(const Geo &g, const void *xt, const void *wt, const v
                            const void *mask, const void *grad_out, void *grad_input,
                            void *grad_offset, void *grad_mask, void *grad_weight, void *grad_bias,
                            float *gi_acc, float *gw_acc, float *gb_acc, void *cgm, void *rec,
-                           int *cnt, int *sidx, float *ring, hipStream_t s);
+                           int *bcnt, int *bstart, int *bcur, int *sidx, float *ring,
+                           hipStream_t s);
 
 }  // namespace dcn2

@@ -9,3 +9,15 @@ for p in (ROOT, os.path.join(ROOT, "tests")):
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (HIP) device")
+
+
+def pytest_sessionfinish(session, exitstatus):
+    path = os.environ.get("DCN2_PARITY_LOG")
+    if not path:
+        return
+    import json
+
+    from util import PARITY_LOG
+    os.makedirs(os.path.dirname(os.path.abspath(path)), exist_ok=True)
+    with open(path, "w") as f:
+        json.dump(PARITY_LOG, f, indent=0)

@@ -25,7 +25,7 @@ from dcnv2_amd import _C
 from dcnv2_amd.dcn_v2_mm import DCN
 from dcnv2_amd.workloads import CONFIGS
 from oracle import oracle
-from util import TOL, rel_err
+from util import TOL, check
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
@@ -57,12 +57,6 @@ def _split(om, n_off):
     """offset, mask of the reference's split, in fp64 (om's stored values)."""
     o = om.double()
     return o[:, :n_off], torch.sigmoid(o[:, n_off:])
-
-
-def check(name, got, ref, tol):
-    e = rel_err(got, ref)
-    print(f"  {name}: rel_err={e:.3e} (tol {tol:.0e})")
-    assert e <= tol, f"{name}: {e:.3e} > {tol:.0e}"
 
 
 GEOMS = {

@@ -27,7 +27,7 @@ from dcnv2_amd import _C
 from dcnv2_amd.workloads import CONFIGS, make_inputs
 from independent import forward_backward_gs, sample_positions
 from oracle import oracle
-from util import GRADS, TOL, load_fixture, rel_err
+from util import GRADS, TOL, check, load_fixture
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
@@ -56,12 +56,6 @@ def oracle_forward(t, geo):
 
 def oracle_backward(t, geo):
     return oracle.dcn_backward(*(t[k] for k in IN5), t["grad_output"], pos_f32=True, **geo)
-
-
-def check(name, got, ref, tol):
-    e = rel_err(got, ref)
-    print(f"  {name}: rel_err={e:.3e} (tol {tol:.0e})")
-    assert e <= tol, f"{name}: {e:.3e} > {tol:.0e}"
 
 
 @functools.lru_cache(maxsize=4)
@@ -342,3 +336,73 @@ def test_torchvision_signature_nonsquare(dtype):
     got = [dev[k].grad for k in ("input", "offset", "mask", "weight", "bias")]
     for name, a, r in zip(GRADS, got, oracle_backward(t, geo)):
         check(name, a, r, TOL[dtype])
+
+
+# --------------------------------------------------------------------------- grad_input buckets
+@pytest.mark.parametrize("k", [5, 7], ids=["5x5", "7x7"])
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+def test_large_kernel_stride1(dtype, k):
+    """5x5 and 7x7 kernels at stride 1: an interior 16x16 cell tile receives
+    about 256*k*k samples (6400, 12544), more than one gather batch holds
+    (4096), so every such bucket is gathered in several batches."""
+    w, t = _small(dtype, B=2, C=64, H=48, W=48, Cout=32, k=k, p=k // 2, G=1, osc=2.0)
+    out = gpu_forward(t, w.geometry())
+    grads = gpu_backward(t, w.geometry())
+    torch.cuda.synchronize()
+    check("output", out, oracle_forward(t, w.geometry()), TOL[dtype])
+    for name, g, r in zip(GRADS, grads, oracle_backward(t, w.geometry())):
+        check(name, g, r, TOL[dtype])
+
+
+def _clustered(dtype, B, C, H, W, Cout, G, target, spread, seed):
+    """Offsets that move every sample of every tap to within +-spread pixels
+    of `target` (the clustering that learned offsets converging on an object
+    produce): all samples of an image land in one or a few cell tiles."""
+    w, t = _small(dtype, B=B, C=C, H=H, W=W, Cout=Cout, G=G, seed=seed)
+    gen = torch.Generator().manual_seed(seed + 100)
+    kk = w.k * w.k
+    oy = torch.arange(w.Ho).view(1, 1, -1, 1) * w.stride - w.pad
+    ox = torch.arange(w.Wo).view(1, 1, 1, -1) * w.stride - w.pad
+    ki = (torch.arange(kk) // w.k).view(1, -1, 1, 1) * w.dil
+    kj = (torch.arange(kk) % w.k).view(1, -1, 1, 1) * w.dil
+    shape = (B, G * kk, w.Ho, w.Wo)
+    dy = (target[0] - (oy + ki.repeat(1, G, 1, 1))).expand(shape) + \
+        (torch.rand(shape, generator=gen) * 2 - 1) * spread
+    dx = (target[1] - (ox + kj.repeat(1, G, 1, 1))).expand(shape) + \
+        (torch.rand(shape, generator=gen) * 2 - 1) * spread
+    off = torch.stack([dy, dx], 2).reshape(B, 2 * G * kk, w.Ho, w.Wo)
+    t["offset"] = off.to(dtype)
+    return w, t
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+def test_clustered_offsets_one_bucket(dtype):
+    """Every sample of an image pulled into a 7x7-pixel patch around (20.3,
+    17.6): about 9*1600*2 = 28800 samples share one or two buckets (several
+    gather batches each) while the other buckets are empty.  All five
+    gradients against the oracle."""
+    w, t = _clustered(dtype, B=1, C=64, H=40, W=40, Cout=32, G=2, target=(20.3, 17.6),
+                      spread=3.0, seed=21)
+    out = gpu_forward(t, w.geometry())
+    grads = gpu_backward(t, w.geometry())
+    torch.cuda.synchronize()
+    check("output", out, oracle_forward(t, w.geometry()), TOL[dtype])
+    for name, g, r in zip(GRADS, grads, oracle_backward(t, w.geometry())):
+        check(name, g, r, TOL[dtype])
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16], ids=["float32", "float16"])
+def test_bucket_table_beyond_lds(dtype):
+    """An image of 2063 x 2063 pixels has 129 x 129 = 16641 cell tiles, more
+    than the bucket pre-pass's LDS table holds (16384), so the count and place
+    passes take their global-atomic variant.  1x1 kernel, 4 channels, offsets
+    N(0, 2): all five gradients against the oracle."""
+    w, t = _small(dtype, B=1, C=4, H=2063, W=2063, Cout=4, k=1, p=0, G=1, osc=2.0, seed=5)
+    out = gpu_forward(t, w.geometry())
+    grads = gpu_backward(t, w.geometry())
+    torch.cuda.synchronize()
+    check("output", out, oracle_forward(t, w.geometry()), TOL[dtype])
+    for name, g, r in zip(GRADS, grads, oracle_backward(t, w.geometry())):
+        check(name, g, r, TOL[dtype])
+    del out, grads
+    torch.cuda.empty_cache()

@@ -27,16 +27,10 @@ from dcnv2_amd.dcn_v2_mm import DCN
 from independent import deform_conv2d_gs
 from oracle import oracle
 from train import build_net, synthetic_batch, train_step
-from util import TOL, rel_err
+from util import TOL, check
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
-
-
-def check(name, got, ref, tol):
-    e = rel_err(got, ref)
-    print(f"  {name}: rel_err={e:.3e} (tol {tol:.0e})")
-    assert e <= tol, f"{name}: {e:.3e} > {tol:.0e}"
 
 
 @pytest.mark.parametrize("fused", [True, False], ids=["fused_om", "separate"])

@@ -1,6 +1,8 @@
 """Shared helpers of the test suite."""
 from __future__ import annotations
 
+import os
+
 import numpy as np
 import torch
 
@@ -28,3 +30,22 @@ def load_fixture(path):
     s, p, dl, G = (int(v) for v in d["geometry"])
     arrays = {k: torch.from_numpy(d[k]) for k in d.files if k != "geometry"}
     return arrays, dict(stride=s, padding=p, dilation=dl, deformable_groups=G)
+
+
+# Every GPU parity comparison (test id, tensor, max relative error, tolerance),
+# written to $DCN2_PARITY_LOG as JSON at the end of the session when that is
+# set (tests/conftest.py), so the margins of a run can be tabulated.
+PARITY_LOG: list = []
+
+
+def record(name: str, err: float, tol: float) -> None:
+    test = os.environ.get("PYTEST_CURRENT_TEST", "?").split(" ")[0]
+    PARITY_LOG.append({"test": test, "tensor": name, "rel_err": err, "tol": tol})
+
+
+def check(name, got, ref, tol):
+    """Asserts max|got - ref| / max|ref| <= tol, printing and recording it."""
+    e = rel_err(got, ref)
+    record(name, e, tol)
+    print(f"  {name}: rel_err={e:.3e} (tol {tol:.0e})")
+    assert e <= tol, f"{name}: {e:.3e} > {tol:.0e}"
