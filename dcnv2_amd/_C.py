@@ -76,6 +76,8 @@ def lib() -> ctypes.CDLL:
             L.dcn2_forward_om.restype = ctypes.c_int
             L.dcn2_backward_om.argtypes = [dp] + [vp] * 9 + [sz, vp]
             L.dcn2_backward_om.restype = ctypes.c_int
+            L.dcn2_forward_noalloc.argtypes = [dp] + [vp] * 7
+            L.dcn2_forward_noalloc.restype = ctypes.c_int
             L.dcn2_last_error.argtypes = []
             L.dcn2_last_error.restype = ctypes.c_char_p
             L.dcn2_version.argtypes = []

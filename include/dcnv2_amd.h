@@ -128,6 +128,23 @@ DCN2_API int dcn2_backward_om(const dcn2_desc *d, const void *input, const void 
                      const void *grad_output, void *grad_input, void *grad_om, void *grad_weight,
                      void *grad_bias, void *workspace, size_t workspace_bytes, void *stream);
 
+/* Forward without allocation or workspace.  No counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Arguments
+ * and results are those of dcn2_forward; the workspace is a static device
+ * array of DCN2_NOALLOC_SCRATCH_BYTES that the library holds on every GPU it
+ * runs on until the process ends (its address is looked up once per device on
+ * the first call there).  A problem whose dcn2_forward_workspace_bytes()
+ * exceeds that size is rejected with DCN2_EWORKSPACE before anything is
+ * launched.  Every call on one GPU uses the same array: calls that overlap on
+ * one GPU (concurrent streams or threads) race and must be serialised by the
+ * caller; consecutive calls on one stream are safe.  Nothing is allocated and
+ * nothing synchronises. */
+#define DCN2_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+DCN2_API int dcn2_forward_noalloc(const dcn2_desc *d, const void *input, const void *weight,
+                                  const void *mask, const void *offset, const void *bias,
+                                  void *output, void *stream);
+
 /* Per-stage kernel timing (no counterpart in the reference, whose timing loops
  * live inside its forward, com_2buffer_cpasyc.cu:334-392).  While enabled on
  * the calling thread, every stage of dcn2_forward / dcn2_backward is bracketed
