@@ -24,10 +24,11 @@ oracle (oracle/dcn_oracle.c, OpenMP) on bounded samples of c0, c1 and c2.
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 
 Profiling aids (not part of the headline line's workload): ``--mode fwd`` runs
-only the c1 forward loops (for ``rocprofv3 --pmc`` passes), ``--mode c2``
-only the c2 forward+backward loop, ``--copy-mib N`` first runs one plain
-device-to-device copy of N MiB, the calibration kernel whose FETCH_SIZE /
-WRITE_SIZE readings scale the kernels' counters.
+only the c1 forward loops (for ``rocprofv3 --pmc`` passes), ``--mode c2`` /
+``c3`` / ``c4`` only that configuration's forward+backward loop, and
+``--copy-mib N`` first runs one plain device-to-device copy of N MiB, the
+calibration kernel whose FETCH_SIZE / WRITE_SIZE readings scale the kernels'
+counters.
 """
 from __future__ import annotations
 
@@ -211,7 +212,7 @@ def main():
     ap.add_argument("--settle-ms", type=float, default=400.0)
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--mode", choices=("full", "fwd", "c2"), default="full")
+    ap.add_argument("--mode", choices=("full", "fwd", "c2", "c3", "c4"), default="full")
     ap.add_argument("--copy-mib", type=int, default=0)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -250,12 +251,13 @@ def main():
         torch.cuda.synchronize()
         del src, dst
 
-    if args.mode == "c2":
-        t2 = load(c2)
-        f = fwd_bwd_fn(c2, t2)
+    if args.mode in ("c2", "c3", "c4"):
+        w = CONFIGS[int(args.mode[1])]
+        t = load(w)
+        f = fwd_bwd_fn(w, t)
         _warm(f, args.warmup, args.settle_ms, torch)
         ms = _events_ms(f, args.steps, torch)
-        print(json.dumps({"mode": "c2", "fwd_bwd_ms": round(ms, 5)}), flush=True)
+        print(json.dumps({"mode": args.mode, "fwd_bwd_ms": round(ms, 5)}), flush=True)
         return
 
     t1 = load(c1)

@@ -97,6 +97,11 @@ int make_geo(const dcn2_desc *d, Geo &g) {
         (long long)g.B * g.G * g.KK * g.Ho * g.Wo >= lim || g.H > 32767 || g.W > 32767)
         return fail(DCN2_ERANGE, "dcn2: problem exceeds the 32-bit per-image index range");
     g.Kp = (int)Kp;
+    // the forward's sampler addresses one image of xt with 32-bit byte offsets
+    // and marks corners outside the image with the offset just past it
+    if (((long long)g.H * g.W + 1) * g.cs * g.esz + 256 >= 0x100000000LL)
+        return fail(DCN2_ERANGE, "dcn2: one image of %d x %d x %d channels exceeds the 32-bit "
+                    "byte range", g.H, g.W, g.cs);
     {
         const GatherGeo gg = gather_geometry(g);
         if (gg.batch_bytes >= gg.max_batch_bytes)

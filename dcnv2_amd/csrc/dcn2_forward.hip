@@ -339,7 +339,10 @@ template <typename T> struct Blend8 {
 // Rows of the LDS bias table of the warp-specialised forward.
 constexpr int kBiasRows = 1024;
 
-template <typename T, int IB, bool MASK>
+// MASK: 0 no mask (all ones), 1 mask values, 2 mask logits (sigmoid on load);
+// a compile-time mode keeps the descriptor code free of branches, so it can
+// be scheduled between the MFMAs.
+template <typename T, int IB, int MASK>
 __global__ __launch_bounds__(512) void dcn2_fwd_ws_kernel(const FwdParams p) {
     using M = Mma<T>;
     using frag = typename M::frag;
@@ -431,6 +434,12 @@ __global__ __launch_bounds__(512) void dcn2_fwd_ws_kernel(const FwdParams p) {
     };
     auto no_tile = [] {};
 
+    // Byte offset the descriptors give a corner outside the image: past the
+    // image's channels-last input, so the sampler's buffer load returns 0
+    // without a memory access (the host keeps it and every in-image offset
+    // plus the chunk's channel offset below 2^32).
+    const uint32_t img_bytes = (uint32_t)((size_t)p.H * p.W * cs * sizeof(T));
+
     if (mfma_role) {
         // ------------------------------------------------------------ MFMA waves
         // Two sets of A fragments: the set of chunk g+1 is loaded at the top
@@ -438,6 +447,69 @@ __global__ __launch_bounds__(512) void dcn2_fwd_ws_kernel(const FwdParams p) {
         // land.  (Left to itself the scheduler sinks the loads to the end of
         // the step, which exposes their full latency every step.)
         frag a[2][IB][NKS];
+
+        // The MFMA waves also compute the bilinear descriptors, three chunks
+        // ahead, into the LDS ring: their instruction stream waits on the
+        // matrix core most of the step, while a sampler wave can issue only
+        // one instruction per cycle slot and is the longer of the two roles.
+        // Threads 2p, 2p+1 (st = rw*64 + lane) both evaluate pixel p of the
+        // descriptor chunk and write half of it each (no divergent branch in
+        // the step, so the compiler's load counting stays exact).
+        const int st = rw * 64 + lane;  // 0..255
+        const int dpix = st >> 1, dhalf = st & 1;
+        // Offset/mask bits of one chunk for pixel dpix (kept raw until used)
+        // with the pixel's output position in the tile they belong to: loaded
+        // in step g for chunk g+4, after the descriptors of chunk g+3 have
+        // used the previous load, so each load has a whole step to land.
+        struct OmBits {
+            int n, by, bx;
+            T dy, dx, m;
+        };
+        OmBits om;
+        // Per-tile state of the offset-load point: offset/mask planes of the
+        // image and the output position of pixel dpix.
+        const T *offb, *mskb;
+        int n_t, nn_t, by_t, bx_t;
+        auto set_om_tile = [&](const Cursor &c) __attribute__((always_inline)) {
+            offb = (const T *)p.offset + (size_t)c.b * p.off_bs;
+            mskb = MASK ? (const T *)p.mask + (size_t)c.b * p.msk_bs : nullptr;
+            n_t = c.n0 + dpix;
+            nn_t = n_t < N ? n_t : 0;
+            const int oy = nn_t / p.Wo, ox = nn_t - oy * p.Wo;
+            by_t = oy * p.sh - p.ph;
+            bx_t = ox * p.sw - p.pw;
+        };
+        auto load_om = [&](const Cursor &c) __attribute__((always_inline)) {
+            const int plane = tabi[4 * c.ch];
+            om.n = n_t;
+            om.by = by_t;
+            om.bx = bx_t;
+            const size_t ob = (size_t)plane * 2 * N + nn_t;
+            om.dy = offb[ob];
+            om.dx = offb[ob + N];
+            if constexpr (MASK) om.m = mskb[(size_t)plane * N + nn_t];
+        };
+        // descriptor of pixel dpix at cursor c from om -> ring slot R (this
+        // thread's half); corner offsets in bytes, img_bytes outside
+        auto put_desc = [&](int R, const Cursor &c) __attribute__((always_inline)) {
+            const ChunkEnt e = tab_ent(c.ch);
+            const float y = (float)(om.by + e.y) + to_f32(om.dy);
+            const float x = (float)(om.bx + e.z) + to_f32(om.dx);
+            float mv = 1.0f;
+            if constexpr (MASK == 1) mv = to_f32(om.m);
+            if constexpr (MASK == 2) mv = 1.0f / (1.0f + __expf(-to_f32(om.m)));
+            mv = om.n < N ? mv : 0.0f;  // pixels past N sample 0
+            const SamplePos sp = sample_pos(y, x, p.H, p.W);
+            const Corners cr = make_corners(sp, mv, p.W, cs);
+            const uint4 wq = Blend8<T>::weights(cr.w);
+            const bool vy = dhalf ? sp.vy1 : sp.vy0;
+            RingHalf hd;
+            hd.o0 = vy && sp.vx0 ? (dhalf ? cr.off[2] : cr.off[0]) * (int)sizeof(T) : (int)img_bytes;
+            hd.o1 = vy && sp.vx1 ? (dhalf ? cr.off[3] : cr.off[1]) * (int)sizeof(T) : (int)img_bytes;
+            hd.w0 = dhalf ? wq.z : wq.x;
+            hd.w1 = dhalf ? wq.w : wq.y;
+            ring[R][dpix].h[dhalf] = hd;
+        };
         f32x16 acc[IB][JB];
         const T *bias = (const T *)p.bias;
         const T *wbase = (const T *)p.wp + (size_t)lane * KPL;
@@ -452,14 +524,15 @@ __global__ __launch_bounds__(512) void dcn2_fwd_ws_kernel(const FwdParams p) {
         // operands have the same register layout), so lane l holds output
         // row m = i*32 + l%32 and, in acc[r], pixel n = j*32 + 8*(r/4) +
         // 4*(l/32) + r%4: four consecutive pixels of one row per r/4.
+        // (filled as 64-bit register pairs: half the move instructions)
         auto init_acc = [&](int m0) __attribute__((always_inline)) {
+            typedef unsigned long long u64x8 __attribute__((ext_vector_type(8)));
 #pragma unroll
             for (int i = 0; i < IB; ++i) {
-                const float bv = sBias[m0 + rw * ROWS + i * 32 + (lane & 31)];
+                const uint32_t bb = __float_as_uint(sBias[m0 + rw * ROWS + i * 32 + (lane & 31)]);
+                const unsigned long long b2 = ((unsigned long long)bb << 32) | bb;
 #pragma unroll
-                for (int j = 0; j < JB; ++j)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) acc[i][j][r] = bv;
+                for (int j = 0; j < JB; ++j) acc[i][j] = __builtin_bit_cast(f32x16, u64x8(b2));
             }
         };
         // A fragments at cursor c: rows m0 + rw*ROWS + i*32 + lane%32 of chunk
@@ -500,73 +573,103 @@ __global__ __launch_bounds__(512) void dcn2_fwd_ws_kernel(const FwdParams p) {
                         acc[i][j] = M::mma(bf[ks & 1][j], a[SET][i][ks], acc[i][j]);
             }
         };
-        // Output tile of this wave: round to T, stage in LDS, 16-byte row stores.
+        // Output tile of this wave: round to T, stage in LDS, then 16-byte
+        // row stores (or, for an output whose rows 16-byte stores cannot
+        // cover, a plain loop of element stores from the staged tile).
         auto store_tile = [&](const Cursor &c) __attribute__((always_inline)) {
             T *out = (T *)p.out + (size_t)c.b * p.Cout * N;
+            // four consecutive pixels of a row -> one 8-byte LDS write
+            T(&so)[ROWS][LDO] = sO[rw];
+#pragma unroll
+            for (int i = 0; i < IB; ++i)
+#pragma unroll
+                for (int j = 0; j < JB; ++j)
+#pragma unroll
+                    for (int rq = 0; rq < 4; ++rq) {
+                        T v4[4];
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) v4[e] = from_f32<T>(acc[i][j][rq * 4 + e]);
+                        *reinterpret_cast<uint2 *>(&so[i * 32 + (lane & 31)][j * 32 + 8 * rq + 4 * (lane >> 5)]) =
+                            __builtin_bit_cast(uint2, v4);
+                    }
             if (p.out_vec) {
-                // four consecutive pixels of a row -> one 8-byte LDS write
-                T(&so)[ROWS][LDO] = sO[rw];
-#pragma unroll
-                for (int i = 0; i < IB; ++i)
-#pragma unroll
-                    for (int j = 0; j < JB; ++j)
-#pragma unroll
-                        for (int rq = 0; rq < 4; ++rq) {
-                            T v4[4];
-#pragma unroll
-                            for (int e = 0; e < 4; ++e) v4[e] = from_f32<T>(acc[i][j][rq * 4 + e]);
-                            *reinterpret_cast<uint2 *>(&so[i * 32 + (lane & 31)][j * 32 + 8 * rq + 4 * (lane >> 5)]) =
-                                __builtin_bit_cast(uint2, v4);
-                        }
-                // a wave instruction covers 64 / SEG whole rows of SEG 16-byte segments
+                // a wave instruction covers 64 / SEG whole rows of SEG 16-byte
+                // segments; buffer stores over the image's output, a segment
+                // outside it (m >= Cout or n >= N; N % 8 == 0, so a segment is
+                // all in or all out) gets an offset past the buffer and is
+                // dropped, so no store sits in a branch
                 constexpr int SEG = BN / 8, RPI = 64 / SEG;
                 const int seg = lane % SEG, r0 = lane / SEG;
                 const int n = c.n0 + seg * 8;
-                T *orow = out + (size_t)(c.m0 + rw * ROWS + r0) * N + n;
+                const uint32_t obytes = (uint32_t)((size_t)p.Cout * N * sizeof(T));
+                const __amdgpu_buffer_rsrc_t ors =
+                    __builtin_amdgcn_make_buffer_rsrc(out, (short)0, (int)obytes, 0x00020000);
 #pragma unroll
                 for (int it = 0; it < ROWS / RPI; ++it) {
                     const int m = c.m0 + rw * ROWS + it * RPI + r0;
                     const uint4 v = *reinterpret_cast<const uint4 *>(&so[it * RPI + r0][seg * 8]);
-                    if (m < p.Cout && n < N)  // N % 8 == 0: a segment is all in or all out
-                        *reinterpret_cast<uint4 *>(orow + (size_t)it * RPI * N) = v;
+                    const uint32_t off = m < p.Cout && n < N
+                                             ? (uint32_t)(((unsigned)m * (unsigned)N + (unsigned)n) * sizeof(T))
+                                             : obytes;
+                    typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+                    __builtin_amdgcn_raw_buffer_store_b128(u32x4{v.x, v.y, v.z, v.w}, ors, (int)off, 0, 0);
                 }
             } else {
-#pragma unroll
-                for (int i = 0; i < IB; ++i) {
-                    const int m = c.m0 + rw * ROWS + i * 32 + (lane & 31);
-                    if (m >= p.Cout) continue;
-#pragma unroll
-                    for (int j = 0; j < JB; ++j)
-#pragma unroll
-                        for (int r = 0; r < 16; ++r) {
-                            const int n = c.n0 + j * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                            if (n < N) out[(size_t)m * N + n] = from_f32<T>(acc[i][j][r]);
-                        }
+#pragma unroll 1
+                for (int idx = lane; idx < ROWS * BN; idx += 64) {
+                    const int row = idx / BN, col = idx % BN;
+                    const int m = c.m0 + rw * ROWS + row, n = c.n0 + col;
+                    if (m < p.Cout && n < N) out[(size_t)m * N + n] = so[row][col];
                 }
             }
         };
-        Cursor cur = cursor(0), nxt = cursor(1);  // chunk being multiplied, chunk loaded next
+        // chunk being multiplied, chunk loaded next, descriptor chunk, offset chunk
+        Cursor cur = cursor(0), nxt = cursor(1), cd = cursor(3), co = cursor(4);
+        // Step g (S_ = g % 2): A fragments of g+1 first, then the MFMAs of g
+        // with the descriptors of g+3 (ring slot (g+3) % 2, from the offsets
+        // loaded one step earlier) in between, then the offsets of g+4.
         auto step = [&](auto s_c) __attribute__((always_inline)) {
             constexpr int S_ = decltype(s_c)::value;
             load_a(std::integral_constant<int, S_ ^ 1>{}, nxt);
             __builtin_amdgcn_sched_barrier(0);
             mfma_stage(std::integral_constant<int, S_>{});
+            put_desc(S_ ^ 1, cd);
+            load_om(co);
             if (cur.j == last) {  // tile done: write it, start the next one at its bias
                 store_tile(cur);
                 if (nxt.k < my_tiles) init_acc(nxt.m0);
             }
             advance(cur, no_tile);
             advance(nxt, [&] { set_wrow(nxt); });
+            advance(cd, no_tile);
+            advance(co, [&] { set_om_tile(co); });
             __syncthreads();
         };
         init_acc(cur.m0);
         set_wrow(cur);
         load_a(std::integral_constant<int, 0>{}, cur);
         set_wrow(nxt);
-        // prologue: the samplers fill the descriptor ring and stage 0
-        __syncthreads();
-        __syncthreads();
-        __syncthreads();
+        // prologue: descriptors of chunks 0 and 1 (ring slots 0, 1) before
+        // the first barrier; chunk 2 into slot 0 once the samplers have read
+        // it (second barrier); offsets of chunk 3 for step 0
+        {
+            const Cursor c0 = cursor(0), c1 = cursor(1), c2 = cursor(2), c3 = cursor(3);
+            set_om_tile(c0);
+            load_om(c0);
+            put_desc(0, c0);
+            set_om_tile(c1);
+            load_om(c1);
+            put_desc(1, c1);
+            set_om_tile(c2);
+            load_om(c2);
+            __syncthreads();
+            __syncthreads();
+            put_desc(0, c2);
+            set_om_tile(c3);
+            load_om(c3);
+            __syncthreads();
+            set_om_tile(co);
+        }
         int g = 0;
         for (; g + 1 < S; g += 2) {
             step(std::integral_constant<int, 0>{});
@@ -575,77 +678,25 @@ __global__ __launch_bounds__(512) void dcn2_fwd_ws_kernel(const FwdParams p) {
         if (g < S) step(std::integral_constant<int, 0>{});
     } else {
         // --------------------------------------------------------- sampler waves
-        const int st = rw * 64 + lane;                // 0..255
         const int cg = lane & 7;                      // 16-byte piece (8 channels) of a corner
         const int pbase = rw * 32 + (lane >> 3);      // slot s covers pixel pbase + 8*s
-        // descriptor work: threads 2p, 2p+1 both evaluate pixel p of the next
-        // descriptor chunk and write half of it each (no divergent branch in
-        // the step, so the compiler's load counting stays exact)
-        const int dpix = st >> 1, dhalf = st & 1;
         uint4 raw[2][4][4];   // [set][slot][corner]
         uint4 wts[2][4];      // [set][slot] corner weights
-        // offsets/mask of the next descriptor chunk (raw bits) with the output
-        // position of pixel dpix in the tile they belong to
-        int n_om, by_om, bx_om;
-        T dy_om, dx_om, m_om;
 
-        // Per-tile state of the offset-load point: offset/mask planes of the
-        // image and the output position of pixel dpix.
-        const T *offb, *mskb;
-        int n_t, nn_t, by_t, bx_t;
-        auto set_om_tile = [&](const Cursor &c) __attribute__((always_inline)) {
-            offb = (const T *)p.offset + (size_t)c.b * p.off_bs;
-            mskb = MASK ? (const T *)p.mask + (size_t)c.b * p.msk_bs : nullptr;
-            n_t = c.n0 + dpix;
-            nn_t = n_t < N ? n_t : 0;
-            const int oy = nn_t / p.Wo, ox = nn_t - oy * p.Wo;
-            by_t = oy * p.sh - p.ph;
-            bx_t = ox * p.sw - p.pw;
-        };
         // Per-tile state of the gather point: a buffer resource over the
         // image's channels-last input (byte offsets are 32-bit, and a read
         // past the image returns 0).
-        const uint32_t img_bytes = (uint32_t)((size_t)p.H * p.W * cs * sizeof(T));
         __amdgpu_buffer_rsrc_t xrs;
         auto set_x_tile = [&](const Cursor &c) __attribute__((always_inline)) {
             const T *xb = (const T *)p.xt + (size_t)c.b * p.H * p.W * cs;
             xrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<T *>(xb), (short)0, (int)img_bytes,
                                                     0x00020000);
         };
-
-        // offset/mask bits of pixel dpix at cursor c (kept raw until used)
-        auto load_om = [&](const Cursor &c) __attribute__((always_inline)) {
-            const int plane = tabi[4 * c.ch];
-            n_om = n_t;
-            by_om = by_t;
-            bx_om = bx_t;
-            const size_t ob = (size_t)plane * 2 * N + nn_t;
-            dy_om = offb[ob];
-            dx_om = offb[ob + N];
-            if constexpr (MASK) m_om = mskb[(size_t)plane * N + nn_t];
-        };
-        // descriptor of pixel dpix at cursor c -> ring slot R (this thread's
-        // half); corner offsets in bytes
-        auto put_desc = [&](int R, const Cursor &c) __attribute__((always_inline)) {
-            const ChunkEnt e = tab_ent(c.ch);
-            const float y = (float)(by_om + e.y) + to_f32(dy_om);
-            const float x = (float)(bx_om + e.z) + to_f32(dx_om);
-            float mv = 1.0f;
-            if constexpr (MASK) mv = mask_value(to_f32(m_om), p.msk_logit);
-            mv = n_om < N ? mv : 0.0f;  // pixels past N sample 0
-            const Corners cr = make_corners(sample_pos(y, x, p.H, p.W), mv, p.W, cs);
-            const uint4 wq = Blend8<T>::weights(cr.w);
-            RingHalf hd;
-            hd.o0 = (dhalf ? cr.off[2] : cr.off[0]) * (int)sizeof(T);
-            hd.o1 = (dhalf ? cr.off[3] : cr.off[1]) * (int)sizeof(T);
-            hd.w0 = dhalf ? wq.z : wq.x;
-            hd.w1 = dhalf ? wq.w : wq.y;
-            ring[R][dpix].h[dhalf] = hd;
-        };
         // corner gathers of the four slots at cursor c (descriptors in ring slot R) -> set SET
         typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
         auto gather = [&](int off, int soff) __attribute__((always_inline)) {
-            const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(xrs, off + cg * 16, soff, 0);
+            const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(
+                xrs, (int)((unsigned)off + (unsigned)cg * 16u), soff, 0);
             return make_uint4(v.x, v.y, v.z, v.w);
         };
         auto issue = [&](auto set_c, int R, const Cursor &c) __attribute__((always_inline)) {
@@ -670,54 +721,37 @@ __global__ __launch_bounds__(512) void dcn2_fwd_ws_kernel(const FwdParams p) {
         };
         // Chunk c uses ring slot, gather set and LDS stage c & 1.  Step g:
         //   gathers of g+2 (ring (g+2)&1) -> set g&1;
-        //   descriptors of g+3 -> ring (g+3)&1, then the offsets of g+4;
         //   blend of g+1 (set (g+1)&1) -> stage (g+1)&1;
-        // with the gathers interleaved into the VALU work so that the vector
+        // with the gathers interleaved into the blend so that the vector
         // memory pipe is fed through the whole step.
-        Cursor ci = cursor(2), cd = cursor(3), co = cursor(4);  // issue, descriptor, offset points
+        Cursor ci = cursor(2);  // issue point
         auto step = [&](auto s_c) __attribute__((always_inline)) {
             constexpr int S_ = decltype(s_c)::value;
             issue(std::integral_constant<int, S_>{}, S_, ci);
-            put_desc(S_ ^ 1, cd);
-            load_om(co);
             blend_store(std::integral_constant<int, S_ ^ 1>{});
             __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);  // ring reads
 #pragma unroll
-            for (int q = 0; q < 5; ++q) {
-                __builtin_amdgcn_sched_group_barrier(0x020, 4, 0);  // gathers / offset loads
-                __builtin_amdgcn_sched_group_barrier(0x002, 20, 0);  // VALU
+            for (int q = 0; q < 4; ++q) {
+                __builtin_amdgcn_sched_group_barrier(0x020, 4, 0);  // gathers
+                __builtin_amdgcn_sched_group_barrier(0x002, 30, 0);  // VALU
             }
             advance(ci, [&] { set_x_tile(ci); });
-            advance(cd, no_tile);
-            advance(co, [&] { set_om_tile(co); });
             __syncthreads();
         };
         // (S >= 1: the grid never exceeds the tile count)
-        // ring <- descriptors of chunks 0 and 1; offsets of chunk 2
+        // after the first barrier the ring holds the descriptors of chunks 0
+        // and 1
         {
-            Cursor c0 = cursor(0), c1 = cursor(1), c2 = cursor(2), c3 = cursor(3);
-            set_om_tile(c0);
-            load_om(c0);
-            put_desc(0, c0);
-            set_om_tile(c1);
-            load_om(c1);
-            put_desc(1, c1);
-            set_om_tile(c2);
-            load_om(c2);
+            const Cursor c0 = cursor(0), c1 = cursor(1);
             __syncthreads();
             set_x_tile(c0);
             issue(std::integral_constant<int, 0>{}, 0, c0);
             __syncthreads();  // ring slot 0 is read: chunk 2 may replace chunk 0
-            put_desc(0, c2);
-            set_om_tile(c3);
-            load_om(c3);
-            __builtin_amdgcn_sched_barrier(0);
             set_x_tile(c1);
             issue(std::integral_constant<int, 1>{}, 1, c1);
             blend_store(std::integral_constant<int, 0>{});
             __syncthreads();
             set_x_tile(ci);
-            set_om_tile(co);
         }
         int g = 0;
         for (; g + 1 < S; g += 2) {
@@ -757,10 +791,12 @@ static hipError_t launch_fwd_ws(const Geo &g, const FwdParams &p0, hipStream_t s
         ncu <= 0)
         ncu = 256;
     const int grid = p.tiles < ncu ? p.tiles : ncu;
-    if (p.mask)
-        dcn2_fwd_ws_kernel<T, IB, true><<<grid, 512, 0, s>>>(p);
+    if (p.mask && p.msk_logit)
+        dcn2_fwd_ws_kernel<T, IB, 2><<<grid, 512, 0, s>>>(p);
+    else if (p.mask)
+        dcn2_fwd_ws_kernel<T, IB, 1><<<grid, 512, 0, s>>>(p);
     else
-        dcn2_fwd_ws_kernel<T, IB, false><<<grid, 512, 0, s>>>(p);
+        dcn2_fwd_ws_kernel<T, IB, 0><<<grid, 512, 0, s>>>(p);
     return hipGetLastError();
 }
 
@@ -769,13 +805,13 @@ static hipError_t launch_fwd_ws(const Geo &g, const FwdParams &p0, hipStream_t s
 template <typename T, int IB>
 static bool ws_two_waves_per_simd() {
     static const bool ok = [] {
-        hipFuncAttributes a;
-        if (hipFuncGetAttributes(&a, reinterpret_cast<const void *>(&dcn2_fwd_ws_kernel<T, IB, true>)) !=
-                hipSuccess || a.numRegs <= 512 / 3)
-            return false;
-        if (hipFuncGetAttributes(&a, reinterpret_cast<const void *>(&dcn2_fwd_ws_kernel<T, IB, false>)) !=
-                hipSuccess || a.numRegs <= 512 / 3)
-            return false;
+        const void *fns[3] = {reinterpret_cast<const void *>(&dcn2_fwd_ws_kernel<T, IB, 0>),
+                              reinterpret_cast<const void *>(&dcn2_fwd_ws_kernel<T, IB, 1>),
+                              reinterpret_cast<const void *>(&dcn2_fwd_ws_kernel<T, IB, 2>)};
+        for (const void *fn : fns) {
+            hipFuncAttributes a;
+            if (hipFuncGetAttributes(&a, fn) != hipSuccess || a.numRegs <= 512 / 3) return false;
+        }
         return true;
     }();
     return ok;
