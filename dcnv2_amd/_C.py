@@ -14,8 +14,9 @@ Extensions over the reference, all trailing and optional: ``dilation_h``,
 them but never forwards them, ``dcn_v2_mm.py:67-68, 94-102``); fp16/bf16 as
 well as fp32 tensors; ``mask`` and ``bias`` may be ``None``; a weight of shape
 ``[Cout, C/groups, kh, kw]`` selects torchvision's weight groups; a
-``channels_last`` input is read without a layout copy, and its ``grad_input``
-comes back channels_last (the output stays contiguous NCHW).
+``channels_last`` input is read without a layout copy, its output and
+``grad_input`` come back channels_last (as torch's own convolutions propagate
+the memory format), and a ``channels_last`` ``grad_output`` is read in place.
 
 Errors: any invalid device, dtype, shape or launch failure raises
 ``RuntimeError``, as the reference's ``AT_ASSERTM`` checks do
@@ -41,7 +42,7 @@ class Desc(ctypes.Structure):
     _fields_ = [(name, ctypes.c_int32) for name in (
         "batch", "in_channels", "height", "width", "out_channels", "kernel_h", "kernel_w",
         "stride_h", "stride_w", "pad_h", "pad_w", "dilation_h", "dilation_w",
-        "deformable_groups", "dtype", "weight_groups", "input_layout")]
+        "deformable_groups", "dtype", "weight_groups", "input_layout", "output_layout")]
 
 
 def library_path() -> str:
@@ -99,27 +100,37 @@ def _ptr(t):
     return None if t is None else ctypes.c_void_p(t.data_ptr())
 
 
-def _input_layout(input):
-    """(input, layout): a channels_last input (one that is not also contiguous
-    NCHW) is handed over as it is, with layout 1 (``DCN2_NHWC``); the kernels
-    read it in place when its channels need no padding.  Anything else becomes
-    contiguous NCHW, layout 0.  grad_input is returned in the same layout."""
+def _layout(t):
+    """(t, layout): a channels_last activation (one that is not also contiguous
+    NCHW) is handed over as it is, with layout 1 (``DCN2_NHWC``); anything
+    else becomes contiguous NCHW, layout 0.  The kernels read a channels_last
+    input in place when its channels need no padding, and a channels_last
+    grad_output always."""
     cl = torch.channels_last
-    if input.dim() == 4 and not input.is_contiguous() and input.is_contiguous(memory_format=cl):
-        if input.data_ptr() % 16:  # in-place reads use 16-byte loads
-            input = input.clone(memory_format=cl)
-        return input, 1
-    return input.contiguous(), 0
+    if t.dim() == 4 and not t.is_contiguous() and t.is_contiguous(memory_format=cl):
+        if t.data_ptr() % 16:  # in-place reads use 16-byte loads
+            t = t.clone(memory_format=cl)
+        return t, 1
+    return t.contiguous(), 0
+
+
+_input_layout = _layout
 
 
 def make_desc(input, weight, stride_h, stride_w, pad_h, pad_w, dilation_h, dilation_w,
-              deformable_groups, input_layout=0) -> Desc:
+              deformable_groups, input_layout=0, output_layout=0) -> Desc:
     B, C, H, W = (int(v) for v in input.shape)
     Cout, Cw, kh, kw = (int(v) for v in weight.shape)
     # weight groups follow from weight.shape[1], as in torchvision's deform_conv2d
     return Desc(B, C, H, W, Cout, kh, kw, int(stride_h), int(stride_w), int(pad_h), int(pad_w),
                 int(dilation_h), int(dilation_w), int(deformable_groups), _DTYPES[input.dtype],
-                C // Cw, int(input_layout))
+                C // Cw, int(input_layout), int(output_layout))
+
+
+def _empty_out(shape, like, layout):
+    """The output tensor: channels_last when `layout` is 1."""
+    fmt = torch.channels_last if layout else torch.contiguous_format
+    return torch.empty(shape, dtype=like.dtype, device=like.device, memory_format=fmt)
 
 
 def _validate(name, input, weight, mask, offset, bias, extra=()):
@@ -188,11 +199,10 @@ def dcn_v2_forward(input, weight, mask, offset, bias, stride_h, stride_w, pad_h,
     mask = mask.contiguous() if mask is not None else None
     bias = bias.contiguous() if bias is not None else None
     desc = make_desc(input, weight, stride_h, stride_w, pad_h, pad_w, dilation_h, dilation_w,
-                     deformable_groups, layout)
+                     deformable_groups, layout, layout)
     ho, wo = _geometry(name, desc, input, mask, offset)
     L = lib()
-    out = torch.empty((desc.batch, desc.out_channels, ho, wo), dtype=input.dtype,
-                      device=input.device)
+    out = _empty_out((desc.batch, desc.out_channels, ho, wo), input, layout)
     with torch.cuda.device(input.device):
         ws_buf, ws, ws_bytes = _workspace(L.dcn2_forward_workspace_bytes(ctypes.byref(desc)),
                                           input.device)
@@ -217,9 +227,9 @@ def dcn_v2_backward(input, weight, mask, offset, bias, grad_output, stride_h, st
     input, layout = _input_layout(input)
     weight, offset = weight.contiguous(), offset.contiguous()
     mask = mask.contiguous() if mask is not None else None
-    grad_output = grad_output.contiguous()
+    grad_output, go_layout = _layout(grad_output)
     desc = make_desc(input, weight, stride_h, stride_w, pad_h, pad_w, dilation_h, dilation_w,
-                     deformable_groups, layout)
+                     deformable_groups, layout, go_layout)
     ho, wo = _geometry(name, desc, input, mask, offset)
     if tuple(grad_output.shape) != (desc.batch, desc.out_channels, ho, wo):
         raise RuntimeError(f"{name}: grad_output shape {tuple(grad_output.shape)} != "
@@ -270,11 +280,10 @@ def dcn_v2_forward_om(input, weight, om, bias, stride_h, stride_w, pad_h, pad_w,
     weight, om = weight.contiguous(), om.contiguous()
     bias = bias.contiguous() if bias is not None else None
     desc = make_desc(input, weight, stride_h, stride_w, pad_h, pad_w, dilation_h, dilation_w,
-                     deformable_groups, layout)
+                     deformable_groups, layout, layout)
     ho, wo = _om_geometry(name, desc, om)
     L = lib()
-    out = torch.empty((desc.batch, desc.out_channels, ho, wo), dtype=input.dtype,
-                      device=input.device)
+    out = _empty_out((desc.batch, desc.out_channels, ho, wo), input, layout)
     with torch.cuda.device(input.device):
         ws_buf, ws, ws_bytes = _workspace(L.dcn2_forward_workspace_bytes(ctypes.byref(desc)),
                                           input.device)
@@ -297,9 +306,9 @@ def dcn_v2_backward_om(input, weight, om, bias, grad_output, stride_h, stride_w,
     _validate(name, input, weight, None, om, bias, extra=[("grad_output", grad_output)])
     input, layout = _input_layout(input)
     weight, om = weight.contiguous(), om.contiguous()
-    grad_output = grad_output.contiguous()
+    grad_output, go_layout = _layout(grad_output)
     desc = make_desc(input, weight, stride_h, stride_w, pad_h, pad_w, dilation_h, dilation_w,
-                     deformable_groups, layout)
+                     deformable_groups, layout, go_layout)
     ho, wo = _om_geometry(name, desc, om)
     if tuple(grad_output.shape) != (desc.batch, desc.out_channels, ho, wo):
         raise RuntimeError(f"{name}: grad_output shape {tuple(grad_output.shape)} != "

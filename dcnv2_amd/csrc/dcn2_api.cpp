@@ -54,6 +54,9 @@ int make_geo(const dcn2_desc *d, Geo &g) {
     g.nhwc = d->input_layout;
     if (g.nhwc != DCN2_NCHW && g.nhwc != DCN2_NHWC)
         return fail(DCN2_EINVAL, "dcn2: unsupported input_layout %d", g.nhwc);
+    g.out_nhwc = d->output_layout;
+    if (g.out_nhwc != DCN2_NCHW && g.out_nhwc != DCN2_NHWC)
+        return fail(DCN2_EINVAL, "dcn2: unsupported output_layout %d", g.out_nhwc);
     if (g.dtype != DCN2_F32 && g.dtype != DCN2_F16 && g.dtype != DCN2_BF16)
         return fail(DCN2_EINVAL, "dcn2: unsupported dtype code %d", g.dtype);
     if (g.B < 0 || g.C <= 0 || g.H <= 0 || g.W <= 0 || g.Cout <= 0)

@@ -38,7 +38,11 @@ struct BwdParams {
     float *gi_acc, *gw_acc, *gb_acc;
     int B, H, W, Cout, kh, kw, sh, sw, ph, pw, dh, dw, G, Cg, Cgp, Ho, Wo, Kp, Mp;
     int tiles_per_img, splits;
-    int go_vec;  // grad_output rows can be read with 16-byte loads (N % 8 == 0, aligned base)
+    int go_nhwc;  // grad_output is channels-last [B][Ho][Wo][Cout]
+    // grad_output can be read with 16-byte loads: 8 consecutive pixels of a row
+    // (NCHW, N % 8 == 0) or channels of a pixel (channels-last, Cout % 8 == 0),
+    // from a 16-byte aligned base
+    int go_vec;
     // grad_input gather: cell-tile buckets (see dcn2_gi_gather_kernel).  The
     // rows of all buckets are packed back to back, bucket k owning rows
     // [bstart[k], bstart[k+1]); there are at most B*G*KK*N of them (one per
@@ -383,15 +387,30 @@ __global__ __launch_bounds__(512) void dcn2_colgrad_kernel(const BwdParams p) {
 
     // gO fragments (MFMA B operand, [m][n]): n = this wave's 32-pixel block.
     frag gfr[NMS];
+    // (channels-last gO: a fragment's KPL rows of one pixel are contiguous,
+    // one 16-byte load for 2-byte types when Cout % 8 == 0)
     auto load_go = [&](int mc) __attribute__((always_inline)) {
         const int n = n0 + nb * 32 + (lane & 31);
 #pragma unroll
         for (int s = 0; s < NMS; ++s) {
+            const int m0s = mc * MCH + wr * MPW + s * KSTEP + (lane >> 5) * KPL;
+            if (p.go_nhwc) {
+                const T *gp = go + (size_t)n * p.Cout + m0s;
+                if (KPL == 8 && p.go_vec && n < N && m0s < p.Cout) {
+                    gfr[s] = *reinterpret_cast<const frag *>(gp);
+                } else {
 #pragma unroll
-            for (int e = 0; e < KPL; ++e) {
-                const int m = mc * MCH + wr * MPW + s * KSTEP + (lane >> 5) * KPL + e;
-                const T v = (n < N && m < p.Cout) ? go[(size_t)m * N + n] : (T)0.0f;
-                FragSet<T, KPL>::set(gfr[s], e, v);
+                    for (int e = 0; e < KPL; ++e)
+                        FragSet<T, KPL>::set(gfr[s], e,
+                                             (n < N && m0s + e < p.Cout) ? gp[e] : (T)0.0f);
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < KPL; ++e) {
+                    const int m = m0s + e;
+                    const T v = (n < N && m < p.Cout) ? go[(size_t)m * N + n] : (T)0.0f;
+                    FragSet<T, KPL>::set(gfr[s], e, v);
+                }
             }
         }
     };
@@ -408,7 +427,7 @@ __global__ __launch_bounds__(512) void dcn2_colgrad_kernel(const BwdParams p) {
     // blocks XOR-permuted by m%4, which puts the 4 rows of one read on
     // distinct banks.  Rows past Cout and pixels past N read 0 (buffer range).
     constexpr int GQ = (sizeof(T) == 2 ? MCH * (BN / 8) : 512) / 512;  // 16-byte pieces per thread
-    const bool go_stage = ONEM && sizeof(T) == 2 && p.go_vec &&
+    const bool go_stage = ONEM && sizeof(T) == 2 && p.go_vec && !p.go_nhwc &&
                           (size_t)p.Cout * N * sizeof(T) <= (size_t)kGoOutOfRange;
     uint4 gst[GQ];
     auto go_stage_issue = [&]() __attribute__((always_inline)) {
@@ -884,6 +903,15 @@ __global__ __launch_bounds__(512) void dcn2_gradw_kernel(const BwdParams p) {
     auto load_a = [&](frag &a, int t, int ks) __attribute__((always_inline)) {
         const int b = t / p.tiles_per_img, n0 = (t - b * p.tiles_per_img) * BN;
         const int n = n0 + ks * KSTEP + (lane >> 5) * KPL;
+        if (p.go_nhwc) {  // channels-last: the KPL pixels of a row are Cout apart
+            const T *col = (const T *)p.gout + (size_t)b * p.Cout * N + mrow;
+#pragma unroll
+            for (int e = 0; e < KPL; ++e) {
+                const T v = (mrow < p.Cout && n + e < N) ? col[(size_t)(n + e) * p.Cout] : (T)0.0f;
+                FragSet<T, KPL>::set(a, e, v);
+            }
+            return;
+        }
         const T *row = (const T *)p.gout + ((size_t)b * p.Cout + mrow) * N;
         if (mrow < p.Cout && aligned && n + KPL <= N && KPL == 8) {
             a = *reinterpret_cast<const frag *>(row + n);
@@ -1022,7 +1050,7 @@ __global__ __launch_bounds__(512) void dcn2_gradw_kernel(const BwdParams p) {
 // Every stage runs unconditionally on a clamped tile index, so no load sits
 // in a divergent branch and the compiler's count of outstanding loads stays
 // exact across steps.
-template <typename T, int MB, bool MASK>
+template <typename T, int MB, bool MASK, bool GN>
 __global__ __launch_bounds__(512) void dcn2_gradw_line_kernel(const BwdParams p) {
     static_assert(sizeof(T) == 2, "2-byte types");
     using M = Mma<T>;
@@ -1096,10 +1124,13 @@ __global__ __launch_bounds__(512) void dcn2_gradw_line_kernel(const BwdParams p)
         }
     };
 
-    // one image's gO rows (the host keeps them within kGoOutOfRange bytes)
+    // one image's gO (the host keeps it within kGoOutOfRange bytes)
     const uint32_t go_bytes = (uint32_t)((size_t)p.Cout * N * sizeof(T));
     const int lg = lane >> 3, lc = lane & 7;
     uint4 ga[NKS];  // gO of the next tile, loaded by line; stored to LDS at the end of the step
+    // NCHW: lanes 8g..8g+7 read one 128-byte line (8 pixels of a row) per
+    // instruction.  Channels-last: lanes 4q..4q+3 read the wave's 32 channels
+    // of one pixel (64 bytes), 16 pixels per instruction.
     auto load_a_tile = [&](uint4 (&a)[NKS], int t) __attribute__((always_inline)) {
         const int b = t / p.tiles_per_img, n0 = (t - b * p.tiles_per_img) * BN;
         const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
@@ -1107,20 +1138,55 @@ __global__ __launch_bounds__(512) void dcn2_gradw_line_kernel(const BwdParams p)
             0x00020000);
 #pragma unroll
         for (int j = 0; j < NKS; ++j) {
-            const unsigned row = (unsigned)(rbase + 8 * (j & 3) + lg);
-            const int n = n0 + 64 * (j >> 2) + 8 * lc;
-            const int off = (int)((row * (unsigned)N + (unsigned)n) * sizeof(T));
-            a[j] = __builtin_bit_cast(
-                uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, n < N ? off : kGoOutOfRange, 0, 0));
+            int off;
+            if constexpr (GN) {
+                const int n = n0 + 16 * j + (lane >> 2);
+                const unsigned m = (unsigned)(rbase + 8 * (lane & 3));
+                off = n < N && (int)m < p.Cout
+                          ? (int)(((unsigned)n * (unsigned)p.Cout + m) * sizeof(T))
+                          : kGoOutOfRange;
+            } else {
+                const unsigned row = (unsigned)(rbase + 8 * (j & 3) + lg);
+                const int n = n0 + 64 * (j >> 2) + 8 * lc;
+                off = n < N ? (int)((row * (unsigned)N + (unsigned)n) * sizeof(T)) : kGoOutOfRange;
+            }
+            a[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
         }
     };
-    // per-wave rearrangement area: 32 rows x 17 slots of 16 bytes
+    // Per-wave rearrangement area.  NCHW: 32 rows x 17 slots of 16 bytes, a
+    // fragment is two 16-byte reads.  Channels-last: [128 pixels][32 rows],
+    // a fragment (8 pixels of one row) is two transposing reads
+    // (ds_read_b64_tr_b16: within 16 lanes, lane i receives element i%4 of
+    // the 4-element pieces that lanes i/4, 4 + i/4, 8 + i/4, 12 + i/4 point
+    // at; lane L points at 4 rows of pixel L/4, so lane i receives row i at
+    // 4 consecutive pixels).
     __shared__ uint4 sG[8][32 * 17];
     uint4 *const gw_st = &sG[wave][17 * lg + lc];                     // + 17*8*q + 8*lam
     const uint4 *const gw_ld = &sG[wave][17 * (lane & 31) + (lane >> 5)];  // + 2*i
+    T *const gn_base = reinterpret_cast<T *>(&sG[wave][0]);
     auto stash = [&]() __attribute__((always_inline)) {
+        if constexpr (GN) {
 #pragma unroll
-        for (int j = 0; j < NKS; ++j) gw_st[17 * 8 * (j & 3) + 8 * (j >> 2)] = ga[j];
+            for (int j = 0; j < NKS; ++j) sG[wave][64 * j + lane] = ga[j];
+        } else {
+#pragma unroll
+            for (int j = 0; j < NKS; ++j) gw_st[17 * 8 * (j & 3) + 8 * (j >> 2)] = ga[j];
+        }
+    };
+    auto read_frag = [&](int ks) __attribute__((always_inline)) {
+        if constexpr (GN) {
+            typedef short s16x4 __attribute__((ext_vector_type(4)));
+            const int g = lane >> 4, li = lane & 15;
+            const int c0 = 16 * (g & 1) + 4 * (li & 3), p0 = ks * KSTEP + 8 * (g >> 1) + (li >> 2);
+            s16x4 h[2];
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh)
+                h[hh] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (__attribute__((address_space(3))) s16x4 *)(gn_base + (p0 + 4 * hh) * 32 + c0));
+            return __builtin_bit_cast(frag, __builtin_shufflevector(h[0], h[1], 0, 1, 2, 3, 4, 5, 6, 7));
+        } else {
+            return __builtin_bit_cast(frag, gw_ld[2 * ks]);
+        }
     };
 
     f32x16 acc[BPW];
@@ -1134,7 +1200,7 @@ __global__ __launch_bounds__(512) void dcn2_gradw_line_kernel(const BwdParams p)
         constexpr int buf = decltype(s_c)::value;
         frag af[NKS];
 #pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) af[ks] = __builtin_bit_cast(frag, gw_ld[2 * ks]);
+        for (int ks = 0; ks < NKS; ++ks) af[ks] = read_frag(ks);
 #pragma unroll
         for (int ks = 0; ks < NKS; ++ks) {
             const frag a = af[ks];
@@ -1726,15 +1792,18 @@ static hipError_t backward_t(const Geo &g, const BwdParams &p0, void *grad_input
             p.splits = S;
             const int grid = S * nch * nmc;
             bool line = false;  // 2-byte type with 16-byte gO rows: whole-line loads
-#define DCN2_GRADW(KERN, MBV, MK) KERN<T, MBV, MK><<<grid, 512, 0, s>>>(p)
-#define DCN2_GRADW_MB(KERN)                                                                      \
+#define DCN2_GRADW(KERN, ...) KERN<T, __VA_ARGS__><<<grid, 512, 0, s>>>(p)
+#define DCN2_GRADW_MB(KERN, ...)                                                                 \
     do {                                                                                         \
-        if (mb == 8) { if (p.mask) DCN2_GRADW(KERN, 8, true); else DCN2_GRADW(KERN, 8, false); } \
-        else { if (p.mask) DCN2_GRADW(KERN, 4, true); else DCN2_GRADW(KERN, 4, false); }         \
+        if (mb == 8) { if (p.mask) DCN2_GRADW(KERN, 8, true __VA_ARGS__);                        \
+                       else DCN2_GRADW(KERN, 8, false __VA_ARGS__); }                            \
+        else { if (p.mask) DCN2_GRADW(KERN, 4, true __VA_ARGS__);                                \
+               else DCN2_GRADW(KERN, 4, false __VA_ARGS__); }                                    \
     } while (0)
             if constexpr (sizeof(T) == 2) {
                 if (p.go_vec && (long long)g.Cout * g.N * (long long)sizeof(T) <= kGoOutOfRange) {
-                    DCN2_GRADW_MB(dcn2_gradw_line_kernel);
+                    if (p.go_nhwc) DCN2_GRADW_MB(dcn2_gradw_line_kernel, , true);
+                    else DCN2_GRADW_MB(dcn2_gradw_line_kernel, , false);
                     line = true;
                 }
             }
@@ -1835,7 +1904,8 @@ hipError_t launch_backward(const Geo &g, const void *xt, const void *wt, const v
     p.Mp = g.Mp;
     p.tiles_per_img = ceil_div(g.N, 128);
     p.splits = 1;
-    p.go_vec = (g.N % 8 == 0) && (((uintptr_t)grad_out & 15) == 0);
+    p.go_nhwc = g.out_nhwc;
+    p.go_vec = (g.out_nhwc ? g.Cout % 8 == 0 : g.N % 8 == 0) && (((uintptr_t)grad_out & 15) == 0);
     const GatherGeo gg = gather_geometry(g);
     p.cgm = cgm;
     p.rec = (int4 *)rec;

@@ -39,6 +39,7 @@ struct FwdParams {
     int Mp;                     // padded output rows of the packed weight
     int ntiles, mtiles, tiles;  // pixel tiles per image, M tiles, B*ntiles*mtiles
     int out_vec;                // output rows can be written with 16-byte stores
+    int out_nhwc;               // output is channels-last [B][Ho][Wo][Cout]
     long long off_bs, msk_bs;   // offset / mask elements between images
     int msk_logit;              // mask buffer holds logits (see mask_value)
 };
@@ -224,10 +225,10 @@ __global__ __launch_bounds__(512) void dcn2_fwd_kernel(const FwdParams p) {
     }
     if (ch < nch) step(std::integral_constant<int, 0>{}, ch);
 
-    // Epilogue: round to T and store NCHW.  For 2-byte types with aligned,
-    // 8-divisible rows each wave stages its 32*IB x 32*JB tile in LDS (the K
-    // loop's stages are free after its last barrier) and writes whole 16-byte
-    // row segments; otherwise every lane stores its own elements.
+    // Epilogue: round to T and store.  For 2-byte types with an NCHW output
+    // of aligned, 8-divisible rows each wave stages its 32*IB x 32*JB tile in
+    // LDS (the K loop's stages are free after its last barrier) and writes
+    // whole 16-byte row segments; otherwise every lane stores its own elements.
     T *out = (T *)p.out + (size_t)b * p.Cout * N;
     if constexpr (sizeof(T) == 2) {
         if (p.out_vec) {
@@ -255,6 +256,8 @@ __global__ __launch_bounds__(512) void dcn2_fwd_kernel(const FwdParams p) {
             return;
         }
     }
+    // element stores: NCHW (m * N + n) or channels-last (n * Cout + m)
+    const size_t ms = p.out_nhwc ? 1 : (size_t)N, ns = p.out_nhwc ? (size_t)p.Cout : 1;
 #pragma unroll
     for (int i = 0; i < IB; ++i) {
 #pragma unroll
@@ -264,7 +267,7 @@ __global__ __launch_bounds__(512) void dcn2_fwd_kernel(const FwdParams p) {
 #pragma unroll
             for (int j = 0; j < JB; ++j) {
                 const int n = n0 + (wn * JB + j) * 32 + (lane & 31);
-                if (n < N) out[(size_t)m * N + n] = from_f32<T>(acc[i][j][r]);
+                if (n < N) out[m * ms + n * ns] = from_f32<T>(acc[i][j][r]);
             }
         }
     }
@@ -341,8 +344,8 @@ constexpr int kBiasRows = 1024;
 
 // MASK: 0 no mask (all ones), 1 mask values, 2 mask logits (sigmoid on load);
 // a compile-time mode keeps the descriptor code free of branches, so it can
-// be scheduled between the MFMAs.
-template <typename T, int IB, int MASK>
+// be scheduled between the MFMAs.  ONHWC: channels-last output.
+template <typename T, int IB, int MASK, bool ONHWC>
 __global__ __launch_bounds__(512) void dcn2_fwd_ws_kernel(const FwdParams p) {
     using M = Mma<T>;
     using frag = typename M::frag;
@@ -350,13 +353,15 @@ __global__ __launch_bounds__(512) void dcn2_fwd_ws_kernel(const FwdParams p) {
     constexpr int BN = 128, JB = 4;      // tile pixels; 32-pixel blocks per MFMA wave
     constexpr int ROWS = 32 * IB;        // output rows per MFMA wave
     constexpr int LDK = KC + 8;          // stage pitch (elements): 144 B, conflict-free fragments
-    constexpr int LDO = BN + 8;          // epilogue staging pitch (elements)
+    constexpr int LDO = BN + 8;          // epilogue staging pitch (elements), NCHW: [row][pixel]
+    constexpr int LDC = ROWS + 8;        // the same, channels-last: [pixel][row]
     static_assert(sizeof(T) == 2, "2-byte types only");
+    constexpr int kOutElems = ONHWC ? BN * LDC : ROWS * LDO;  // per MFMA wave
 
     __shared__ __attribute__((aligned(16))) T sB[2][BN][LDK];
-    __shared__ __attribute__((aligned(16))) T sO[4][ROWS][LDO];
+    __shared__ __attribute__((aligned(16))) T sO[4][kOutElems];
     __shared__ RingDesc ring[2][BN];
-    __shared__ float sBias[kBiasRows];
+    __shared__ __attribute__((aligned(16))) float sBias[kBiasRows];
 
     const int tid = threadIdx.x, lane = tid & 63;
     // Role election: the MFMA waves must sit on four different SIMDs (two
@@ -524,15 +529,33 @@ __global__ __launch_bounds__(512) void dcn2_fwd_ws_kernel(const FwdParams p) {
         // operands have the same register layout), so lane l holds output
         // row m = i*32 + l%32 and, in acc[r], pixel n = j*32 + 8*(r/4) +
         // 4*(l/32) + r%4: four consecutive pixels of one row per r/4.
-        // (filled as 64-bit register pairs: half the move instructions)
+        // (filled as 64-bit register pairs: half the move instructions).
+        // With a channels-last output the MFMAs compute D[m][n] instead
+        // (weight fragment as the A operand): lane l then holds pixel
+        // n = j*32 + l%32 and, in acc[r], output row m = i*32 + 8*(r/4) +
+        // 4*(l/32) + r%4, four consecutive channels of one pixel per r/4.
         auto init_acc = [&](int m0) __attribute__((always_inline)) {
-            typedef unsigned long long u64x8 __attribute__((ext_vector_type(8)));
+            if constexpr (ONHWC) {
 #pragma unroll
-            for (int i = 0; i < IB; ++i) {
-                const uint32_t bb = __float_as_uint(sBias[m0 + rw * ROWS + i * 32 + (lane & 31)]);
-                const unsigned long long b2 = ((unsigned long long)bb << 32) | bb;
+                for (int i = 0; i < IB; ++i)
 #pragma unroll
-                for (int j = 0; j < JB; ++j) acc[i][j] = __builtin_bit_cast(f32x16, u64x8(b2));
+                    for (int rq = 0; rq < 4; ++rq) {
+                        const f32x4 b4 = *reinterpret_cast<const f32x4 *>(
+                            &sBias[m0 + rw * ROWS + i * 32 + 8 * rq + 4 * (lane >> 5)]);
+#pragma unroll
+                        for (int j = 0; j < JB; ++j)
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) acc[i][j][4 * rq + e] = b4[e];
+                    }
+            } else {
+                typedef unsigned long long u64x8 __attribute__((ext_vector_type(8)));
+#pragma unroll
+                for (int i = 0; i < IB; ++i) {
+                    const uint32_t bb = __float_as_uint(sBias[m0 + rw * ROWS + i * 32 + (lane & 31)]);
+                    const unsigned long long b2 = ((unsigned long long)bb << 32) | bb;
+#pragma unroll
+                    for (int j = 0; j < JB; ++j) acc[i][j] = __builtin_bit_cast(f32x16, u64x8(b2));
+                }
             }
         };
         // A fragments at cursor c: rows m0 + rw*ROWS + i*32 + lane%32 of chunk
@@ -569,57 +592,105 @@ __global__ __launch_bounds__(512) void dcn2_fwd_ws_kernel(const FwdParams p) {
 #pragma unroll
                 for (int i = 0; i < IB; ++i)
 #pragma unroll
-                    for (int j = 0; j < JB; ++j)
-                        acc[i][j] = M::mma(bf[ks & 1][j], a[SET][i][ks], acc[i][j]);
+                    for (int j = 0; j < JB; ++j) {
+                        if constexpr (ONHWC)
+                            acc[i][j] = M::mma(a[SET][i][ks], bf[ks & 1][j], acc[i][j]);
+                        else
+                            acc[i][j] = M::mma(bf[ks & 1][j], a[SET][i][ks], acc[i][j]);
+                    }
             }
         };
         // Output tile of this wave: round to T, stage in LDS, then 16-byte
-        // row stores (or, for an output whose rows 16-byte stores cannot
-        // cover, a plain loop of element stores from the staged tile).
+        // stores (or, for an output whose rows 16-byte stores cannot cover, a
+        // plain loop of element stores from the staged tile).  Stores go
+        // through a buffer over the image's output: a 16-byte piece outside
+        // the output gets an offset past the buffer and is dropped, so no
+        // store sits in a branch.
+        typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
         auto store_tile = [&](const Cursor &c) __attribute__((always_inline)) {
             T *out = (T *)p.out + (size_t)c.b * p.Cout * N;
-            // four consecutive pixels of a row -> one 8-byte LDS write
-            T(&so)[ROWS][LDO] = sO[rw];
+            const uint32_t obytes = (uint32_t)((size_t)p.Cout * N * sizeof(T));
+            const __amdgpu_buffer_rsrc_t ors =
+                __builtin_amdgcn_make_buffer_rsrc(out, (short)0, (int)obytes, 0x00020000);
+            const int mw = c.m0 + rw * ROWS;  // first output row of this wave
+            if constexpr (ONHWC) {
+                // [pixel][row] staging: four consecutive rows of a pixel -> one
+                // 8-byte LDS write; then each pixel's ROWS channels are
+                // ROWS/8 16-byte pieces, 8 lanes per pixel per instruction
+                T(&so)[BN][LDC] = *reinterpret_cast<T(*)[BN][LDC]>(sO[rw]);
 #pragma unroll
-            for (int i = 0; i < IB; ++i)
+                for (int i = 0; i < IB; ++i)
 #pragma unroll
-                for (int j = 0; j < JB; ++j)
+                    for (int j = 0; j < JB; ++j)
 #pragma unroll
-                    for (int rq = 0; rq < 4; ++rq) {
-                        T v4[4];
+                        for (int rq = 0; rq < 4; ++rq) {
+                            T v4[4];
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) v4[e] = from_f32<T>(acc[i][j][rq * 4 + e]);
-                        *reinterpret_cast<uint2 *>(&so[i * 32 + (lane & 31)][j * 32 + 8 * rq + 4 * (lane >> 5)]) =
-                            __builtin_bit_cast(uint2, v4);
+                            for (int e = 0; e < 4; ++e) v4[e] = from_f32<T>(acc[i][j][rq * 4 + e]);
+                            *reinterpret_cast<uint2 *>(&so[j * 32 + (lane & 31)][i * 32 + 8 * rq + 4 * (lane >> 5)]) =
+                                __builtin_bit_cast(uint2, v4);
+                        }
+                if (p.out_vec) {
+                    constexpr int SEG = ROWS / 8, PPI = 64 / SEG;
+                    const int seg = lane % SEG, q = lane / SEG;
+                    const int m = mw + seg * 8;
+#pragma unroll
+                    for (int it = 0; it < BN / PPI; ++it) {
+                        const int pl = it * PPI + q, n = c.n0 + pl;
+                        const uint4 v = *reinterpret_cast<const uint4 *>(&so[pl][seg * 8]);
+                        const uint32_t off =
+                            m < p.Cout && n < N
+                                ? (uint32_t)(((unsigned)n * (unsigned)p.Cout + (unsigned)m) * sizeof(T))
+                                : obytes;
+                        __builtin_amdgcn_raw_buffer_store_b128(u32x4{v.x, v.y, v.z, v.w}, ors, (int)off, 0, 0);
                     }
-            if (p.out_vec) {
-                // a wave instruction covers 64 / SEG whole rows of SEG 16-byte
-                // segments; buffer stores over the image's output, a segment
-                // outside it (m >= Cout or n >= N; N % 8 == 0, so a segment is
-                // all in or all out) gets an offset past the buffer and is
-                // dropped, so no store sits in a branch
-                constexpr int SEG = BN / 8, RPI = 64 / SEG;
-                const int seg = lane % SEG, r0 = lane / SEG;
-                const int n = c.n0 + seg * 8;
-                const uint32_t obytes = (uint32_t)((size_t)p.Cout * N * sizeof(T));
-                const __amdgpu_buffer_rsrc_t ors =
-                    __builtin_amdgcn_make_buffer_rsrc(out, (short)0, (int)obytes, 0x00020000);
-#pragma unroll
-                for (int it = 0; it < ROWS / RPI; ++it) {
-                    const int m = c.m0 + rw * ROWS + it * RPI + r0;
-                    const uint4 v = *reinterpret_cast<const uint4 *>(&so[it * RPI + r0][seg * 8]);
-                    const uint32_t off = m < p.Cout && n < N
-                                             ? (uint32_t)(((unsigned)m * (unsigned)N + (unsigned)n) * sizeof(T))
-                                             : obytes;
-                    typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
-                    __builtin_amdgcn_raw_buffer_store_b128(u32x4{v.x, v.y, v.z, v.w}, ors, (int)off, 0, 0);
+                } else {
+#pragma unroll 1
+                    for (int idx = lane; idx < ROWS * BN; idx += 64) {
+                        const int pl = idx / ROWS, row = idx % ROWS;
+                        const int m = mw + row, n = c.n0 + pl;
+                        if (m < p.Cout && n < N) out[(size_t)n * p.Cout + m] = so[pl][row];
+                    }
                 }
             } else {
+                // [row][pixel] staging: four consecutive pixels of a row -> one
+                // 8-byte LDS write
+                T(&so)[ROWS][LDO] = *reinterpret_cast<T(*)[ROWS][LDO]>(sO[rw]);
+#pragma unroll
+                for (int i = 0; i < IB; ++i)
+#pragma unroll
+                    for (int j = 0; j < JB; ++j)
+#pragma unroll
+                        for (int rq = 0; rq < 4; ++rq) {
+                            T v4[4];
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) v4[e] = from_f32<T>(acc[i][j][rq * 4 + e]);
+                            *reinterpret_cast<uint2 *>(&so[i * 32 + (lane & 31)][j * 32 + 8 * rq + 4 * (lane >> 5)]) =
+                                __builtin_bit_cast(uint2, v4);
+                        }
+                if (p.out_vec) {
+                    // a wave instruction covers 64 / SEG whole rows of SEG
+                    // 16-byte segments (N % 8 == 0: a segment is all in or out)
+                    constexpr int SEG = BN / 8, RPI = 64 / SEG;
+                    const int seg = lane % SEG, r0 = lane / SEG;
+                    const int n = c.n0 + seg * 8;
+#pragma unroll
+                    for (int it = 0; it < ROWS / RPI; ++it) {
+                        const int m = mw + it * RPI + r0;
+                        const uint4 v = *reinterpret_cast<const uint4 *>(&so[it * RPI + r0][seg * 8]);
+                        const uint32_t off =
+                            m < p.Cout && n < N
+                                ? (uint32_t)(((unsigned)m * (unsigned)N + (unsigned)n) * sizeof(T))
+                                : obytes;
+                        __builtin_amdgcn_raw_buffer_store_b128(u32x4{v.x, v.y, v.z, v.w}, ors, (int)off, 0, 0);
+                    }
+                } else {
 #pragma unroll 1
-                for (int idx = lane; idx < ROWS * BN; idx += 64) {
-                    const int row = idx / BN, col = idx % BN;
-                    const int m = c.m0 + rw * ROWS + row, n = c.n0 + col;
-                    if (m < p.Cout && n < N) out[(size_t)m * N + n] = so[row][col];
+                    for (int idx = lane; idx < ROWS * BN; idx += 64) {
+                        const int row = idx / BN, col = idx % BN;
+                        const int m = mw + row, n = c.n0 + col;
+                        if (m < p.Cout && n < N) out[(size_t)m * N + n] = so[row][col];
+                    }
                 }
             }
         };
@@ -768,7 +839,7 @@ static hipError_t launch_fwd_t(const Geo &g, const FwdParams &p0, hipStream_t s)
     p.ntiles = ceil_div(g.N, 32 * JB * WN);
     p.mtiles = g.Mp / (32 * IB * WM);
     p.tiles = g.B * p.ntiles * p.mtiles;
-    p.out_vec = (g.N % 8 == 0) && (((uintptr_t)p.out & 15) == 0);
+    p.out_vec = !p.out_nhwc && (g.N % 8 == 0) && (((uintptr_t)p.out & 15) == 0);
     if (p.mask)
         dcn2_fwd_kernel<T, WM, WN, IB, JB, true><<<p.tiles, 512, 0, s>>>(p);
     else
@@ -784,19 +855,24 @@ static hipError_t launch_fwd_ws(const Geo &g, const FwdParams &p0, hipStream_t s
     p.ntiles = ceil_div(g.N, 128);
     p.mtiles = g.Mp / (128 * IB);
     p.tiles = g.B * p.ntiles * p.mtiles;
-    p.out_vec = (g.N % 8 == 0) && (((uintptr_t)p.out & 15) == 0);
+    // 16-byte pieces of NCHW rows need N % 8 == 0, of channels-last pixels Cout % 8 == 0
+    p.out_vec = (p.out_nhwc ? g.Cout % 8 == 0 : g.N % 8 == 0) && (((uintptr_t)p.out & 15) == 0);
     int dev = 0, ncu = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         ncu <= 0)
         ncu = 256;
     const int grid = p.tiles < ncu ? p.tiles : ncu;
-    if (p.mask && p.msk_logit)
-        dcn2_fwd_ws_kernel<T, IB, 2><<<grid, 512, 0, s>>>(p);
-    else if (p.mask)
-        dcn2_fwd_ws_kernel<T, IB, 1><<<grid, 512, 0, s>>>(p);
-    else
-        dcn2_fwd_ws_kernel<T, IB, 0><<<grid, 512, 0, s>>>(p);
+    const int mode = p.mask ? (p.msk_logit ? 2 : 1) : 0;
+    if (p.out_nhwc) {
+        if (mode == 2) dcn2_fwd_ws_kernel<T, IB, 2, true><<<grid, 512, 0, s>>>(p);
+        else if (mode == 1) dcn2_fwd_ws_kernel<T, IB, 1, true><<<grid, 512, 0, s>>>(p);
+        else dcn2_fwd_ws_kernel<T, IB, 0, true><<<grid, 512, 0, s>>>(p);
+    } else {
+        if (mode == 2) dcn2_fwd_ws_kernel<T, IB, 2, false><<<grid, 512, 0, s>>>(p);
+        else if (mode == 1) dcn2_fwd_ws_kernel<T, IB, 1, false><<<grid, 512, 0, s>>>(p);
+        else dcn2_fwd_ws_kernel<T, IB, 0, false><<<grid, 512, 0, s>>>(p);
+    }
     return hipGetLastError();
 }
 
@@ -805,9 +881,12 @@ static hipError_t launch_fwd_ws(const Geo &g, const FwdParams &p0, hipStream_t s
 template <typename T, int IB>
 static bool ws_two_waves_per_simd() {
     static const bool ok = [] {
-        const void *fns[3] = {reinterpret_cast<const void *>(&dcn2_fwd_ws_kernel<T, IB, 0>),
-                              reinterpret_cast<const void *>(&dcn2_fwd_ws_kernel<T, IB, 1>),
-                              reinterpret_cast<const void *>(&dcn2_fwd_ws_kernel<T, IB, 2>)};
+        const void *fns[6] = {reinterpret_cast<const void *>(&dcn2_fwd_ws_kernel<T, IB, 0, false>),
+                              reinterpret_cast<const void *>(&dcn2_fwd_ws_kernel<T, IB, 1, false>),
+                              reinterpret_cast<const void *>(&dcn2_fwd_ws_kernel<T, IB, 2, false>),
+                              reinterpret_cast<const void *>(&dcn2_fwd_ws_kernel<T, IB, 0, true>),
+                              reinterpret_cast<const void *>(&dcn2_fwd_ws_kernel<T, IB, 1, true>),
+                              reinterpret_cast<const void *>(&dcn2_fwd_ws_kernel<T, IB, 2, true>)};
         for (const void *fn : fns) {
             hipFuncAttributes a;
             if (hipFuncGetAttributes(&a, fn) != hipSuccess || a.numRegs <= 512 / 3) return false;
@@ -852,6 +931,7 @@ hipError_t launch_forward(const Geo &g, const void *xt, const void *wp, const vo
     p.msk_logit = mask ? g.msk_logit : 0;
     p.bias = bias;
     p.out = out;
+    p.out_nhwc = g.out_nhwc;
     p.H = g.H;
     p.W = g.W;
     p.Cout = g.Cout;

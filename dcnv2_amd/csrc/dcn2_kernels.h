@@ -18,6 +18,7 @@ struct Geo {
     int Cg;         // channels per deformable group
     int WG, Cw;     // weight groups and input channels per weight group (C / WG)
     int nhwc;       // input / grad_input are channels-last [B][H][W][C]
+    int out_nhwc;   // output / grad_output are channels-last [B][Ho][Wo][Cout]
     int xt_direct;  // nhwc and cs == C: the input itself serves as xt (no repacking)
     int KC;         // channel chunk of one LDS stage (64 for f16/bf16, 32 for f32)
     int Cgp;        // Cg rounded up to KC

@@ -20,7 +20,8 @@
  *   x = ox*stride_w - pad_w + j*dilation_w + offset[b, 2*(g*kh*kw + k) + 1, oy, ox]
  * with bilinear() reading 0 outside the image (reference com.cu:119-148, 187).
  *
- * Tensor layouts are contiguous NCHW in the caller's dtype:
+ * Tensor layouts are contiguous NCHW in the caller's dtype (input, grad_input,
+ * output and grad_output may instead be channels_last, see dcn2_layout):
  *   input  [B, C, H, W]            weight [Cout, C/weight_groups, kh, kw]    bias [Cout]
  *   offset [B, 2*G*kh*kw, Ho, Wo]  mask   [B, G*kh*kw, Ho, Wo]    output [B, Cout, Ho, Wo]
  *   Ho = (H + 2*pad_h - (dilation_h*(kh-1) + 1)) / stride_h + 1   (likewise Wo)
@@ -42,17 +43,20 @@
 extern "C" {
 #endif
 
-#define DCN2_ABI_VERSION 2
+#define DCN2_ABI_VERSION 3
 #define DCN2_API __attribute__((visibility("default")))
 
 enum dcn2_dtype { DCN2_F32 = 0, DCN2_F16 = 1, DCN2_BF16 = 2 };
 
-/* Memory layout of `input` and `grad_input` (every other tensor is NCHW).
- * DCN2_NHWC is torch's channels_last: [B][H][W][C].  When C/deformable_groups
- * is a multiple of 64 (fp16/bf16) or 32 (fp32) the kernels read such an input
- * in place (it must then be 16-byte aligned) and the forward workspace holds
- * no repacked copy; otherwise it is repacked like an NCHW input.  No
- * counterpart in the reference, which takes contiguous NCHW only. */
+/* Memory layout of an activation tensor.  DCN2_NHWC is torch's channels_last:
+ * [B][H][W][C] (for the output [B][Ho][Wo][Cout]).  dcn2_desc.input_layout
+ * covers `input` and `grad_input`: when C/deformable_groups is a multiple of
+ * 64 (fp16/bf16) or 32 (fp32) the kernels read such an input in place (it
+ * must then be 16-byte aligned) and the forward workspace holds no repacked
+ * copy; otherwise it is repacked like an NCHW input.
+ * dcn2_desc.output_layout covers `output` (written by the forward) and
+ * `grad_output` (read by the backward), both read and written in place.  No
+ * counterpart in the reference, which takes and returns contiguous NCHW only. */
 enum dcn2_layout { DCN2_NCHW = 0, DCN2_NHWC = 1 };
 
 enum dcn2_status {
@@ -71,7 +75,7 @@ enum dcn2_status {
  * groups (its deform_conv2d infers them from weight.shape[1]; the reference has
  * none).  weight_groups 0 means 1, so a zero-initialised descriptor is
  * ungrouped; in_channels and out_channels must both divide by it.
- * input_layout is an enum dcn2_layout (0 = NCHW). */
+ * input_layout and output_layout are enum dcn2_layout values (0 = NCHW). */
 typedef struct dcn2_desc {
     int32_t batch, in_channels, height, width;
     int32_t out_channels, kernel_h, kernel_w;
@@ -80,6 +84,7 @@ typedef struct dcn2_desc {
     int32_t dtype; /* enum dcn2_dtype */
     int32_t weight_groups;
     int32_t input_layout;
+    int32_t output_layout;
 } dcn2_desc;
 
 /* Output spatial size for `d`; DCN2_EINVAL if it would be empty. */

@@ -260,31 +260,48 @@ def test_weight_groups(dtype, case):
 
 # --------------------------------------------------------------------------- channels_last
 @pytest.mark.parametrize("case", [
-    # dtype, C, deformable groups: in place when C/G is a multiple of the channel chunk
-    (torch.float16, 64, 1),      # read in place
-    (torch.bfloat16, 128, 2),    # read in place, two groups
-    (torch.float32, 64, 2),      # read in place (fp32 chunk is 32 channels)
-    (torch.float16, 24, 2),      # padded: repacked from channels-last
-    (torch.bfloat16, 18, 2),     # padded, 9 channels per group: element-wise grad_input stores
-], ids=["f16_c64", "bf16_c128_dg2", "f32_c64_dg2", "f16_c24_dg2_padded", "bf16_c18_dg2_padded"])
+    # dtype, C, deformable groups, Cout: the input is read in place when C/G is a
+    # multiple of the channel chunk; channels-last output rows are stored as
+    # 16-byte pieces when Cout % 8 == 0, element by element otherwise
+    (torch.float16, 64, 1, 40),      # read in place
+    (torch.bfloat16, 128, 2, 40),    # read in place, two groups
+    (torch.float32, 64, 2, 40),      # read in place (fp32 chunk is 32 channels)
+    (torch.float16, 24, 2, 40),      # padded: repacked from channels-last
+    (torch.bfloat16, 18, 2, 40),     # padded, 9 channels per group: element-wise grad_input stores
+    (torch.float16, 64, 1, 36),      # Cout % 8 != 0: element-wise output / grad_output access
+    (torch.bfloat16, 64, 1, 300),    # two M tiles, non-warp-specialised forward
+], ids=["f16_c64", "bf16_c128_dg2", "f32_c64_dg2", "f16_c24_dg2_padded", "bf16_c18_dg2_padded",
+        "f16_cout36", "bf16_cout300"])
 def test_channels_last_input(case):
-    """A channels_last input gives the same forward, bit for bit, as its NCHW
-    copy (the kernels see the same channels-last data), and a backward within
-    tolerance of the oracle whose grad_input is channels_last."""
-    dtype, C, G = case
-    w, t = _small(dtype, B=2, C=C, H=13, W=11, Cout=40, G=G, osc=2.0)
+    """A channels_last input gives a channels_last output (read and written in
+    place by the kernels) equal to the oracle and to the NCHW run, and a
+    backward whose grad_input is channels_last; grad_output is read in place
+    in either layout.  All five gradients against the oracle for both
+    grad_output layouts."""
+    dtype, C, G, Cout = case
+    w, t = _small(dtype, B=2, C=C, H=13, W=11, Cout=Cout, G=G, osc=2.0)
     geo = w.geometry()
-    x_cl = t["input"].to(DEV).to(memory_format=torch.channels_last)
+    cl = torch.channels_last
+    x_cl = t["input"].to(DEV).to(memory_format=cl)
     assert not x_cl.is_contiguous()
     args = [None if t[k] is None else t[k].to(DEV) for k in IN5]
     out_nchw = _C.dcn_v2_forward(*args, *_args(geo))
     out_cl = _C.dcn_v2_forward(x_cl, *args[1:], *_args(geo))
-    grads = _C.dcn_v2_backward(x_cl, *args[1:], t["grad_output"].to(DEV), *_args(geo))
+    go = t["grad_output"].to(DEV)
+    grads_go_cl = _C.dcn_v2_backward(x_cl, *args[1:], go.to(memory_format=cl), *_args(geo))
+    grads_go_nchw = _C.dcn_v2_backward(x_cl, *args[1:], go, *_args(geo))
     torch.cuda.synchronize()
-    assert torch.equal(out_cl, out_nchw)
-    assert grads[0].is_contiguous(memory_format=torch.channels_last)
-    for name, g, r in zip(GRADS, grads, oracle_backward(t, geo)):
-        check(name, g, r, TOL[dtype])
+    assert out_cl.is_contiguous(memory_format=cl) and not out_cl.is_contiguous()
+    assert out_nchw.is_contiguous()
+    ref = oracle_forward(t, geo)
+    check("output (channels_last)", out_cl, ref, TOL[dtype])
+    check("output (channels_last vs NCHW run)", out_cl, out_nchw, TOL[dtype])
+    rgrads = oracle_backward(t, geo)
+    for grads, tag in ((grads_go_cl, "grad_output channels_last"),
+                       (grads_go_nchw, "grad_output NCHW")):
+        assert grads[0].is_contiguous(memory_format=cl)
+        for name, g, r in zip(GRADS, grads, rgrads):
+            check(f"{name} ({tag})", g, r, TOL[dtype])
 
 
 def test_channels_last_predictor_output_path():
@@ -302,7 +319,8 @@ def test_channels_last_predictor_output_path():
     g_ref = _C.dcn_v2_backward_om(x, wt, om, b, go, *_args(geo))
     g_cl = _C.dcn_v2_backward_om(x_cl, wt, om, b, go, *_args(geo))
     torch.cuda.synchronize()
-    assert torch.equal(got, ref)
+    assert got.is_contiguous(memory_format=torch.channels_last)
+    check("output", got, ref, TOL[torch.float16])
     assert g_cl[0].is_contiguous(memory_format=torch.channels_last)
     for a, r in zip(g_cl, g_ref):
         check("grad", a, r, TOL[torch.float16])

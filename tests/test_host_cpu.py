@@ -49,8 +49,9 @@ def header_functions():
 
 
 def desc(B=2, C=8, H=9, W=10, Co=5, kh=3, kw=3, sh=1, sw=1, ph=1, pw=1, dh=1, dw=1, G=1,
-         dtype=0, WG=0, layout=0):
-    return _C.Desc(B, C, H, W, Co, kh, kw, sh, sw, ph, pw, dh, dw, G, dtype, WG, layout)
+         dtype=0, WG=0, layout=0, out_layout=0):
+    return _C.Desc(B, C, H, W, Co, kh, kw, sh, sw, ph, pw, dh, dw, G, dtype, WG, layout,
+                   out_layout)
 
 
 def out_hw(L, d):
@@ -94,6 +95,7 @@ def test_output_shape_matches_formula(L, geo):
     (dict(C=8, Co=6, WG=4), 1, "weight_groups"),
     (dict(WG=-1), 1, "weight_groups"),
     (dict(layout=2), 1, "input_layout"),
+    (dict(out_layout=-1), 1, "output_layout"),
     (dict(dtype=7), 1, "dtype"),
     (dict(C=0), 1, "shape"),
     (dict(sh=0), 1, "stride"),
@@ -122,6 +124,22 @@ def test_workspace_sizes(L):
         assert fs >= 2 * 9 * 10 * Cgp * esz
     # empty batch still has a valid workspace (weight packing)
     assert L.dcn2_forward_workspace_bytes(ctypes.byref(desc(B=0))) > 0
+
+
+def test_backward_workspace_is_exact_size(L):
+    """The grad_input buckets hold one row per sample (B*G*kh*kw*Ho*Wo rows of
+    Cg rounded to 64 channels), however the samples cluster, so the c2 shape
+    (B8 C64 128x128 Cout256 fp16) needs about 236 MB: channels-last input
+    copy 16.8 MB, fp32 grad_input accumulator 33.6 MB, rows 151 MB, records
+    18.9 MB, sample rows 4.7 MB, border rings 10.6 MB, packed weights and
+    grad_weight accumulator 0.9 MB."""
+    d = desc(B=8, C=64, H=128, W=128, Co=256, dtype=1)
+    nbytes = L.dcn2_backward_workspace_bytes(ctypes.byref(d))
+    rows = 8 * 9 * 128 * 128
+    assert rows * (64 * 2 + 16) < nbytes < 240e6
+    # bf16 hands fp32 rows to the gather: twice the row bytes
+    d16 = desc(B=8, C=64, H=128, W=128, Co=256, dtype=2)
+    assert L.dcn2_backward_workspace_bytes(ctypes.byref(d16)) - nbytes == rows * 64 * 2
 
 
 def test_entry_points_reject_before_any_launch(L):
