@@ -368,6 +368,25 @@ def main():
     result["fwd_bwd_ms"] = others[c2.name]["fwd_bwd_ms"]
     result["configs"] = others
 
+    # Weight groups (torchvision's groups; the reference has none): a layer of
+    # the c2 pixel shape with 128 input channels in 2 weight groups, against
+    # the same layer ungrouped.  The grouped layer runs one GEMM per group over
+    # its own channels, half the sampling and MFMA work of the ungrouped one.
+    grp = {}
+    for wg in (1, 2):
+        w = c2.with_(C=128, seed=7)
+        t = load(w)
+        if wg > 1:
+            t["weight"] = t["weight"][:, : w.C // wg].contiguous()
+        f, fb = fwd_fn(w, t), fwd_bwd_fn(w, t)
+        _warm(f, 10, 100.0, torch)
+        fms = _events_ms(f, max(5, args.steps // 4), torch)
+        _warm(fb, 5, 50.0, torch)
+        fbms = _events_ms(fb, max(5, args.steps // 4), torch)
+        grp[f"weight_groups_{wg}"] = {"fwd_ms": round(fms, 5), "fwd_bwd_ms": round(fbms, 5)}
+        del t, f, fb
+    result["weight_groups"] = dict(grp, workload="B8 C128 H128 W128 Cout256 3x3 s1 p1 dg1 fp16")
+
     # The c1/c2 workloads in channels_last: the kernels read the input in
     # place (C = 64 needs no channel padding), so the repacking pass drops out,
     # write the output and grad_input channels-last and read grad_output

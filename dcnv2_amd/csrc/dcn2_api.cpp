@@ -7,6 +7,7 @@
 // hipMalloc, and every launch goes to the caller's stream.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <string>
@@ -100,6 +101,26 @@ int make_geo(const dcn2_desc *d, Geo &g) {
         (long long)g.B * g.G * g.KK * g.Ho * g.Wo >= lim || g.H > 32767 || g.W > 32767)
         return fail(DCN2_ERANGE, "dcn2: problem exceeds the 32-bit per-image index range");
     g.Kp = (int)Kp;
+    // weight-group walk (see Geo::gsplit): every chunk (deformable group dg,
+    // channel chunk cc) must lie inside the group q / cpw of its index q in
+    // the tap
+    g.cpt = g.G * (g.Cgp / g.KC);
+    g.cpw = g.cpt;
+    g.gsplit = 0;
+    if (g.WG > 1 && (g.Cout / g.WG) % 128 == 0 && g.cpt % g.WG == 0) {
+        const int cpg = g.Cgp / g.KC, cpw = g.cpt / g.WG;
+        bool ok = true;
+        for (int q = 0; q < g.cpt && ok; ++q) {
+            const int dg = q / cpg, cc = q % cpg;
+            const int lo = dg * g.Cg + cc * g.KC;
+            const int hi = dg * g.Cg + std::min((cc + 1) * g.KC, g.Cg) - 1;
+            ok = lo / g.Cw == hi / g.Cw && lo / g.Cw == q / cpw;
+        }
+        if (ok) {
+            g.gsplit = 1;
+            g.cpw = cpw;
+        }
+    }
     // the forward's sampler addresses one image of xt with 32-bit byte offsets
     // and marks corners outside the image with the offset just past it
     if (((long long)g.H * g.W + 1) * g.cs * g.esz + 256 >= 0x100000000LL)

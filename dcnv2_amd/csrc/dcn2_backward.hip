@@ -60,7 +60,20 @@ struct BwdParams {
     // the gradient of the logits)
     long long off_bs, msk_bs;
     int msk_logit;
+    // grad_weight work items: gw_nch chunks per M chunk.  Ungrouped (gw_cog
+    // 0): every chunk.  Weight groups whose chunks never mix: an M chunk of
+    // group w = m0 / gw_cog walks only that group's chunks tap*gw_cpt +
+    // w*gw_cpw + i, i < gw_cpw (the other blocks of the block-diagonal packed
+    // weight are zero and their grad_weight is not kept).
+    int gw_nch, gw_cpt, gw_cpw, gw_cog;
 };
+
+// Packed chunk index of the j-th grad_weight chunk of the M chunk at row m0.
+__device__ __forceinline__ int gw_chunk(const BwdParams &p, int j, int m0) {
+    if (p.gw_cog == 0) return j;
+    const int tap = j / p.gw_cpw;
+    return tap * p.gw_cpt + (m0 / p.gw_cog) * p.gw_cpw + (j - tap * p.gw_cpw);
+}
 
 // Element type of the masked column-gradient rows the column-gradient kernel
 // hands to the grad_input gather: fp32 for bf16, whose 8-bit mantissa would
@@ -839,10 +852,11 @@ __global__ __launch_bounds__(512) void dcn2_gradw_kernel(const BwdParams p) {
     // Work item = (pixel-tile range sp, K chunk ch, M chunk mc), handed to XCDs
     // in contiguous ranges with the range index slowest, so one XCD works on
     // consecutive pixel tiles (same images) for all chunks.
-    const int nch = p.Kp / KC, nmc = p.Mp / (32 * MB);
-    const int wi = xcd_remap(blockIdx.x, p.splits * nch * nmc);
-    const int mc = wi % nmc, ch = (wi / nmc) % nch, sp = wi / (nmc * nch);
-    const bool do_bias = p.gb_acc != nullptr && ch == 0 && kblk0 == 0 && active;
+    const int nmc = p.Mp / (32 * MB);
+    const int wi = xcd_remap(blockIdx.x, p.splits * p.gw_nch * nmc);
+    const int mc = wi % nmc, j = (wi / nmc) % p.gw_nch, sp = wi / (nmc * p.gw_nch);
+    const int ch = gw_chunk(p, j, mc * 32 * MB);
+    const bool do_bias = p.gb_acc != nullptr && j == 0 && kblk0 == 0 && active;
     const int mrow = mc * 32 * MB + mblk * 32 + (lane & 31);
     const int N = p.Ho * p.Wo, KK = p.kh * p.kw, cs = p.G * p.Cgp;
     const int T_total = p.B * p.tiles_per_img;
@@ -1075,10 +1089,11 @@ __global__ __launch_bounds__(512) void dcn2_gradw_line_kernel(const BwdParams p)
         kblk0 = wave - mblk * KB;
     }
     // work item as in dcn2_gradw_kernel (every wave is active: NBLK >= 8)
-    const int nch = p.Kp / KC, nmc = p.Mp / (32 * MB);
-    const int wi = xcd_remap(blockIdx.x, p.splits * nch * nmc);
-    const int mc = wi % nmc, ch = (wi / nmc) % nch, sp = wi / (nmc * nch);
-    const bool do_bias = p.gb_acc != nullptr && ch == 0 && kblk0 == 0;
+    const int nmc = p.Mp / (32 * MB);
+    const int wi = xcd_remap(blockIdx.x, p.splits * p.gw_nch * nmc);
+    const int mc = wi % nmc, j = (wi / nmc) % p.gw_nch, sp = wi / (nmc * p.gw_nch);
+    const int ch = gw_chunk(p, j, mc * 32 * MB);
+    const bool do_bias = p.gb_acc != nullptr && j == 0 && kblk0 == 0;
     const int rbase = mc * 32 * MB + mblk * 32;  // first gO row of this wave
     const int mrow = rbase + (lane & 31);
     const int N = p.Ho * p.Wo, KK = p.kh * p.kw, cs = p.G * p.Cgp;
@@ -1775,8 +1790,15 @@ static hipError_t backward_t(const Geo &g, const BwdParams &p0, void *grad_input
         // 3. grad_weight / grad_bias
         prof_begin(DCN2_STAGE_BWD_GRADW, s);
         {
-            const int nch = g.Kp / g.KC;
-            const int mb = (g.Mp % 256 == 0) ? 8 : 4;
+            // weight groups split per group (Geo::gsplit): an M chunk must lie
+            // in one group, whose rows are a multiple of 128
+            const int cog = g.gsplit ? g.Cout / g.WG : 0;
+            const int mb = (cog ? cog % 256 == 0 : g.Mp % 256 == 0) ? 8 : 4;
+            p.gw_cpt = g.cpt;
+            p.gw_cpw = g.cpw;
+            p.gw_cog = cog;
+            p.gw_nch = cog ? g.KK * g.cpw : g.Kp / g.KC;
+            const int nch = p.gw_nch;
             const int nmc = g.Mp / (32 * mb);
             const int T_total = g.B * p.tiles_per_img;
             // One workgroup per CU: each (K chunk, M chunk) pair gets CUs/(nch*nmc)

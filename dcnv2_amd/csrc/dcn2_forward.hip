@@ -38,6 +38,13 @@ struct FwdParams {
     int H, W, Cout, kh, kw, sh, sw, ph, pw, dh, dw, G, Cgp, Ho, Wo, Kp;
     int Mp;                     // padded output rows of the packed weight
     int ntiles, mtiles, tiles;  // pixel tiles per image, M tiles, B*ntiles*mtiles
+    // Chunks and M tiles walked by this launch.  A launch covers the M tiles
+    // [mt_base, mt_base + mtiles) and, per tile, the nch_eff = KK*cpw chunks
+    // ch = tap*cpt + cb + i (i < cpw) of the packed K order (tap, group,
+    // channel chunk), cpt chunks per tap.  One launch per weight group walks
+    // only that group's rows and chunks; an ungrouped launch has cb = 0 and
+    // cpw = cpt, i.e. every chunk.
+    int mt_base, cpt, cpw, cb, nch_eff;
     int out_vec;                // output rows can be written with 16-byte stores
     int out_nhwc;               // output is channels-last [B][Ho][Wo][Cout]
     long long off_bs, msk_bs;   // offset / mask elements between images
@@ -76,9 +83,16 @@ __global__ __launch_bounds__(512) void dcn2_fwd_kernel(const FwdParams p) {
     // corner gathers.
     const int t = xcd_remap(blockIdx.x, p.tiles);
     const int mt = t % p.mtiles, nt = (t / p.mtiles) % p.ntiles, b = t / (p.mtiles * p.ntiles);
-    const int n0 = nt * BN, m0 = mt * BM;
+    const int n0 = nt * BN, m0 = (p.mt_base + mt) * BM;
     const int N = p.Ho * p.Wo, KK = p.kh * p.kw, cs = p.G * p.Cgp;
-    const int nch = p.Kp / KC, last = nch - 1;
+    const int nch_all = p.Kp / KC;         // chunks of the packed weight rows
+    const int nch = p.nch_eff, last = nch - 1;  // chunks walked (see FwdParams)
+    // j-th chunk of the walk -> packed chunk index
+    auto chmap = [&](int j) __attribute__((always_inline)) {
+        j = min(j, last);
+        const int tap = j / p.cpw;
+        return tap * p.cpt + p.cb + (j - tap * p.cpw);
+    };
 
     const T *__restrict__ xt = (const T *)p.xt + (size_t)b * p.H * p.W * cs;
     const T *__restrict__ offs = (const T *)p.offset + (size_t)b * p.off_bs;
@@ -102,7 +116,7 @@ __global__ __launch_bounds__(512) void dcn2_fwd_kernel(const FwdParams p) {
     SlotOM<T, SPT> om[2];
     frag a[2][IB][NKS];
 
-    auto ent = [&](int ch) __attribute__((always_inline)) { return tab[min(ch, last)]; };
+    auto ent = [&](int ch) __attribute__((always_inline)) { return tab[chmap(ch)]; };
 
     // Bilinear blend of sampler set SET, stored to LDS stage SET as
     // [pixel][channel] rows (the MFMA B-operand order).
@@ -127,11 +141,11 @@ __global__ __launch_bounds__(512) void dcn2_fwd_kernel(const FwdParams p) {
     const T *wfrag[IB];
 #pragma unroll
     for (int i = 0; i < IB; ++i)
-        wfrag[i] = (const T *)p.wp + ((size_t)((m0 + wm * 32 * IB + i * 32) / 32) * nch * NKS * 64 +
+        wfrag[i] = (const T *)p.wp + ((size_t)((m0 + wm * 32 * IB + i * 32) / 32) * nch_all * NKS * 64 +
                                       lane) * KPL;
     auto load_a = [&](auto set_c, int ch) __attribute__((always_inline)) {
         constexpr int SET = decltype(set_c)::value;
-        const int c = min(ch, last) * NKS * 64 * KPL;
+        const int c = chmap(ch) * NKS * 64 * KPL;
 #pragma unroll
         for (int i = 0; i < IB; ++i)
 #pragma unroll
@@ -379,7 +393,8 @@ __global__ __launch_bounds__(512) void dcn2_fwd_ws_kernel(const FwdParams p) {
     if (lane == 0) rank = atomicAdd(&simd_seen[rw], 1);
     const bool mfma_role = __builtin_amdgcn_readfirstlane(__shfl(rank, 0)) == 0;
     const int N = p.Ho * p.Wo, KK = p.kh * p.kw, cs = p.G * p.Cgp;
-    const int nch = p.Kp / KC, last = nch - 1;
+    const int nch_all = p.Kp / KC;              // chunks of the packed weight rows
+    const int nch = p.nch_eff, last = nch - 1;  // chunks walked per tile (see FwdParams)
     const int ntile = p.tiles, G = gridDim.x;
     // this workgroup's tiles are the dispatch ids blockIdx.x + k*G, k = 0..
     const int my_tiles = blockIdx.x < ntile ? (ntile - 1 - blockIdx.x) / G + 1 : 0;
@@ -401,7 +416,8 @@ __global__ __launch_bounds__(512) void dcn2_fwd_ws_kernel(const FwdParams p) {
     // stores they issue) of different workgroups are spread over time instead
     // of hitting HBM all at once.  j counts the chunks done in the tile.
     const int rot = blockIdx.x % nch;
-    struct Cursor { int k, j, ch, b, n0, m0; };
+    // (tap, i): position in the chunk walk, ch = tap*cpt + cb + i the packed chunk
+    struct Cursor { int k, j, tap, i, ch, b, n0, m0; };
     // Cursor fields are wave-uniform; readfirstlane keeps them in SGPRs.
     // Otherwise (the role branch is divergent code to the compiler) they
     // live in VGPRs, the chunk-table reads become vector loads, and waiting
@@ -412,13 +428,16 @@ __global__ __launch_bounds__(512) void dcn2_fwd_ws_kernel(const FwdParams p) {
         const int mt = t % p.mtiles, r = t / p.mtiles;
         c.n0 = uni((r % p.ntiles) * BN);
         c.b = uni(r / p.ntiles);
-        c.m0 = uni(mt * 4 * ROWS);
+        c.m0 = uni((p.mt_base + mt) * 4 * ROWS);
     };
     auto cursor = [&](int g) __attribute__((always_inline)) {
         Cursor c;
         c.k = uni(g / nch);
         c.j = uni(g - c.k * nch);
-        c.ch = uni(c.j + rot < nch ? c.j + rot : c.j + rot - nch);
+        const int r = c.j + rot < nch ? c.j + rot : c.j + rot - nch;
+        c.tap = uni(r / p.cpw);
+        c.i = uni(r - c.tap * p.cpw);
+        c.ch = uni(c.tap * p.cpt + p.cb + c.i);
         set_tile(c);
         return c;
     };
@@ -427,7 +446,11 @@ __global__ __launch_bounds__(512) void dcn2_fwd_ws_kernel(const FwdParams p) {
     // volatile asm keeps the (rare) tile change a real branch: if-converted,
     // its divisions would run every step on the scalar unit.
     auto advance = [&](Cursor &c, auto &&on_tile) __attribute__((always_inline)) {
-        c.ch = uni(c.ch + 1 == nch ? 0 : c.ch + 1);
+        // next chunk of the walk: i + 1, else the next tap (the walk wraps at KK)
+        const bool wrap_i = c.i + 1 == p.cpw, wrap_t = wrap_i && c.tap + 1 == KK;
+        c.ch = uni(wrap_t ? p.cb : (wrap_i ? c.ch + 1 + p.cpt - p.cpw : c.ch + 1));
+        c.tap = uni(wrap_t ? 0 : (wrap_i ? c.tap + 1 : c.tap));
+        c.i = uni(wrap_i ? 0 : c.i + 1);
         c.j = uni(c.j + 1);
         if (c.j == nch) {
             asm volatile("");
@@ -562,7 +585,7 @@ __global__ __launch_bounds__(512) void dcn2_fwd_ws_kernel(const FwdParams p) {
         // c.ch; wrow = first fragment of this wave's rows of the next tile's M block
         const T *wrow;
         auto set_wrow = [&](const Cursor &c) __attribute__((always_inline)) {
-            wrow = wbase + (size_t)((c.m0 + rw * ROWS) / 32) * nch * NKS * 64 * KPL;
+            wrow = wbase + (size_t)((c.m0 + rw * ROWS) / 32) * nch_all * NKS * 64 * KPL;
         };
         auto load_a = [&](auto set_c, const Cursor &c) __attribute__((always_inline)) {
             constexpr int SET = decltype(set_c)::value;
@@ -572,7 +595,7 @@ __global__ __launch_bounds__(512) void dcn2_fwd_ws_kernel(const FwdParams p) {
 #pragma unroll
                 for (int ks = 0; ks < NKS; ++ks)
                     a[SET][i][ks] = *reinterpret_cast<const frag *>(
-                        w0 + ((size_t)i * nch * NKS + ks) * 64 * KPL);
+                        w0 + ((size_t)i * nch_all * NKS + ks) * 64 * KPL);
         };
         auto mfma_stage = [&](auto set_c) __attribute__((always_inline)) {
             constexpr int SET = decltype(set_c)::value;
@@ -837,7 +860,6 @@ template <typename T, int WM, int WN, int IB, int JB>
 static hipError_t launch_fwd_t(const Geo &g, const FwdParams &p0, hipStream_t s) {
     FwdParams p = p0;
     p.ntiles = ceil_div(g.N, 32 * JB * WN);
-    p.mtiles = g.Mp / (32 * IB * WM);
     p.tiles = g.B * p.ntiles * p.mtiles;
     p.out_vec = !p.out_nhwc && (g.N % 8 == 0) && (((uintptr_t)p.out & 15) == 0);
     if (p.mask)
@@ -853,7 +875,6 @@ template <typename T, int IB>
 static hipError_t launch_fwd_ws(const Geo &g, const FwdParams &p0, hipStream_t s) {
     FwdParams p = p0;
     p.ntiles = ceil_div(g.N, 128);
-    p.mtiles = g.Mp / (128 * IB);
     p.tiles = g.B * p.ntiles * p.mtiles;
     // 16-byte pieces of NCHW rows need N % 8 == 0, of channels-last pixels Cout % 8 == 0
     p.out_vec = (p.out_nhwc ? g.Cout % 8 == 0 : g.N % 8 == 0) && (((uintptr_t)p.out & 15) == 0);
@@ -896,24 +917,53 @@ static bool ws_two_waves_per_simd() {
     return ok;
 }
 
-// fp32 (and 2-byte types with more than kBiasRows padded output rows): block
-// tile 256x128 (8 waves of 32x128) when Cout > 128, else 128x128 (8 waves of
-// 64x32); both sample 128 pixels, one slot per thread.
+// One launch over the output rows [row0, row0 + rows) with M tile bm (256 or
+// 128 rows; rows and row0 are multiples of it).  fp32 (and 2-byte types with
+// more than kBiasRows padded output rows): block tile 256x128 (8 waves of
+// 32x128) when bm is 256, else 128x128 (8 waves of 64x32); both sample 128
+// pixels, one slot per thread.
 template <typename T>
-static hipError_t launch_fwd_dt(const Geo &g, const FwdParams &p, hipStream_t s) {
+static hipError_t launch_fwd_dt(const Geo &g, FwdParams p, int bm, int row0, int rows,
+                                hipStream_t s) {
+    p.mt_base = row0 / bm;
+    p.mtiles = rows / bm;
     if constexpr (sizeof(T) == 2) {
         if (g.Mp <= kBiasRows) {
-            if (g.BM == 256 && ws_two_waves_per_simd<T, 2>()) return launch_fwd_ws<T, 2>(g, p, s);
-            if (g.BM == 128 && ws_two_waves_per_simd<T, 1>()) return launch_fwd_ws<T, 1>(g, p, s);
+            if (bm == 256 && ws_two_waves_per_simd<T, 2>()) return launch_fwd_ws<T, 2>(g, p, s);
+            if (bm == 128 && ws_two_waves_per_simd<T, 1>()) return launch_fwd_ws<T, 1>(g, p, s);
         }
         // more than kBiasRows output rows (or a register count that would let
         // three waves share a SIMD): the non-specialised kernel
-        if (g.BM == 256) return launch_fwd_t<T, 8, 1, 1, 4>(g, p, s);
+        if (bm == 256) return launch_fwd_t<T, 8, 1, 1, 4>(g, p, s);
         return launch_fwd_t<T, 2, 4, 2, 1>(g, p, s);
     } else {
-        if (g.BM == 256) return launch_fwd_t<T, 8, 1, 1, 4>(g, p, s);
+        if (bm == 256) return launch_fwd_t<T, 8, 1, 1, 4>(g, p, s);
         return launch_fwd_t<T, 2, 4, 2, 1>(g, p, s);
     }
+}
+
+// Ungrouped (or not splittable): one launch over every row and chunk.  With
+// weight groups whose chunks never mix (Geo::gsplit): one launch per group
+// over its Cout/WG rows and its cpw chunks per tap, so no launch samples or
+// multiplies the zero blocks of the block-diagonal packed weight.
+template <typename T>
+static hipError_t launch_fwd_groups(const Geo &g, FwdParams p, hipStream_t s) {
+    p.cpt = g.cpt;
+    if (!g.gsplit) {
+        p.cb = 0;
+        p.cpw = g.cpt;
+        p.nch_eff = g.Kp / g.KC;
+        return launch_fwd_dt<T>(g, p, g.BM, 0, g.Mp, s);
+    }
+    const int cog = g.Cout / g.WG, bm = cog % 256 == 0 ? 256 : 128;
+    p.cpw = g.cpw;
+    p.nch_eff = g.KK * g.cpw;
+    for (int w = 0; w < g.WG; ++w) {
+        p.cb = w * g.cpw;
+        const hipError_t e = launch_fwd_dt<T>(g, p, bm, w * cog, cog, s);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 hipError_t launch_forward(const Geo &g, const void *xt, const void *wp, const void *tab,
@@ -950,9 +1000,9 @@ hipError_t launch_forward(const Geo &g, const void *xt, const void *wp, const vo
     p.Kp = g.Kp;
     p.Mp = g.Mp;
     switch (g.dtype) {
-    case DCN2_F16: return launch_fwd_dt<f16>(g, p, s);
-    case DCN2_BF16: return launch_fwd_dt<bf16>(g, p, s);
-    default: return launch_fwd_dt<float>(g, p, s);
+    case DCN2_F16: return launch_fwd_groups<f16>(g, p, s);
+    case DCN2_BF16: return launch_fwd_groups<bf16>(g, p, s);
+    default: return launch_fwd_groups<float>(g, p, s);
     }
 }
 

@@ -28,6 +28,11 @@ struct Geo {
     int Kp;         // packed GEMM K = KK*G*Cgp
     int BM;         // forward block tile in M (128 or 256)
     int Mp;         // Cout rounded up to BM
+    // Chunks per tap of the packed K order (G * Cgp / KC), and the weight-group
+    // walk: gsplit when every chunk lies in one weight group, group w's chunks
+    // of a tap are [w*cpw, (w+1)*cpw) and each group's Cout/WG rows are a
+    // multiple of 128, so the GEMMs can run per group over its own chunks.
+    int cpt, cpw, gsplit;
     // Offset / mask buffers (and their gradients): elements between images,
     // and whether the mask buffer holds logits that the kernels pass through
     // sigmoid (the offset-and-mask predictor's raw output, dcn2_*_om).

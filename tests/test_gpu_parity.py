@@ -258,6 +258,31 @@ def test_weight_groups(dtype, case):
         check(name, g, r, TOL[dtype])
 
 
+@pytest.mark.parametrize("case", [
+    # C, Cout, deformable groups, weight groups: every channel chunk of the
+    # packed K order lies in one weight group and each group has a multiple of
+    # 128 output channels, so the forward runs one launch per group over its
+    # own rows and chunks and grad_weight walks only the diagonal blocks
+    (128, 256, 1, 2),    # 128 rows per group (128-row tiles)
+    (256, 512, 2, 2),    # 256 rows per group, one weight group per deformable group
+    (256, 512, 4, 4),    # four groups of 128 rows
+    (256, 256, 4, 2),    # a weight group spans two deformable groups
+], ids=["c128_wg2", "c256_dg2_wg2", "c256_dg4_wg4", "c256_dg4_wg2"])
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+def test_weight_groups_split_per_group(dtype, case):
+    """Grouped GEMMs that skip the zero blocks of the block-diagonal weight:
+    forward and all five gradients against the oracle's grouped loops."""
+    C, Cout, G, WG = case
+    w, t = _small(dtype, B=2, C=C, H=11, W=13, Cout=Cout, G=G, osc=2.0, seed=13)
+    t["weight"] = t["weight"][:, : C // WG].contiguous()
+    out = gpu_forward(t, w.geometry())
+    grads = gpu_backward(t, w.geometry())
+    torch.cuda.synchronize()
+    check("output", out, oracle_forward(t, w.geometry()), TOL[dtype])
+    for name, g, r in zip(GRADS, grads, oracle_backward(t, w.geometry())):
+        check(name, g, r, TOL[dtype])
+
+
 # --------------------------------------------------------------------------- channels_last
 @pytest.mark.parametrize("case", [
     # dtype, C, deformable groups, Cout: the input is read in place when C/G is a
