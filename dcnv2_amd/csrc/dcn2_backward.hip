@@ -22,6 +22,7 @@
 //  finalize kernels: fp32 accumulators -> caller dtype and layout.
 #include <algorithm>
 #include <cstddef>
+#include <cstdlib>
 #include <type_traits>
 
 #include "dcn2_common.h"
@@ -1289,6 +1290,525 @@ __global__ __launch_bounds__(512) void dcn2_gradw_line_kernel(const BwdParams p)
 }
 
 // ---------------------------------------------------------------------------
+// Fused backward kernel: column gradient, grad_offset / grad_mask, the
+// grad_input hand-off, grad_weight and grad_bias in one pass over gO.  It
+// serves 2-byte types with one 256-row M chunk (Mp == 256), one K chunk per
+// deformable group (Cgp == KC) and gO rows that take 16-byte loads; other
+// shapes run dcn2_colgrad_kernel and a grad_weight kernel.
+//
+// Grid: pixel-tile ranges x K chunks, one workgroup of 4 waves per CU (one
+// wave per SIMD, so each wave has the whole register file of its SIMD).  A
+// workgroup keeps one K chunk, i.e. one (tap, group): its W'^T fragments stay
+// in registers and its grad_weight block gW[256][64] is accumulated in
+// registers over all of its tiles, then added to the fp32 accumulator once.
+// Wave w = (K block kb = w%2, pixel half P = w/2) of a tile of BN = 64 pixels
+// of one image.  Per tile, with the tile's gO [256][64] and the corner
+// gathers of its samples already in LDS:
+//   top      the loads of the next tile are issued (straight into the other
+//            LDS buffers): each wave's 64 gO rows, and the corner gathers of
+//            its 32 pixels x 32 channels, whose addresses come from the
+//            sampling descriptors computed here (one lane per pixel);
+//   phase A  cg[k][n] = sum_m W'^T[k][m] gO[m][n] for the wave's K block and
+//            pixels (MFMA), handed to the lanes through a wave-local LDS area;
+//            lane (pixel pair, 8 channels): partial corner sums
+//            S_q = sum_c cg_c x_c(corner q) -> LDS, the masked cg row of the
+//            sample's grad_input bucket -> memory, the blended columns -> LDS;
+//   phase B  grad_mask / grad_offset from both K blocks' corner sums (as in
+//            dcn2_colgrad_kernel); gW[m][k] += sum_n gO[m][n] col[k][n] (MFMA;
+//            wave w: gO rows 64w.., both K blocks).
+// The loads of a tile are issued a whole tile ahead and waited for once, at
+// the end of the tile before its last barrier.  A gather lane group of 4
+// lanes reads 64 contiguous bytes of one corner, so an instruction touches
+// 16 cache lines.
+//
+// LDS layouts (16-byte pieces XOR-permuted per line so that the transposing
+// 8-byte reads, the 16-byte reads and the 16-byte stores are free of bank
+// conflicts; a wave's 1 KiB load lands on consecutive LDS bytes, so each lane
+// loads the piece that belongs at its LDS slot):
+//   NCHW gO          [256 rows m][64 pixels], piece j of row r at
+//                    j ^ fused_swz(r); rows 64w.. are wave w's.
+//   channels-last gO [8 row blocks][64 pixels][32 rows], piece j (rows
+//                    8j..8j+7 of the block) of pixel n at j ^ fused_swz_cl(n);
+//                    blocks 2w, 2w+1 are wave w's.
+//   columns          [64 pixels][64 channels], piece j of pixel n at
+//                    j ^ fused_swz_c(n), read as grad_weight B fragments by
+//                    transposing reads.
+//   corner gathers   per wave [corner q][pixel group i][lane] 16-byte slots;
+//                    after they are read, the same bytes hold the wave's cg.
+__device__ __forceinline__ int fused_swz(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
+__device__ __forceinline__ int fused_swz_cl(int n) { return (((n >> 1) & 1) << 1) | ((n >> 2) & 1); }
+__device__ __forceinline__ int fused_swz_c(int n) { return ((n & 3) << 1) | ((n >> 1) & 1); }
+
+// Trash bytes each lane of the fused kernel may write (its widest hand-off row).
+constexpr int kFusedTrashLane = 32;
+// Zero bytes for the stage loads of gO rows past Cout or pixels past N.
+__device__ __attribute__((aligned(16))) const unsigned char dcn2_zero16[16 * 64] = {};
+
+// Global -> LDS copy of 16 bytes per lane: lane i's 16 bytes from `src` land
+// at LDS byte lds + 16*i (lds is wave-uniform).  Written as inline assembly so
+// that the compiler does not make later LDS reads wait for it (it cannot tell
+// which LDS bytes it writes); the kernel waits for it explicitly
+// (s_waitcnt vmcnt(0)) before the barrier after which the bytes are read, and
+// the bytes it overwrites were last read before the previous barrier.  (A
+// volatile asm statement stays between the barriers around it; without a
+// memory clobber, LDS reads of the other buffer may be scheduled across it.)
+// M0 holds the LDS base and is set right before the load.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(const void *src, unsigned lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+                 :
+                 : "v"(src), "s"(lds)
+                 : "m0");
+}
+#pragma clang diagnostic pop
+// Value of lane l ^ 1 / l ^ 2 (within each group of 4 lanes), by DPP quad permutes.
+__device__ __forceinline__ float quad_xor1(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, true));
+}
+__device__ __forceinline__ float quad_xor2(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, true));
+}
+__device__ __forceinline__ unsigned lds_addr(const void *p) {
+    return (unsigned)(size_t)(__attribute__((address_space(3))) const void *)p;
+}
+
+template <typename T, bool GN>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void dcn2_bwd_fused_kernel(const BwdParams p) {
+    static_assert(sizeof(T) == 2, "2-byte types");
+    using M = Mma<T>;
+    using frag = typename M::frag;
+    typedef typename RowOf<T>::type R;
+    typedef short s16x4 __attribute__((ext_vector_type(4)));
+    constexpr int KC = M::KC, KSTEP = M::KSTEP;
+    constexpr int BN = 64, MP = 256;
+    constexpr int NMS = MP / KSTEP;  // column-gradient MFMA steps (over M)
+    constexpr int NKS = BN / KSTEP;  // grad_weight MFMA steps (over pixels)
+    constexpr int LDX = 32 + 4;      // pitch (floats) of the wave-local cg area
+    constexpr int E = 8;             // channels of one 16-byte piece
+    constexpr int NST = E * (int)sizeof(R) / 16;  // 16-byte hand-off stores per pixel
+    constexpr int GLINE = GN ? 32 : BN;           // elements of one gO stage line
+    static_assert(KC == 64 && Unpack<T>::E == E && NST * 16 <= kFusedTrashLane, "geometry");
+
+    __shared__ __attribute__((aligned(16))) T sG[2][MP * BN];          // gO stage
+    __shared__ __attribute__((aligned(16))) uint4 sK[2][4][8][64];     // corner gathers / cg
+    __shared__ __attribute__((aligned(16))) T sC[BN][KC];              // blended columns
+    __shared__ __attribute__((aligned(16))) f32x4 sS[2][BN];           // corner sums per K block
+    __shared__ __attribute__((aligned(16))) f32x4 sD[2][4][32][3];     // sampling descriptors
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int kb = wave & 1, P = wave >> 1;
+    const int N = p.Ho * p.Wo, KK = p.kh * p.kw, cs = p.G * p.Cgp;
+    const int nch = KK * p.G;
+    const int tpi = p.tiles_per_img;  // tiles of BN pixels per image
+    // work item = (tile range sp, chunk c) with the chunk fastest, handed to
+    // XCDs in contiguous ranges: the workgroups of one XCD share tile ranges,
+    // so a gO tile is read from HBM about once per XCD
+    const int wi = xcd_remap(blockIdx.x, p.splits * nch);
+    const int c = wi % nch, sp = wi / nch;
+    const int T_total = p.B * tpi;
+    const int t_begin = (int)((long)T_total * sp / p.splits);
+    const int t_end = (int)((long)T_total * (sp + 1) / p.splits);
+    if (t_begin >= t_end) return;  // the whole workgroup
+    const int t_last = t_end - 1;
+    const ChunkEnt ce = ((const ChunkEnt *)p.tab)[c];
+    const int plane = ce.x;  // offset / mask plane g*KK + tap
+
+    // W'^T fragments of K block kb of chunk c (pack_weight_kernel layout 1:
+    // fragment (row block 2c + kb, step s) is one contiguous run of 64 lanes
+    // x 8 elements).
+    frag wa[NMS];
+    {
+        const T *wrow = (const T *)p.wt + (size_t)(c * (KC / 32) + kb) * NMS * 512 + lane * 8;
+#pragma unroll
+        for (int s = 0; s < NMS; ++s) wa[s] = *reinterpret_cast<const frag *>(wrow + s * 512);
+    }
+
+    // ---- loads of a tile into LDS buffer `buf` --------------------------------
+    // Sources of the wave's 64 gO rows (8 KiB): 8 loads of 1 KiB, load q to
+    // LDS byte go_lds(buf) + 1024 q.
+    auto go_lds = [&](int buf) __attribute__((always_inline)) {
+        return lds_addr(&sG[buf][0]) + wave * 8192;
+    };
+    auto go_sources = [&](int t, const void *(&srcs)[8]) __attribute__((always_inline)) {
+        const int b = t / tpi, n0 = (t - b * tpi) * BN;
+        const T *go = (const T *)p.gout + (size_t)b * p.Cout * N;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const void *src;
+            if constexpr (GN) {
+                const int n = 16 * (q & 3) + (lane >> 2);
+                const int m = 32 * (2 * wave + (q >> 2)) + 8 * ((lane & 3) ^ fused_swz_cl(n));
+                src = n0 + n < N && m < p.Cout ? (const void *)(go + (size_t)(n0 + n) * p.Cout + m)
+                                               : (const void *)(dcn2_zero16 + lane * 16);
+            } else {
+                const int r = 64 * wave + 8 * q + (lane >> 3);
+                const int n = n0 + 8 * ((lane & 7) ^ fused_swz(r));
+                src = r < p.Cout && n < N ? (const void *)(go + (size_t)r * N + n)
+                                          : (const void *)(dcn2_zero16 + lane * 16);
+            }
+            srcs[q] = src;
+        }
+    };
+    // NCHW: element (row r, pixel x); channels-last: element (pixel n, row m);
+    // columns: element (pixel n, channel k)
+    auto at_rm = [&](int buf, int r, int x) __attribute__((always_inline)) {
+        return &sG[buf][r * BN + (((x >> 3) ^ fused_swz(r)) << 3) + (x & 7)];
+    };
+    auto at_nm = [&](int buf, int n, int m) __attribute__((always_inline)) {
+        return &sG[buf][(m >> 5) * (BN * 32) + n * 32 + ((((m >> 3) & 3) ^ fused_swz_cl(n)) << 3) +
+                        (m & 7)];
+    };
+    auto at_c = [&](int n, int k) __attribute__((always_inline)) {
+        return &sC[n][(((k >> 3) ^ fused_swz_c(n)) << 3) + (k & 7)];
+    };
+    // Transposing read (ds_read_b64_tr_b16: within 16 lanes, lane i receives
+    // element i%4 of the 4-element pieces that lanes i/4, 4 + i/4, 8 + i/4,
+    // 12 + i/4 point at).  Lane L of 16-lane group g points at 4 consecutive
+    // elements of line (l0 + 8*(g>>1) + 4*hh + L/4), starting at element
+    // x0 + 16*(g&1) + 4*(L%4) of the line; lane l then holds element
+    // x0 + l%32 of lines l0 + 8*(l/32) .. +7: an MFMA fragment whose 8 K
+    // values run across the lines.
+    auto tr_frag = [&](auto addr, int l0, int x0) __attribute__((always_inline)) {
+        const int g = lane >> 4, li = lane & 15;
+        s16x4 h[2];
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh)
+            h[hh] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) s16x4 *)addr(
+                    l0 + 8 * (g >> 1) + 4 * hh + (li >> 2), x0 + 16 * (g & 1) + 4 * (li & 3)));
+        return __builtin_bit_cast(frag, __builtin_shufflevector(h[0], h[1], 0, 1, 2, 3, 4, 5, 6, 7));
+    };
+    // Column-gradient B fragment of step s: gO rows 16s + 8*(l/32) .., pixel
+    // 32P + l%32.  grad_weight A fragment of row block j, step ks: row
+    // 64 wave + 32 j + l%32, pixels 16 ks + 8*(l/32) ...
+    auto go_bfrag = [&](int buf, int s) __attribute__((always_inline)) {
+        if constexpr (GN) {
+            return *reinterpret_cast<const frag *>(
+                at_nm(buf, P * 32 + (lane & 31), s * KSTEP + 8 * (lane >> 5)));
+        } else {
+            return tr_frag([&](int r, int x) { return at_rm(buf, r, x); }, s * KSTEP, P * 32);
+        }
+    };
+    auto go_afrag = [&](int buf, int j, int ks) __attribute__((always_inline)) {
+        if constexpr (GN) {
+            return tr_frag([&](int n, int m) { return at_nm(buf, n, m); }, ks * KSTEP,
+                           wave * 64 + j * 32);
+        } else {
+            return *reinterpret_cast<const frag *>(
+                at_rm(buf, wave * 64 + j * 32 + (lane & 31), ks * KSTEP + 8 * (lane >> 5)));
+        }
+    };
+
+    // ---- sampling (one lane per pixel: pixel 32P + lane%32 of the tile) ------
+    const int pl = lane & 31;
+    struct OM {
+        T dy, dx, m;
+        int sx;
+    };
+    auto load_om = [&](int t, OM &o) __attribute__((always_inline)) {
+        const int b = t / tpi;
+        const int nr = (t - b * tpi) * BN + P * 32 + pl;
+        const int nn = nr < N ? nr : 0;
+        const T *offs = (const T *)p.offset + (size_t)b * p.off_bs + (size_t)plane * 2 * N;
+        // (without a mask the load re-reads the offset: no load in a branch)
+        const T *mk = p.mask ? (const T *)p.mask + (size_t)b * p.msk_bs + (size_t)plane * N : offs;
+        o.dy = offs[nn];
+        o.dx = offs[N + nn];
+        const T mraw = mk[nn];
+        o.m = p.mask ? mraw : (T)1.0f;
+        o.sx = p.sidx[((size_t)b * p.G * KK + plane) * N + nn];
+    };
+    // Descriptors of tile t's pixel into sD[buf][wave][pl] (corner weights;
+    // mask value, bucket row, fractions; corner validity) and the sources of
+    // the corner gathers of the wave's pixels: load j = 2q + i brings corner q
+    // of pixels 16i + l/4, 16 bytes (8 channels) per lane, to LDS byte
+    // gather_lds(buf) + 1024 j.
+    auto gather_lds = [&](int buf) __attribute__((always_inline)) {
+        return lds_addr(&sK[buf][wave][0][0]);
+    };
+    auto sample = [&](int t, const OM &o, int buf, const void *(&srcs)[8]) __attribute__((always_inline)) {
+        const int b = t / tpi;
+        const int nr = (t - b * tpi) * BN + P * 32 + pl;
+        const bool live = nr < N;
+        int oy = 0, ox = 0;
+        if (live) {
+            oy = nr / p.Wo;
+            ox = nr - oy * p.Wo;
+        }
+        const float y = (float)(oy * p.sh - p.ph + ce.y) + to_f32(o.dy);
+        const float x = (float)(ox * p.sw - p.pw + ce.z) + to_f32(o.dx);
+        const float mv = live ? mask_value(to_f32(o.m), p.msk_logit) : 0.0f;
+        const SamplePos spos = sample_pos(live ? y : -2.0f, live ? x : -2.0f, p.H, p.W);
+        const Corners cr = make_corners(spos, mv, p.W, cs);
+        const int valid = (spos.vy0 && spos.vx0 ? 1 : 0) | (spos.vy0 && spos.vx1 ? 2 : 0) |
+                          (spos.vy1 && spos.vx0 ? 4 : 0) | (spos.vy1 && spos.vx1 ? 8 : 0);
+        if (lane < 32) {
+            sD[buf][wave][pl][0] = f32x4{cr.w[0], cr.w[1], cr.w[2], cr.w[3]};
+            sD[buf][wave][pl][1] = f32x4{mv, __int_as_float(live ? o.sx : -1), spos.ly, spos.lx};
+            sD[buf][wave][pl][2] = f32x4{__int_as_float(valid), 0.0f, 0.0f, 0.0f};
+        }
+        const T *xb = (const T *)p.xt + (size_t)b * p.H * p.W * cs + ce.w + kb * 32 + (lane & 3) * E;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+                srcs[2 * q + i] = xb + __shfl(cr.off[q], 16 * i + (lane >> 2), 64);
+    };
+
+    // this lane's kFusedTrashLane bytes of dcn2_trash
+    constexpr int kTrashWaves = kTrashBytes / (64 * kFusedTrashLane);
+    uint4 *const trash_v = reinterpret_cast<uint4 *>(dcn2_trash) +
+                           ((blockIdx.x * 4 + wave) % kTrashWaves) * (64 * kFusedTrashLane / 16) +
+                           lane * (kFusedTrashLane / 16);
+    T *const trash_t = reinterpret_cast<T *>(trash_v);
+
+    // ---- phase A --------------------------------------------------------------
+    // Column gradient of K block kb, pixels 32P .. 32P+31 of the tile.
+    // after(s) runs after the MFMA of step s (it issues the next tile's loads,
+    // spread over the MFMAs).  The fragments are read two steps ahead of their
+    // MFMA; each step ends in a scheduling barrier, which keeps that order and
+    // the loads where they are.
+    auto colgrad_mfma = [&](int buf, auto after) __attribute__((always_inline)) {
+        f32x16 acc;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+        frag bf[NMS];
+        bf[0] = go_bfrag(buf, 0);
+        bf[1] = go_bfrag(buf, 1);
+#pragma unroll
+        for (int s = 0; s < NMS; ++s) {
+            if (s + 2 < NMS) bf[s + 2] = go_bfrag(buf, s + 2);
+            acc = M::mma(wa[s], bf[s], acc);
+            after(s);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        return acc;
+    };
+    // Lane (pixel pair pq = l/4: pixels pq, pq+16 of the wave; channels
+    // 32kb + 8(l%4) ..): corner sums, hand-off and blend.
+    const int pq = lane >> 2, cq = lane & 3;
+    auto consume = [&](int buf, int t, const f32x16 &acc) __attribute__((always_inline)) {
+        uint4 raw[4][2];
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int i = 0; i < 2; ++i) raw[q][i] = sK[buf][wave][q * 2 + i][lane];
+        f32x4 d0[2], d1[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            d0[i] = sD[buf][wave][pq + 16 * i][0];
+            d1[i] = sD[buf][wave][pq + 16 * i][1];
+        }
+        // cg through the wave's area (it reuses the gather bytes just read;
+        // a wave's LDS operations are done in order)
+        float *const sX = reinterpret_cast<float *>(&sK[buf][wave][0][0]);
+        __builtin_amdgcn_wave_barrier();
+        // acc[r] = cg[32kb + 8(r/4) + 4(l/32) + r%4][32P + l%32]
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            *reinterpret_cast<f32x4 *>(&sX[(lane & 31) * LDX + 8 * j + 4 * (lane >> 5)]) =
+                f32x4{acc[4 * j], acc[4 * j + 1], acc[4 * j + 2], acc[4 * j + 3]};
+        __builtin_amdgcn_wave_barrier();
+        float cgv[2][E];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const f32x4 v = *reinterpret_cast<const f32x4 *>(&sX[(pq + 16 * i) * LDX + cq * E + 4 * h]);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) cgv[i][4 * h + e] = v[e];
+            }
+        // corner sums over the lane's 8 channels, then over the 4 lanes of the pixel
+        f32x4 S[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                float v[E];
+                Unpack<T>::run(raw[q][i], v);
+                float s = 0.0f;
+#pragma unroll
+                for (int e = 0; e < E; ++e) s = fmaf(cgv[i][e], v[e], s);
+                s += quad_xor1(s);
+                s += quad_xor2(s);
+                S[i][q] = s;
+            }
+        if (cq < 2) sS[kb][P * 32 + pq + 16 * cq] = cq ? S[1] : S[0];
+        // masked column-gradient rows
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int srow = __float_as_int(d1[i][1]);
+            float mrow[E];
+#pragma unroll
+            for (int e = 0; e < E; ++e) mrow[e] = cgv[i][e] * d1[i][0];
+            uint4 *row = srow >= 0
+                             ? reinterpret_cast<uint4 *>((R *)p.cgm + (size_t)srow * KC + kb * 32 + cq * E)
+                             : trash_v;
+#pragma unroll
+            for (int u = 0; u < NST; ++u) row[u] = pack16<R>(mrow + u * (16 / sizeof(R)));
+        }
+        // blended columns
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            float col[E], v[E];
+#pragma unroll
+            for (int e = 0; e < E; ++e) col[e] = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                Unpack<T>::run(raw[q][i], v);
+#pragma unroll
+                for (int e = 0; e < E; ++e) col[e] = fmaf(d0[i][q], v[e], col[e]);
+            }
+            *reinterpret_cast<uint4 *>(at_c(P * 32 + pq + 16 * i, kb * 32 + cq * E)) = pack16<T>(col);
+        }
+    };
+
+    // ---- phase B --------------------------------------------------------------
+    // grad_mask / grad_offset of pixel 32P + l%32 from both K blocks' corner
+    // sums: one store per lane (kb 0: grad_off_y, grad_off_x; kb 1:
+    // grad_mask, none; a pixel past N stores to dcn2_trash).
+    auto finish_sums = [&](int buf, int t) __attribute__((always_inline)) {
+        const int b = t / tpi;
+        const int nr = (t - b * tpi) * BN + P * 32 + pl;
+        const f32x4 S = sS[0][P * 32 + pl] + sS[1][P * 32 + pl];
+        const f32x4 d1 = sD[buf][wave][pl][1];
+        const int valid = __float_as_int(sD[buf][wave][pl][2][0]);
+        const float mv = d1[0], fly = d1[2], flx = d1[3];
+        const float S0 = (valid & 1) ? S[0] : 0.0f, S1 = (valid & 2) ? S[1] : 0.0f;
+        const float S2 = (valid & 4) ? S[2] : 0.0f, S3 = (valid & 8) ? S[3] : 0.0f;
+        const float hy = 1.0f - fly, hx = 1.0f - flx;
+        float v;
+        T *dst = trash_t;
+        const bool hi = lane >= 32;
+        if (kb == 0) {
+            v = hi ? mv * (hy * (S1 - S0) + fly * (S3 - S2))   // grad_off_x
+                   : mv * (hx * (S2 - S0) + flx * (S3 - S1));  // grad_off_y
+            if (nr < N) dst = (T *)p.goff + (size_t)b * p.off_bs + (size_t)plane * 2 * N + (hi ? N : 0) + nr;
+        } else {
+            const float gmr = hy * hx * S0 + hy * flx * S1 + fly * hx * S2 + fly * flx * S3;
+            // d/d(logit) of sigmoid = s (1 - s), s = the mask value used
+            v = p.msk_logit ? gmr * mv * (1.0f - mv) : gmr;
+            if (nr < N && !hi && p.gmask)
+                dst = (T *)p.gmask + (size_t)b * p.msk_bs + (size_t)plane * N + nr;
+        }
+        *dst = from_f32<T>(v);
+    };
+    f32x16 gacc[2][2];  // [gO row block j][K block i]
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) gacc[j][i][r] = 0.0f;
+    float bsum[2] = {0.0f, 0.0f};
+    const bool do_bias = p.gb_acc != nullptr && c == 0;
+    // acc + the sum of a fragment's 8 values (four 2-element dot products
+    // with (1, 1), accumulated in fp32)
+    auto sum8 = [](frag a, float acc) __attribute__((always_inline)) {
+        typedef T t2 __attribute__((ext_vector_type(2)));
+        const t2 one = {(T)1.0f, (T)1.0f};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const t2 pr2 = {a[2 * e], a[2 * e + 1]};
+            if constexpr (std::is_same<T, f16>::value)
+                acc = __builtin_amdgcn_fdot2(pr2, one, acc, false);
+            else
+                acc = __builtin_amdgcn_fdot2_f32_bf16(pr2, one, acc, false);
+        }
+        return acc;
+    };
+    // (grad_bias: compile-time switch, so no branch sits between the MFMAs)
+    auto gradw_mfma = [&](int buf, auto bias_c, auto after) __attribute__((always_inline)) {
+        frag a[NKS][2], bf[NKS][2];
+        auto rd = [&](int ks) __attribute__((always_inline)) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j) a[ks][j] = go_afrag(buf, j, ks);
+#pragma unroll
+            for (int i = 0; i < 2; ++i) bf[ks][i] = tr_frag(at_c, ks * KSTEP, i * 32);
+        };
+        rd(0);
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) {
+            if (ks + 1 < NKS) rd(ks + 1);
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    gacc[j][i] = M::mma(a[ks][j], bf[ks][i], gacc[j][i]);
+                    after(4 * ks + 2 * j + i);
+                }
+            if constexpr (decltype(bias_c)::value) {
+#pragma unroll
+                for (int j = 0; j < 2; ++j) bsum[j] = sum8(a[ks][j], bsum[j]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    // ---- the tiles ----------------------------------------------------------------
+    auto tiles = [&](auto bias_c) __attribute__((always_inline)) {
+        OM om;
+        const void *gsrc[8], *ksrc[8];
+        load_om(t_begin, om);
+        go_sources(t_begin, gsrc);
+        sample(t_begin, om, 0, ksrc);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) dma16(gsrc[q], go_lds(0) + q * 1024);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) dma16(ksrc[j], gather_lds(0) + j * 1024);
+        load_om(min(t_begin + 1, t_last), om);
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the stage loads
+        __syncthreads();
+        for (int t = t_begin; t < t_end; ++t) {
+            const int buf = (t - t_begin) & 1;
+            const int tn = min(t + 1, t_last);
+            // the next tile's loads: gO rows during the column-gradient MFMAs,
+            // corner gathers during the grad_weight MFMAs
+            go_sources(tn, gsrc);
+            sample(tn, om, buf ^ 1, ksrc);
+            load_om(min(t + 2, t_last), om);
+            const unsigned gl = go_lds(buf ^ 1), kl = gather_lds(buf ^ 1);
+            consume(buf, t, colgrad_mfma(buf, [&](int s) __attribute__((always_inline)) {
+                        if (s & 1) dma16(gsrc[s >> 1], gl + (s >> 1) * 1024);
+                    }));
+            __syncthreads();
+            finish_sums(buf, t);
+            gradw_mfma(buf, bias_c, [&](int s) __attribute__((always_inline)) {
+                if (s & 1) dma16(ksrc[s >> 1], kl + (s >> 1) * 1024);
+            });
+            __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the next tile's stage loads
+            __syncthreads();
+        }
+    };
+    if (do_bias) tiles(std::true_type{});
+    else tiles(std::false_type{});
+
+    // grad_weight block of this workgroup: rows 64*wave .., columns c*KC ..
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int k = c * KC + i * 32 + (lane & 31);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int m = wave * 64 + j * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                if (m < p.Cout) unsafeAtomicAdd(p.gw_acc + (size_t)m * p.Kp + k, gacc[j][i][r]);
+            }
+        }
+    if (do_bias) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const float v = bsum[j] + shfl_xor_f(bsum[j], 32);
+            const int m = wave * 64 + j * 32 + (lane & 31);
+            if (lane < 32 && m < p.Cout) unsafeAtomicAdd(p.gb_acc + m, v);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // grad_input gather.  One block per bucket (image, group, 16x16 cell tile).
 // The bucket's records are taken in batches of up to kGatherBatch; each
 // batch is counting-sorted by cell in LDS, together with the fractional
@@ -1724,8 +2244,24 @@ static hipError_t backward_t(const Geo &g, const BwdParams &p0, void *grad_input
         }
     }
     prof_end(DCN2_STAGE_BWD_PACK, s);
+    int dev = 0, ncu = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        ncu <= 0)
+        ncu = 256;
+    // The fused kernel (column gradient and grad_weight in one pass) serves
+    // 2-byte types with Mp == 256, one K chunk per deformable group and gO
+    // rows that take 16-byte loads.
+    // DCN2_BWD_FUSED=0 in the environment selects the two-kernel path for
+    // every shape (the tests compare both paths).
+    bool fused = false;
+    const char *fenv = std::getenv("DCN2_BWD_FUSED");
+    if constexpr (sizeof(T) == 2)
+        fused = !(fenv && fenv[0] == '0') && g.Mp == 256 && g.Cgp == g.KC && p.go_vec &&
+                (long long)g.Cout * g.N * (long long)sizeof(T) <= kGoOutOfRange;
     if (g.B > 0) {
         // 2. column gradient: grad_offset, grad_mask, grad_input accumulation
+        //    (and grad_weight / grad_bias when fused)
         prof_begin(DCN2_STAGE_BWD_COLGRAD, s);
         {
             // buckets: count, scan, place (exact sizes, see dcn2_bucket_kernel)
@@ -1741,6 +2277,22 @@ static hipError_t backward_t(const Geo &g, const BwdParams &p0, void *grad_input
             if (tab) dcn2_bucket_kernel<true><<<bgrid, 256, 0, s>>>(p, p.offset, f32, isbf);
             else dcn2_bucket_global_kernel<true><<<bgrid, 256, 0, s>>>(p, p.offset, f32, isbf);
             if ((e = hipGetLastError()) != hipSuccess) return e;
+            if constexpr (sizeof(T) == 2) {
+                if (fused) {
+                    // one workgroup per CU: each K chunk gets CUs/nch ranges of
+                    // 64-pixel tiles
+                    BwdParams pf = p;
+                    const int nch = g.KK * g.G;
+                    pf.tiles_per_img = ceil_div(g.N, 64);
+                    pf.splits = std::max(1, std::min(ncu / nch, g.B * pf.tiles_per_img));
+                    const int grid = pf.splits * nch;
+                    if (p.go_nhwc) dcn2_bwd_fused_kernel<T, true><<<grid, 256, 0, s>>>(pf);
+                    else dcn2_bwd_fused_kernel<T, false><<<grid, 256, 0, s>>>(pf);
+                    if ((e = hipGetLastError()) != hipSuccess) return e;
+                }
+            }
+        }
+        if (!fused) {
             dim3 grid(p.tiles_per_img, g.B);
             // W'^T staged in LDS when a chunk of it fits (Mp <= 256); gO resident
             // in registers when one M chunk covers all rows.  fp32 keeps the
@@ -1788,8 +2340,8 @@ static hipError_t backward_t(const Geo &g, const BwdParams &p0, void *grad_input
         if ((e = hipGetLastError()) != hipSuccess) return e;
         prof_end(DCN2_STAGE_BWD_GATHER, s);
         // 3. grad_weight / grad_bias
-        prof_begin(DCN2_STAGE_BWD_GRADW, s);
-        {
+        if (!fused) {
+            prof_begin(DCN2_STAGE_BWD_GRADW, s);
             // weight groups split per group (Geo::gsplit): an M chunk must lie
             // in one group, whose rows are a multiple of 128
             const int cog = g.gsplit ? g.Cout / g.WG : 0;
@@ -1804,11 +2356,6 @@ static hipError_t backward_t(const Geo &g, const BwdParams &p0, void *grad_input
             // One workgroup per CU: each (K chunk, M chunk) pair gets CUs/(nch*nmc)
             // contiguous pixel-tile ranges, so the partial grad_weight tiles a
             // workgroup adds with fp32 atomics are few (one set per range).
-            int dev = 0, ncu = 0;
-            if (hipGetDevice(&dev) != hipSuccess ||
-                hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-                ncu <= 0)
-                ncu = 256;
             int S = ncu / (nch * nmc);
             S = std::max(1, std::min(S, T_total));
             p.splits = S;
@@ -1833,8 +2380,8 @@ static hipError_t backward_t(const Geo &g, const BwdParams &p0, void *grad_input
 #undef DCN2_GRADW_MB
 #undef DCN2_GRADW
             if ((e = hipGetLastError()) != hipSuccess) return e;
+            prof_end(DCN2_STAGE_BWD_GRADW, s);
         }
-        prof_end(DCN2_STAGE_BWD_GRADW, s);
         // 4. grad_input to the caller's layout
         prof_begin(DCN2_STAGE_BWD_FINAL, s);
         {

@@ -44,13 +44,23 @@ template <> struct Unpack<float> {
     }
 };
 
-// Packs 16/sizeof(T) floats into one 16-byte register of T (round to nearest even).
+// Packs 16/sizeof(T) floats into one 16-byte register of T (round to nearest
+// even).  2-byte types convert pairs (one v_cvt_pk_{f16,bf16}_f32 each).
 template <typename T> __device__ __forceinline__ uint4 pack16(const float *v) {
     constexpr int E = 16 / sizeof(T);
-    T t[E];
+    if constexpr (sizeof(T) == 2) {
+        typedef float f2 __attribute__((ext_vector_type(2)));
+        typedef T t2 __attribute__((ext_vector_type(2)));
+        t2 t[E / 2];
 #pragma unroll
-    for (int e = 0; e < E; ++e) t[e] = (T)v[e];
-    return __builtin_bit_cast(uint4, t);
+        for (int e = 0; e < E / 2; ++e) t[e] = __builtin_convertvector(f2{v[2 * e], v[2 * e + 1]}, t2);
+        return __builtin_bit_cast(uint4, t);
+    } else {
+        T t[E];
+#pragma unroll
+        for (int e = 0; e < E; ++e) t[e] = (T)v[e];
+        return __builtin_bit_cast(uint4, t);
+    }
 }
 
 // Geometry of one sampling problem (one image at a time).

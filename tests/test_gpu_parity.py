@@ -449,3 +449,60 @@ def test_bucket_table_beyond_lds(dtype):
         check(name, g, r, TOL[dtype])
     del out, grads
     torch.cuda.empty_cache()
+
+
+# --------------------------------------------------------------------------- fused backward
+def _backward_path(t, geo, go, fused):
+    """Backward with the fused kernel allowed or not (DCN2_BWD_FUSED), and
+    whether the separate grad_weight stage ran (it does not when fused)."""
+    prev = os.environ.get("DCN2_BWD_FUSED")
+    os.environ["DCN2_BWD_FUSED"] = "1" if fused else "0"
+    try:
+        _C.profile_enable(True)
+        for s in _C.STAGES:
+            _C.profile_read(s)
+        args = [None if t[k] is None else t[k].to(DEV) for k in IN5]
+        grads = _C.dcn_v2_backward(*args, go, *_args(geo))
+        torch.cuda.synchronize()
+        gradw_launches = _C.profile_read("bwd_gradw")[1]
+    finally:
+        _C.profile_enable(False)
+        if prev is None:
+            del os.environ["DCN2_BWD_FUSED"]
+        else:
+            os.environ["DCN2_BWD_FUSED"] = prev
+    return grads, gradw_launches
+
+
+@pytest.mark.parametrize("case", [
+    # C, deformable groups, Cout, H, W, kernel, mask and bias, grad_output channels_last
+    (64, 1, 200, 12, 14, 3, True, False),   # Cout not a multiple of 32; last pixel tile partial
+    (128, 2, 256, 9, 16, 3, False, False),  # two deformable groups; no mask, no bias
+    (48, 1, 160, 12, 12, 3, True, False),   # 48 channels padded to the 64-channel chunk
+    (64, 1, 136, 13, 11, 3, True, True),    # channels-last grad_output, N % 8 != 0
+    (64, 1, 256, 10, 16, 1, True, False),   # 1x1 kernel
+], ids=["cout200", "dg2_nomask", "c48_padded", "go_channels_last", "k1"])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["float16", "bfloat16"])
+def test_fused_backward(dtype, case):
+    """The fused backward kernel (2-byte types, 129..256 output channels, one
+    channel chunk per deformable group, 16-byte grad_output rows) takes the
+    place of the column-gradient and grad_weight kernels: all five gradients
+    against the oracle, and the two-kernel path on the same inputs likewise."""
+    C, G, Cout, H, W, k, mb, go_cl = case
+    w, t = _small(dtype, B=2, C=C, H=H, W=W, Cout=Cout, k=k, p=k // 2, G=G, osc=2.0, seed=21)
+    if not mb:
+        t["mask"] = None
+        t["bias"] = None
+    geo = w.geometry()
+    go = t["grad_output"].to(DEV)
+    if go_cl:
+        go = go.to(memory_format=torch.channels_last)
+    rg = oracle_backward(t, geo)
+    for fused in (True, False):
+        grads, gradw_launches = _backward_path(t, geo, go, fused)
+        assert (gradw_launches == 0) == fused, "fused kernel selection"
+        if not mb:
+            assert grads[2] is None and grads[4] is None
+        for name, g, r in zip(GRADS, grads, rg):
+            if g is not None:
+                check(f"{name} ({'fused' if fused else 'two kernels'})", g, r, TOL[dtype])
