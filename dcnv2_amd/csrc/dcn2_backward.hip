@@ -1374,7 +1374,7 @@ __device__ __forceinline__ unsigned lds_addr(const void *p) {
 }
 
 template <typename T, bool GN>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void dcn2_bwd_fused_kernel(const BwdParams p) {
     static_assert(sizeof(T) == 2, "2-byte types");
     using M = Mma<T>;
@@ -1383,23 +1383,27 @@ void dcn2_bwd_fused_kernel(const BwdParams p) {
     typedef short s16x4 __attribute__((ext_vector_type(4)));
     constexpr int KC = M::KC, KSTEP = M::KSTEP;
     constexpr int BN = 64, MP = 256;
-    constexpr int NMS = MP / KSTEP;  // column-gradient MFMA steps (over M)
-    constexpr int NKS = BN / KSTEP;  // grad_weight MFMA steps (over pixels)
-    constexpr int LDX = 32 + 4;      // pitch (floats) of the wave-local cg area
-    constexpr int E = 8;             // channels of one 16-byte piece
-    constexpr int NST = E * (int)sizeof(R) / 16;  // 16-byte hand-off stores per pixel
-    constexpr int GLINE = GN ? 32 : BN;           // elements of one gO stage line
+    constexpr int NMS = MP / KSTEP / 2;  // column-gradient MFMA steps of one M half
+    constexpr int NKS = BN / KSTEP;      // grad_weight MFMA steps (over pixels)
+    constexpr int LDX = 32 + 4;          // pitch (floats) of the cg areas
+    constexpr int E = 8;                 // channels of one 16-byte piece
+    constexpr int NST = E * (int)sizeof(R) / 16;  // 16-byte hand-off stores per lane
     static_assert(KC == 64 && Unpack<T>::E == E && NST * 16 <= kFusedTrashLane, "geometry");
 
-    __shared__ __attribute__((aligned(16))) T sG[2][MP * BN];          // gO stage
-    __shared__ __attribute__((aligned(16))) uint4 sK[2][4][8][64];     // corner gathers / cg
-    __shared__ __attribute__((aligned(16))) T sC[BN][KC];              // blended columns
-    __shared__ __attribute__((aligned(16))) f32x4 sS[2][BN];           // corner sums per K block
-    __shared__ __attribute__((aligned(16))) f32x4 sD[2][4][32][3];     // sampling descriptors
+    __shared__ __attribute__((aligned(16))) T sG[2][MP * BN];         // gO stage (double)
+    __shared__ __attribute__((aligned(16))) uint4 sK[8][4][64];       // corner gathers per wave
+    __shared__ __attribute__((aligned(16))) float sX[2][4][32][LDX];  // cg partials [M half][block]
+    __shared__ __attribute__((aligned(16))) T sC[BN][KC];             // blended columns
+    __shared__ __attribute__((aligned(16))) f32x4 sS[2][BN];          // corner sums per K block
+    __shared__ __attribute__((aligned(16))) f32x4 sD[2][BN][3];       // sampling descriptors
+    __shared__ int sV[2][BN];                                         // corner validity bits
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int kb = wave & 1, P = wave >> 1;
+    // column-gradient block (K block kb, pixels 32P..) and M half mh of this
+    // wave; its gathered / consumed pixels are 32P + 16mh .. +15
+    const int kb = wave & 1, P = (wave >> 1) & 1, mh = wave >> 2;
+    const int blk = wave & 3, px0 = 32 * P + 16 * mh;
     const int N = p.Ho * p.Wo, KK = p.kh * p.kw, cs = p.G * p.Cgp;
     const int nch = KK * p.G;
     const int tpi = p.tiles_per_img;  // tiles of BN pixels per image
@@ -1416,40 +1420,36 @@ void dcn2_bwd_fused_kernel(const BwdParams p) {
     const ChunkEnt ce = ((const ChunkEnt *)p.tab)[c];
     const int plane = ce.x;  // offset / mask plane g*KK + tap
 
-    // W'^T fragments of K block kb of chunk c (pack_weight_kernel layout 1:
-    // fragment (row block 2c + kb, step s) is one contiguous run of 64 lanes
-    // x 8 elements).
+    // W'^T fragments of K block kb, M half mh of chunk c (pack_weight_kernel
+    // layout 1: fragment (row block 2c + kb, step s) is one contiguous run of
+    // 64 lanes x 8 elements).
     frag wa[NMS];
     {
-        const T *wrow = (const T *)p.wt + (size_t)(c * (KC / 32) + kb) * NMS * 512 + lane * 8;
+        const T *wrow = (const T *)p.wt + ((size_t)(c * (KC / 32) + kb) * (2 * NMS) + mh * NMS) * 512 +
+                        lane * 8;
 #pragma unroll
         for (int s = 0; s < NMS; ++s) wa[s] = *reinterpret_cast<const frag *>(wrow + s * 512);
     }
 
-    // ---- loads of a tile into LDS buffer `buf` --------------------------------
-    // Sources of the wave's 64 gO rows (8 KiB): 8 loads of 1 KiB, load q to
-    // LDS byte go_lds(buf) + 1024 q.
+    // ---- gO stage --------------------------------------------------------
+    // The wave's 32 gO rows of tile t (4 KiB): load q (of 4) lands at LDS
+    // byte go_lds(buf) + 1024 q.  Rows past Cout and pixels past N read zeros.
     auto go_lds = [&](int buf) __attribute__((always_inline)) {
-        return lds_addr(&sG[buf][0]) + wave * 8192;
+        return lds_addr(&sG[buf][0]) + wave * 4096;
     };
-    auto go_sources = [&](int t, const void *(&srcs)[8]) __attribute__((always_inline)) {
+    auto go_src = [&](int t, int q) __attribute__((always_inline)) {
         const int b = t / tpi, n0 = (t - b * tpi) * BN;
         const T *go = (const T *)p.gout + (size_t)b * p.Cout * N;
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            const void *src;
-            if constexpr (GN) {
-                const int n = 16 * (q & 3) + (lane >> 2);
-                const int m = 32 * (2 * wave + (q >> 2)) + 8 * ((lane & 3) ^ fused_swz_cl(n));
-                src = n0 + n < N && m < p.Cout ? (const void *)(go + (size_t)(n0 + n) * p.Cout + m)
-                                               : (const void *)(dcn2_zero16 + lane * 16);
-            } else {
-                const int r = 64 * wave + 8 * q + (lane >> 3);
-                const int n = n0 + 8 * ((lane & 7) ^ fused_swz(r));
-                src = r < p.Cout && n < N ? (const void *)(go + (size_t)r * N + n)
-                                          : (const void *)(dcn2_zero16 + lane * 16);
-            }
-            srcs[q] = src;
+        if constexpr (GN) {  // block `wave`, pixel lines 16q + l/4, 4 pieces of 8 rows
+            const int n = 16 * q + (lane >> 2);
+            const int m = 32 * wave + 8 * ((lane & 3) ^ fused_swz_cl(n));
+            return n0 + n < N && m < p.Cout ? (const void *)(go + (size_t)(n0 + n) * p.Cout + m)
+                                            : (const void *)(dcn2_zero16 + lane * 16);
+        } else {  // rows 32 wave + 8q + l/8, 8 pieces of 8 pixels
+            const int r = 32 * wave + 8 * q + (lane >> 3);
+            const int n = n0 + 8 * ((lane & 7) ^ fused_swz(r));
+            return r < p.Cout && n < N ? (const void *)(go + (size_t)r * N + n)
+                                       : (const void *)(dcn2_zero16 + lane * 16);
         }
     };
     // NCHW: element (row r, pixel x); channels-last: element (pixel n, row m);
@@ -1481,9 +1481,9 @@ void dcn2_bwd_fused_kernel(const BwdParams p) {
                     l0 + 8 * (g >> 1) + 4 * hh + (li >> 2), x0 + 16 * (g & 1) + 4 * (li & 3)));
         return __builtin_bit_cast(frag, __builtin_shufflevector(h[0], h[1], 0, 1, 2, 3, 4, 5, 6, 7));
     };
-    // Column-gradient B fragment of step s: gO rows 16s + 8*(l/32) .., pixel
-    // 32P + l%32.  grad_weight A fragment of row block j, step ks: row
-    // 64 wave + 32 j + l%32, pixels 16 ks + 8*(l/32) ...
+    // Column-gradient B fragment of M step s (0..15): gO rows 16s + 8*(l/32)
+    // .., pixel 32P + l%32.  grad_weight A fragment of step ks: row
+    // 32 wave + l%32, pixels 16 ks + 8*(l/32) ...
     auto go_bfrag = [&](int buf, int s) __attribute__((always_inline)) {
         if constexpr (GN) {
             return *reinterpret_cast<const frag *>(
@@ -1492,158 +1492,155 @@ void dcn2_bwd_fused_kernel(const BwdParams p) {
             return tr_frag([&](int r, int x) { return at_rm(buf, r, x); }, s * KSTEP, P * 32);
         }
     };
-    auto go_afrag = [&](int buf, int j, int ks) __attribute__((always_inline)) {
+    auto go_afrag = [&](int buf, int ks) __attribute__((always_inline)) {
         if constexpr (GN) {
-            return tr_frag([&](int n, int m) { return at_nm(buf, n, m); }, ks * KSTEP,
-                           wave * 64 + j * 32);
+            return tr_frag([&](int n, int m) { return at_nm(buf, n, m); }, ks * KSTEP, wave * 32);
         } else {
             return *reinterpret_cast<const frag *>(
-                at_rm(buf, wave * 64 + j * 32 + (lane & 31), ks * KSTEP + 8 * (lane >> 5)));
+                at_rm(buf, wave * 32 + (lane & 31), ks * KSTEP + 8 * (lane >> 5)));
         }
     };
 
-    // ---- sampling (one lane per pixel: pixel 32P + lane%32 of the tile) ------
-    const int pl = lane & 31;
+    // ---- sampling: wave kSampler, one lane per pixel of the tile ------------
+    // Offsets, mask and bucket row of a tile's pixel `lane`, loaded a tile
+    // before they are used and kept raw (no instruction reads them until
+    // then, so their load is never waited for early).
+    constexpr int kSampler = 1, kFinisher = 0;
     struct OM {
         T dy, dx, m;
         int sx;
     };
     auto load_om = [&](int t, OM &o) __attribute__((always_inline)) {
         const int b = t / tpi;
-        const int nr = (t - b * tpi) * BN + P * 32 + pl;
+        const int nr = (t - b * tpi) * BN + lane;
         const int nn = nr < N ? nr : 0;
         const T *offs = (const T *)p.offset + (size_t)b * p.off_bs + (size_t)plane * 2 * N;
         // (without a mask the load re-reads the offset: no load in a branch)
         const T *mk = p.mask ? (const T *)p.mask + (size_t)b * p.msk_bs + (size_t)plane * N : offs;
         o.dy = offs[nn];
         o.dx = offs[N + nn];
-        const T mraw = mk[nn];
-        o.m = p.mask ? mraw : (T)1.0f;
+        o.m = mk[nn];
         o.sx = p.sidx[((size_t)b * p.G * KK + plane) * N + nn];
     };
-    // Descriptors of tile t's pixel into sD[buf][wave][pl] (corner weights;
-    // mask value, bucket row, fractions; corner validity) and the sources of
-    // the corner gathers of the wave's pixels: load j = 2q + i brings corner q
-    // of pixels 16i + l/4, 16 bytes (8 channels) per lane, to LDS byte
-    // gather_lds(buf) + 1024 j.
-    auto gather_lds = [&](int buf) __attribute__((always_inline)) {
-        return lds_addr(&sK[buf][wave][0][0]);
-    };
-    auto sample = [&](int t, const OM &o, int buf, const void *(&srcs)[8]) __attribute__((always_inline)) {
-        const int b = t / tpi;
-        const int nr = (t - b * tpi) * BN + P * 32 + pl;
-        const bool live = nr < N;
-        int oy = 0, ox = 0;
-        if (live) {
-            oy = nr / p.Wo;
-            ox = nr - oy * p.Wo;
+    // Output row and column of the sampler lane's pixel in tile t, kept
+    // incrementally (tiles of one workgroup are consecutive): sample() is
+    // called for t_begin, t_begin + 1, ... in order.
+    int s_t = -2, s_oy = 0, s_ox = 0;  // (s_t: the tile last sampled; none yet)
+    auto advance_pixel = [&](int t) __attribute__((always_inline)) {
+        const int n0 = (t % tpi) * BN;
+        if (t != s_t + 1 || n0 == 0) {  // first tile, or a new image
+            const int nr = n0 + lane;
+            s_oy = nr / p.Wo;
+            s_ox = nr - s_oy * p.Wo;
+        } else {
+            s_ox += BN;
+            while (s_ox >= p.Wo) {
+                s_ox -= p.Wo;
+                ++s_oy;
+            }
         }
-        const float y = (float)(oy * p.sh - p.ph + ce.y) + to_f32(o.dy);
-        const float x = (float)(ox * p.sw - p.pw + ce.z) + to_f32(o.dx);
-        const float mv = live ? mask_value(to_f32(o.m), p.msk_logit) : 0.0f;
+        s_t = t;
+    };
+    // Descriptors of tile t's pixel `lane` into sD[buf][lane] (corner
+    // weights; mask value, bucket row, fractions; corner element offsets) and
+    // sV[buf][lane] (corner validity).
+    auto sample = [&](int t, const OM &o, int buf) __attribute__((always_inline)) {
+        advance_pixel(t);
+        const int nr = (t % tpi) * BN + lane;
+        const bool live = nr < N;
+        const float y = (float)(s_oy * p.sh - p.ph + ce.y) + to_f32(o.dy);
+        const float x = (float)(s_ox * p.sw - p.pw + ce.z) + to_f32(o.dx);
+        float mv = p.mask ? to_f32(o.m) : 1.0f;
+        if (p.msk_logit) mv = mask_value(mv, 1);
+        mv = live ? mv : 0.0f;
         const SamplePos spos = sample_pos(live ? y : -2.0f, live ? x : -2.0f, p.H, p.W);
         const Corners cr = make_corners(spos, mv, p.W, cs);
-        const int valid = (spos.vy0 && spos.vx0 ? 1 : 0) | (spos.vy0 && spos.vx1 ? 2 : 0) |
-                          (spos.vy1 && spos.vx0 ? 4 : 0) | (spos.vy1 && spos.vx1 ? 8 : 0);
-        if (lane < 32) {
-            sD[buf][wave][pl][0] = f32x4{cr.w[0], cr.w[1], cr.w[2], cr.w[3]};
-            sD[buf][wave][pl][1] = f32x4{mv, __int_as_float(live ? o.sx : -1), spos.ly, spos.lx};
-            sD[buf][wave][pl][2] = f32x4{__int_as_float(valid), 0.0f, 0.0f, 0.0f};
-        }
-        const T *xb = (const T *)p.xt + (size_t)b * p.H * p.W * cs + ce.w + kb * 32 + (lane & 3) * E;
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-                srcs[2 * q + i] = xb + __shfl(cr.off[q], 16 * i + (lane >> 2), 64);
+        sD[buf][lane][0] = f32x4{cr.w[0], cr.w[1], cr.w[2], cr.w[3]};
+        sD[buf][lane][1] = f32x4{mv, __int_as_float(live ? o.sx : -1), spos.ly, spos.lx};
+        sD[buf][lane][2] = f32x4{__int_as_float(cr.off[0]), __int_as_float(cr.off[1]),
+                                 __int_as_float(cr.off[2]), __int_as_float(cr.off[3])};
+        sV[buf][lane] = (spos.vy0 && spos.vx0 ? 1 : 0) | (spos.vy0 && spos.vx1 ? 2 : 0) |
+                        (spos.vy1 && spos.vx0 ? 4 : 0) | (spos.vy1 && spos.vx1 ? 8 : 0);
     };
+    // Corner gathers of the wave's pixels px0 .. px0+15: load q brings corner
+    // q, lanes 4i..4i+3 the 64 bytes (32 channels of K block kb) of pixel
+    // px0 + i; the corner offsets come from the descriptors in sD[buf].
+    auto gather_offsets = [&](int buf) __attribute__((always_inline)) {
+        return sD[buf][px0 + (lane >> 2)][2];
+    };
+    auto gather_src = [&](int t, int q, const f32x4 &goff) __attribute__((always_inline)) {
+        const int b = t / tpi;
+        return (const void *)((const T *)p.xt + (size_t)b * p.H * p.W * cs + ce.w + kb * 32 +
+                              (lane & 3) * E + __float_as_int(goff[q]));
+    };
+    const unsigned k_lds = lds_addr(&sK[wave][0][0]);
 
     // this lane's kFusedTrashLane bytes of dcn2_trash
     constexpr int kTrashWaves = kTrashBytes / (64 * kFusedTrashLane);
     uint4 *const trash_v = reinterpret_cast<uint4 *>(dcn2_trash) +
-                           ((blockIdx.x * 4 + wave) % kTrashWaves) * (64 * kFusedTrashLane / 16) +
+                           ((blockIdx.x * 8 + wave) % kTrashWaves) * (64 * kFusedTrashLane / 16) +
                            lane * (kFusedTrashLane / 16);
     T *const trash_t = reinterpret_cast<T *>(trash_v);
 
-    // ---- phase A --------------------------------------------------------------
-    // Column gradient of K block kb, pixels 32P .. 32P+31 of the tile.
-    // after(s) runs after the MFMA of step s (it issues the next tile's loads,
-    // spread over the MFMAs).  The fragments are read two steps ahead of their
-    // MFMA; each step ends in a scheduling barrier, which keeps that order and
-    // the loads where they are.
-    auto colgrad_mfma = [&](int buf, auto after) __attribute__((always_inline)) {
+    // ---- phase A: column gradient ---------------------------------------------
+    // Partial cg of block (kb, P) over the wave's M half -> sX[mh][blk].
+    // after(s) runs after MFMA s (it issues the next tile's gO loads).  The
+    // fragments are read two steps ahead; each step ends in a scheduling
+    // barrier, which keeps that order and the loads where they are.
+    auto colgrad = [&](int buf, auto after) __attribute__((always_inline)) {
         f32x16 acc;
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
         frag bf[NMS];
-        bf[0] = go_bfrag(buf, 0);
-        bf[1] = go_bfrag(buf, 1);
+        bf[0] = go_bfrag(buf, mh * NMS);
+        bf[1] = go_bfrag(buf, mh * NMS + 1);
 #pragma unroll
         for (int s = 0; s < NMS; ++s) {
-            if (s + 2 < NMS) bf[s + 2] = go_bfrag(buf, s + 2);
+            if (s + 2 < NMS) bf[s + 2] = go_bfrag(buf, mh * NMS + s + 2);
             acc = M::mma(wa[s], bf[s], acc);
             after(s);
             __builtin_amdgcn_sched_barrier(0);
         }
-        return acc;
-    };
-    // Lane (pixel pair pq = l/4: pixels pq, pq+16 of the wave; channels
-    // 32kb + 8(l%4) ..): corner sums, hand-off and blend.
-    const int pq = lane >> 2, cq = lane & 3;
-    auto consume = [&](int buf, int t, const f32x16 &acc) __attribute__((always_inline)) {
-        uint4 raw[4][2];
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-#pragma unroll
-            for (int i = 0; i < 2; ++i) raw[q][i] = sK[buf][wave][q * 2 + i][lane];
-        f32x4 d0[2], d1[2];
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            d0[i] = sD[buf][wave][pq + 16 * i][0];
-            d1[i] = sD[buf][wave][pq + 16 * i][1];
-        }
-        // cg through the wave's area (it reuses the gather bytes just read;
-        // a wave's LDS operations are done in order)
-        float *const sX = reinterpret_cast<float *>(&sK[buf][wave][0][0]);
-        __builtin_amdgcn_wave_barrier();
         // acc[r] = cg[32kb + 8(r/4) + 4(l/32) + r%4][32P + l%32]
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-            *reinterpret_cast<f32x4 *>(&sX[(lane & 31) * LDX + 8 * j + 4 * (lane >> 5)]) =
+            *reinterpret_cast<f32x4 *>(&sX[mh][blk][lane & 31][8 * j + 4 * (lane >> 5)]) =
                 f32x4{acc[4 * j], acc[4 * j + 1], acc[4 * j + 2], acc[4 * j + 3]};
-        __builtin_amdgcn_wave_barrier();
-        float cgv[2][E];
+    };
+    // Lane (pixel px0 + l/4, channels 32kb + 8(l%4) ..): corner sums, hand-off
+    // and blend.  raw: the lane's corner gathers (read before the barrier).
+    const int pq = lane >> 2, cq = lane & 3;
+    auto consume = [&](int buf, const uint4 (&raw)[4]) __attribute__((always_inline)) {
+        const int px = px0 + pq;
+        const f32x4 d0 = sD[buf][px][0], d1 = sD[buf][px][1];
+        float cgv[E];
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int h = 0; h < 2; ++h) {
+            const f32x4 v = *reinterpret_cast<const f32x4 *>(&sX[0][blk][16 * mh + pq][cq * E + 4 * h]) +
+                            *reinterpret_cast<const f32x4 *>(&sX[1][blk][16 * mh + pq][cq * E + 4 * h]);
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const f32x4 v = *reinterpret_cast<const f32x4 *>(&sX[(pq + 16 * i) * LDX + cq * E + 4 * h]);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) cgv[i][4 * h + e] = v[e];
-            }
+            for (int e = 0; e < 4; ++e) cgv[4 * h + e] = v[e];
+        }
         // corner sums over the lane's 8 channels, then over the 4 lanes of the pixel
-        f32x4 S[2];
+        f32x4 S;
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int q = 0; q < 4; ++q) {
+            float v[E];
+            Unpack<T>::run(raw[q], v);
+            float s = 0.0f;
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                float v[E];
-                Unpack<T>::run(raw[q][i], v);
-                float s = 0.0f;
-#pragma unroll
-                for (int e = 0; e < E; ++e) s = fmaf(cgv[i][e], v[e], s);
-                s += quad_xor1(s);
-                s += quad_xor2(s);
-                S[i][q] = s;
-            }
-        if (cq < 2) sS[kb][P * 32 + pq + 16 * cq] = cq ? S[1] : S[0];
-        // masked column-gradient rows
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int srow = __float_as_int(d1[i][1]);
+            for (int e = 0; e < E; ++e) s = fmaf(cgv[e], v[e], s);
+            s += quad_xor1(s);
+            s += quad_xor2(s);
+            S[q] = s;
+        }
+        if (cq == 0) sS[kb][px] = S;
+        // masked column-gradient row
+        {
+            const int srow = __float_as_int(d1[1]);
             float mrow[E];
 #pragma unroll
-            for (int e = 0; e < E; ++e) mrow[e] = cgv[i][e] * d1[i][0];
+            for (int e = 0; e < E; ++e) mrow[e] = cgv[e] * d1[0];
             uint4 *row = srow >= 0
                              ? reinterpret_cast<uint4 *>((R *)p.cgm + (size_t)srow * KC + kb * 32 + cq * E)
                              : trash_v;
@@ -1651,59 +1648,51 @@ void dcn2_bwd_fused_kernel(const BwdParams p) {
             for (int u = 0; u < NST; ++u) row[u] = pack16<R>(mrow + u * (16 / sizeof(R)));
         }
         // blended columns
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        {
             float col[E], v[E];
 #pragma unroll
             for (int e = 0; e < E; ++e) col[e] = 0.0f;
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                Unpack<T>::run(raw[q][i], v);
+                Unpack<T>::run(raw[q], v);
 #pragma unroll
-                for (int e = 0; e < E; ++e) col[e] = fmaf(d0[i][q], v[e], col[e]);
+                for (int e = 0; e < E; ++e) col[e] = fmaf(d0[q], v[e], col[e]);
             }
-            *reinterpret_cast<uint4 *>(at_c(P * 32 + pq + 16 * i, kb * 32 + cq * E)) = pack16<T>(col);
+            *reinterpret_cast<uint4 *>(at_c(px, kb * 32 + cq * E)) = pack16<T>(col);
         }
     };
 
-    // ---- phase B --------------------------------------------------------------
-    // grad_mask / grad_offset of pixel 32P + l%32 from both K blocks' corner
-    // sums: one store per lane (kb 0: grad_off_y, grad_off_x; kb 1:
-    // grad_mask, none; a pixel past N stores to dcn2_trash).
+    // ---- phase B ----------------------------------------------------------------
+    // grad_mask / grad_offset of pixel `lane` of tile t from both K blocks'
+    // corner sums (wave kFinisher; pixels past N store to dcn2_trash).
     auto finish_sums = [&](int buf, int t) __attribute__((always_inline)) {
         const int b = t / tpi;
-        const int nr = (t - b * tpi) * BN + P * 32 + pl;
-        const f32x4 S = sS[0][P * 32 + pl] + sS[1][P * 32 + pl];
-        const f32x4 d1 = sD[buf][wave][pl][1];
-        const int valid = __float_as_int(sD[buf][wave][pl][2][0]);
+        const int nr = (t - b * tpi) * BN + lane;
+        const f32x4 S = sS[0][lane] + sS[1][lane];
+        const f32x4 d1 = sD[buf][lane][1];
+        const int valid = sV[buf][lane];
         const float mv = d1[0], fly = d1[2], flx = d1[3];
         const float S0 = (valid & 1) ? S[0] : 0.0f, S1 = (valid & 2) ? S[1] : 0.0f;
         const float S2 = (valid & 4) ? S[2] : 0.0f, S3 = (valid & 8) ? S[3] : 0.0f;
         const float hy = 1.0f - fly, hx = 1.0f - flx;
-        float v;
-        T *dst = trash_t;
-        const bool hi = lane >= 32;
-        if (kb == 0) {
-            v = hi ? mv * (hy * (S1 - S0) + fly * (S3 - S2))   // grad_off_x
-                   : mv * (hx * (S2 - S0) + flx * (S3 - S1));  // grad_off_y
-            if (nr < N) dst = (T *)p.goff + (size_t)b * p.off_bs + (size_t)plane * 2 * N + (hi ? N : 0) + nr;
-        } else {
-            const float gmr = hy * hx * S0 + hy * flx * S1 + fly * hx * S2 + fly * flx * S3;
-            // d/d(logit) of sigmoid = s (1 - s), s = the mask value used
-            v = p.msk_logit ? gmr * mv * (1.0f - mv) : gmr;
-            if (nr < N && !hi && p.gmask)
-                dst = (T *)p.gmask + (size_t)b * p.msk_bs + (size_t)plane * N + nr;
-        }
-        *dst = from_f32<T>(v);
+        const float goy = mv * (hx * (S2 - S0) + flx * (S3 - S1));
+        const float gox = mv * (hy * (S1 - S0) + fly * (S3 - S2));
+        const float gmr = hy * hx * S0 + hy * flx * S1 + fly * hx * S2 + fly * flx * S3;
+        // d/d(logit) of sigmoid = s (1 - s), s = the mask value used
+        const float gm = p.msk_logit ? gmr * mv * (1.0f - mv) : gmr;
+        const bool live = nr < N;
+        T *go = (T *)p.goff + (size_t)b * p.off_bs + (size_t)plane * 2 * N + nr;
+        *(live ? go : trash_t) = from_f32<T>(goy);
+        *(live ? go + N : trash_t + 1) = from_f32<T>(gox);
+        T *gmp = p.gmask ? (T *)p.gmask + (size_t)b * p.msk_bs + (size_t)plane * N + nr : trash_t + 2;
+        *(live ? gmp : trash_t + 2) = from_f32<T>(gm);
     };
-    f32x16 gacc[2][2];  // [gO row block j][K block i]
+    f32x16 gacc[2];  // gW rows 32 wave .., K blocks 0 and 1
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) gacc[j][i][r] = 0.0f;
-    float bsum[2] = {0.0f, 0.0f};
+        for (int r = 0; r < 16; ++r) gacc[i][r] = 0.0f;
+    float bsum = 0.0f;
     const bool do_bias = p.gb_acc != nullptr && c == 0;
     // acc + the sum of a fragment's 8 values (four 2-element dot products
     // with (1, 1), accumulated in fp32)
@@ -1720,12 +1709,12 @@ void dcn2_bwd_fused_kernel(const BwdParams p) {
         }
         return acc;
     };
-    // (grad_bias: compile-time switch, so no branch sits between the MFMAs)
-    auto gradw_mfma = [&](int buf, auto bias_c, auto after) __attribute__((always_inline)) {
-        frag a[NKS][2], bf[NKS][2];
+    // (grad_bias: compile-time switch, so no branch sits between the MFMAs;
+    // after(s) runs after MFMA s = 2 ks + i)
+    auto gradw = [&](int buf, auto bias_c, auto after) __attribute__((always_inline)) {
+        frag a[NKS], bf[NKS][2];
         auto rd = [&](int ks) __attribute__((always_inline)) {
-#pragma unroll
-            for (int j = 0; j < 2; ++j) a[ks][j] = go_afrag(buf, j, ks);
+            a[ks] = go_afrag(buf, ks);
 #pragma unroll
             for (int i = 0; i < 2; ++i) bf[ks][i] = tr_frag(at_c, ks * KSTEP, i * 32);
         };
@@ -1734,77 +1723,81 @@ void dcn2_bwd_fused_kernel(const BwdParams p) {
         for (int ks = 0; ks < NKS; ++ks) {
             if (ks + 1 < NKS) rd(ks + 1);
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
-#pragma unroll
-                for (int i = 0; i < 2; ++i) {
-                    gacc[j][i] = M::mma(a[ks][j], bf[ks][i], gacc[j][i]);
-                    after(4 * ks + 2 * j + i);
-                }
-            if constexpr (decltype(bias_c)::value) {
-#pragma unroll
-                for (int j = 0; j < 2; ++j) bsum[j] = sum8(a[ks][j], bsum[j]);
+            for (int i = 0; i < 2; ++i) {
+                gacc[i] = M::mma(a[ks], bf[ks][i], gacc[i]);
+                after(2 * ks + i);
             }
+            if constexpr (decltype(bias_c)::value) bsum = sum8(a[ks], bsum);
             __builtin_amdgcn_sched_barrier(0);
         }
     };
 
     // ---- the tiles ----------------------------------------------------------------
+    // gO: double-buffered, the next tile's rows loaded during the column
+    // gradient; corner gathers: one buffer per wave, the next tile's issued
+    // during grad_weight (after the tile's own were read).  Everything a tile
+    // loads is waited for once, before its last barrier.
     auto tiles = [&](auto bias_c) __attribute__((always_inline)) {
-        OM om;
-        const void *gsrc[8], *ksrc[8];
-        load_om(t_begin, om);
-        go_sources(t_begin, gsrc);
-        sample(t_begin, om, 0, ksrc);
+        OM om, om2;  // offsets of the tile sampled next, and of the one after
+        if (wave == kSampler) {
+            load_om(t_begin, om);
+            sample(t_begin, om, 0);
+            load_om(min(t_begin + 1, t_last), om);
+        }
+        __syncthreads();  // descriptors of the first tile
+        {
+            const f32x4 goff = gather_offsets(0);
 #pragma unroll
-        for (int q = 0; q < 8; ++q) dma16(gsrc[q], go_lds(0) + q * 1024);
+            for (int q = 0; q < 4; ++q) dma16(go_src(t_begin, q), go_lds(0) + q * 1024);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) dma16(ksrc[j], gather_lds(0) + j * 1024);
-        load_om(min(t_begin + 1, t_last), om);
+            for (int q = 0; q < 4; ++q) dma16(gather_src(t_begin, q, goff), k_lds + q * 1024);
+        }
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the stage loads
         __syncthreads();
         for (int t = t_begin; t < t_end; ++t) {
             const int buf = (t - t_begin) & 1;
             const int tn = min(t + 1, t_last);
-            // the next tile's loads: gO rows during the column-gradient MFMAs,
-            // corner gathers during the grad_weight MFMAs
-            go_sources(tn, gsrc);
-            sample(tn, om, buf ^ 1, ksrc);
-            load_om(min(t + 2, t_last), om);
-            const unsigned gl = go_lds(buf ^ 1), kl = gather_lds(buf ^ 1);
-            consume(buf, t, colgrad_mfma(buf, [&](int s) __attribute__((always_inline)) {
-                        if (s & 1) dma16(gsrc[s >> 1], gl + (s >> 1) * 1024);
-                    }));
-            __syncthreads();
-            finish_sums(buf, t);
-            gradw_mfma(buf, bias_c, [&](int s) __attribute__((always_inline)) {
-                if (s & 1) dma16(ksrc[s >> 1], kl + (s >> 1) * 1024);
+            const unsigned gl = go_lds(buf ^ 1);
+            if (wave == kSampler) load_om(min(t + 2, t_last), om2);
+            colgrad(buf, [&](int s) __attribute__((always_inline)) {
+                if (s & 1) dma16(go_src(tn, s >> 1), gl + (s >> 1) * 1024);
             });
-            __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the next tile's stage loads
+            uint4 raw[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) raw[q] = sK[wave][q][lane];
+            if (wave == kSampler) {  // the next tile's descriptors (its offsets were loaded a tile ago)
+                sample(tn, om, buf ^ 1);
+                om = om2;
+            }
+            __syncthreads();  // cg partials of both M halves; the next tile's descriptors
+            consume(buf, raw);
+            __syncthreads();  // sums, columns; the gather buffers are free
+            if (wave == kFinisher) finish_sums(buf, t);
+            const f32x4 goff = gather_offsets(buf ^ 1);
+            gradw(buf, bias_c, [&](int s) __attribute__((always_inline)) {
+                if (s & 1) dma16(gather_src(tn, s >> 1, goff), k_lds + (s >> 1) * 1024);
+            });
+            __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the next tile's loads
             __syncthreads();
         }
     };
     if (do_bias) tiles(std::true_type{});
     else tiles(std::false_type{});
 
-    // grad_weight block of this workgroup: rows 64*wave .., columns c*KC ..
+    // grad_weight block of this workgroup: rows 32 wave .., columns c*KC ..
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int i = 0; i < 2; ++i) {
+        const int k = c * KC + i * 32 + (lane & 31);
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int k = c * KC + i * 32 + (lane & 31);
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int m = wave * 64 + j * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (m < p.Cout) unsafeAtomicAdd(p.gw_acc + (size_t)m * p.Kp + k, gacc[j][i][r]);
-            }
+        for (int r = 0; r < 16; ++r) {
+            const int m = wave * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            if (m < p.Cout) unsafeAtomicAdd(p.gw_acc + (size_t)m * p.Kp + k, gacc[i][r]);
         }
+    }
     if (do_bias) {
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const float v = bsum[j] + shfl_xor_f(bsum[j], 32);
-            const int m = wave * 64 + j * 32 + (lane & 31);
-            if (lane < 32 && m < p.Cout) unsafeAtomicAdd(p.gb_acc + m, v);
-        }
+        const float v = bsum + shfl_xor_f(bsum, 32);
+        const int m = wave * 32 + (lane & 31);
+        if (lane < 32 && m < p.Cout) unsafeAtomicAdd(p.gb_acc + m, v);
     }
 }
 
@@ -2286,8 +2279,8 @@ static hipError_t backward_t(const Geo &g, const BwdParams &p0, void *grad_input
                     pf.tiles_per_img = ceil_div(g.N, 64);
                     pf.splits = std::max(1, std::min(ncu / nch, g.B * pf.tiles_per_img));
                     const int grid = pf.splits * nch;
-                    if (p.go_nhwc) dcn2_bwd_fused_kernel<T, true><<<grid, 256, 0, s>>>(pf);
-                    else dcn2_bwd_fused_kernel<T, false><<<grid, 256, 0, s>>>(pf);
+                    if (p.go_nhwc) dcn2_bwd_fused_kernel<T, true><<<grid, 512, 0, s>>>(pf);
+                    else dcn2_bwd_fused_kernel<T, false><<<grid, 512, 0, s>>>(pf);
                     if ((e = hipGetLastError()) != hipSuccess) return e;
                 }
             }
