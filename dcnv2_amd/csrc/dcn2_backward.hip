@@ -1341,24 +1341,24 @@ __device__ __forceinline__ int fused_swz_c(int n) { return ((n & 3) << 1) | ((n 
 
 // Trash bytes each lane of the fused kernel may write (its widest hand-off row).
 constexpr int kFusedTrashLane = 32;
-// Zero bytes for the stage loads of gO rows past Cout or pixels past N.
-__device__ __attribute__((aligned(16))) const unsigned char dcn2_zero16[16 * 64] = {};
 
-// Global -> LDS copy of 16 bytes per lane: lane i's 16 bytes from `src` land
-// at LDS byte lds + 16*i (lds is wave-uniform).  Written as inline assembly so
-// that the compiler does not make later LDS reads wait for it (it cannot tell
-// which LDS bytes it writes); the kernel waits for it explicitly
-// (s_waitcnt vmcnt(0)) before the barrier after which the bytes are read, and
-// the bytes it overwrites were last read before the previous barrier.  (A
-// volatile asm statement stays between the barriers around it; without a
-// memory clobber, LDS reads of the other buffer may be scheduled across it.)
-// M0 holds the LDS base and is set right before the load.
+// Buffer -> LDS copy of 16 bytes per lane: lane i's 16 bytes at byte offset
+// `off` of the buffer resource land at LDS byte lds + 16*i (lds is
+// wave-uniform; an offset at or past the resource's size reads zeros).
+// Written as inline assembly so that the compiler does not make later LDS
+// reads wait for it (it cannot tell which LDS bytes it writes); the kernel
+// waits for it explicitly (s_waitcnt vmcnt(0)) before the barrier after which
+// the bytes are read, and the bytes it overwrites were last read before the
+// previous barrier.  (A volatile asm statement stays between the barriers
+// around it; without a memory clobber, LDS reads of the other buffer may be
+// scheduled across it.)  M0 holds the LDS base and is set right before the
+// load.
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void dma16(const void *src, unsigned lds) {
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rs, int off, unsigned lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %2, 0 offen lds"
                  :
-                 : "v"(src), "s"(lds)
+                 : "v"(off), "s"(lds), "s"(rs)
                  : "m0");
 }
 #pragma clang diagnostic pop
@@ -1437,20 +1437,45 @@ void dcn2_bwd_fused_kernel(const BwdParams p) {
     auto go_lds = [&](int buf) __attribute__((always_inline)) {
         return lds_addr(&sG[buf][0]) + wave * 4096;
     };
-    auto go_src = [&](int t, int q) __attribute__((always_inline)) {
-        const int b = t / tpi, n0 = (t - b * tpi) * BN;
-        const T *go = (const T *)p.gout + (size_t)b * p.Cout * N;
-        if constexpr (GN) {  // block `wave`, pixel lines 16q + l/4, 4 pieces of 8 rows
+    // Tile t = image b, pixels n0 .. n0 + BN - 1.
+    struct TileId {
+        int b, n0;
+    };
+    auto tile_id = [&](int t) __attribute__((always_inline)) {
+        const int b = t / tpi;
+        return TileId{b, (t - b * tpi) * BN};
+    };
+    const uint32_t go_bytes = (uint32_t)((size_t)p.Cout * N * sizeof(T));
+    auto go_rsrc = [&](const TileId &id) __attribute__((always_inline)) {
+        return __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<T *>((const T *)p.gout + (size_t)id.b * p.Cout * N), (short)0, (int)go_bytes,
+            0x00020000);
+    };
+    // Load q of the wave's rows: NCHW rows 32 wave + 8q + l/8, 8 pieces of 8
+    // pixels; channels-last block `wave`, pixel lines 16q + l/4, 4 pieces of 8
+    // rows.  The per-lane part of the byte offset (go_lo), the pixel of the
+    // piece within the tile (go_px) and whether its row exists (go_ok).
+    int go_lo[4], go_px[4];
+    bool go_ok[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        if constexpr (GN) {
             const int n = 16 * q + (lane >> 2);
             const int m = 32 * wave + 8 * ((lane & 3) ^ fused_swz_cl(n));
-            return n0 + n < N && m < p.Cout ? (const void *)(go + (size_t)(n0 + n) * p.Cout + m)
-                                            : (const void *)(dcn2_zero16 + lane * 16);
-        } else {  // rows 32 wave + 8q + l/8, 8 pieces of 8 pixels
+            go_lo[q] = (n * p.Cout + m) * (int)sizeof(T);
+            go_px[q] = n;
+            go_ok[q] = m < p.Cout;
+        } else {
             const int r = 32 * wave + 8 * q + (lane >> 3);
-            const int n = n0 + 8 * ((lane & 7) ^ fused_swz(r));
-            return r < p.Cout && n < N ? (const void *)(go + (size_t)r * N + n)
-                                       : (const void *)(dcn2_zero16 + lane * 16);
+            const int n = 8 * ((lane & 7) ^ fused_swz(r));
+            go_lo[q] = (r * N + n) * (int)sizeof(T);
+            go_px[q] = n;
+            go_ok[q] = r < p.Cout;
         }
+    }
+    auto go_off = [&](const TileId &id, int q) __attribute__((always_inline)) {
+        const int hi = (GN ? id.n0 * p.Cout : id.n0) * (int)sizeof(T);
+        return go_ok[q] && id.n0 + go_px[q] < N ? go_lo[q] + hi : kGoOutOfRange;
     };
     // NCHW: element (row r, pixel x); channels-last: element (pixel n, row m);
     // columns: element (pixel n, channel k)
@@ -1510,9 +1535,9 @@ void dcn2_bwd_fused_kernel(const BwdParams p) {
         T dy, dx, m;
         int sx;
     };
-    auto load_om = [&](int t, OM &o) __attribute__((always_inline)) {
-        const int b = t / tpi;
-        const int nr = (t - b * tpi) * BN + lane;
+    auto load_om = [&](const TileId &id, OM &o) __attribute__((always_inline)) {
+        const int b = id.b;
+        const int nr = id.n0 + lane;
         const int nn = nr < N ? nr : 0;
         const T *offs = (const T *)p.offset + (size_t)b * p.off_bs + (size_t)plane * 2 * N;
         // (without a mask the load re-reads the offset: no load in a branch)
@@ -1526,8 +1551,7 @@ void dcn2_bwd_fused_kernel(const BwdParams p) {
     // incrementally (tiles of one workgroup are consecutive): sample() is
     // called for t_begin, t_begin + 1, ... in order.
     int s_t = -2, s_oy = 0, s_ox = 0;  // (s_t: the tile last sampled; none yet)
-    auto advance_pixel = [&](int t) __attribute__((always_inline)) {
-        const int n0 = (t % tpi) * BN;
+    auto advance_pixel = [&](int t, int n0) __attribute__((always_inline)) {
         if (t != s_t + 1 || n0 == 0) {  // first tile, or a new image
             const int nr = n0 + lane;
             s_oy = nr / p.Wo;
@@ -1544,9 +1568,9 @@ void dcn2_bwd_fused_kernel(const BwdParams p) {
     // Descriptors of tile t's pixel `lane` into sD[buf][lane] (corner
     // weights; mask value, bucket row, fractions; corner element offsets) and
     // sV[buf][lane] (corner validity).
-    auto sample = [&](int t, const OM &o, int buf) __attribute__((always_inline)) {
-        advance_pixel(t);
-        const int nr = (t % tpi) * BN + lane;
+    auto sample = [&](int t, const TileId &id, const OM &o, int buf) __attribute__((always_inline)) {
+        advance_pixel(t, id.n0);
+        const int nr = id.n0 + lane;
         const bool live = nr < N;
         const float y = (float)(s_oy * p.sh - p.ph + ce.y) + to_f32(o.dy);
         const float x = (float)(s_ox * p.sw - p.pw + ce.z) + to_f32(o.dx);
@@ -1568,10 +1592,16 @@ void dcn2_bwd_fused_kernel(const BwdParams p) {
     auto gather_offsets = [&](int buf) __attribute__((always_inline)) {
         return sD[buf][px0 + (lane >> 2)][2];
     };
-    auto gather_src = [&](int t, int q, const f32x4 &goff) __attribute__((always_inline)) {
-        const int b = t / tpi;
-        return (const void *)((const T *)p.xt + (size_t)b * p.H * p.W * cs + ce.w + kb * 32 +
-                              (lane & 3) * E + __float_as_int(goff[q]));
+    // (one image of xt is below 2 GiB: 32-bit byte offsets)
+    const uint32_t xt_bytes = (uint32_t)((size_t)p.H * p.W * cs * sizeof(T));
+    auto xt_rsrc = [&](const TileId &id) __attribute__((always_inline)) {
+        return __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<T *>((const T *)p.xt + (size_t)id.b * p.H * p.W * cs), (short)0, (int)xt_bytes,
+            0x00020000);
+    };
+    const int gather_lane = (ce.w + kb * 32 + (lane & 3) * E) * (int)sizeof(T);
+    auto gather_off = [&](int q, const f32x4 &goff) __attribute__((always_inline)) {
+        return __float_as_int(goff[q]) * (int)sizeof(T) + gather_lane;
     };
     const unsigned k_lds = lds_addr(&sK[wave][0][0]);
 
@@ -1610,9 +1640,9 @@ void dcn2_bwd_fused_kernel(const BwdParams p) {
     // Lane (pixel px0 + l/4, channels 32kb + 8(l%4) ..): corner sums, hand-off
     // and blend.  raw: the lane's corner gathers (read before the barrier).
     const int pq = lane >> 2, cq = lane & 3;
-    auto consume = [&](int buf, const uint4 (&raw)[4]) __attribute__((always_inline)) {
+    auto consume = [&](int buf, int dbuf, const uint4 (&raw)[4]) __attribute__((always_inline)) {
         const int px = px0 + pq;
-        const f32x4 d0 = sD[buf][px][0], d1 = sD[buf][px][1];
+        const f32x4 d0 = sD[dbuf][px][0], d1 = sD[dbuf][px][1];
         float cgv[E];
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
@@ -1621,15 +1651,29 @@ void dcn2_bwd_fused_kernel(const BwdParams p) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) cgv[4 * h + e] = v[e];
         }
-        // corner sums over the lane's 8 channels, then over the 4 lanes of the pixel
+        // corner sums over the lane's 8 channels, then over the 4 lanes of the
+        // pixel.  f16: 2-element dot products (v_dot2_f32_f16) of the corner
+        // values with the column gradient rounded to f16, accumulated in fp32
+        // (the rounding is that of the f16 grad_offset / grad_mask outputs).
         f32x4 S;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            float v[E];
-            Unpack<T>::run(raw[q], v);
             float s = 0.0f;
+            if constexpr (std::is_same<T, f16>::value) {
+                typedef f16 h2 __attribute__((ext_vector_type(2)));
+                typedef float f2 __attribute__((ext_vector_type(2)));
+                const f16x8 x = __builtin_bit_cast(f16x8, raw[q]);
 #pragma unroll
-            for (int e = 0; e < E; ++e) s = fmaf(cgv[e], v[e], s);
+                for (int e = 0; e < E / 2; ++e) {
+                    const h2 cg2 = __builtin_convertvector(f2{cgv[2 * e], cgv[2 * e + 1]}, h2);
+                    s = __builtin_amdgcn_fdot2(cg2, h2{x[2 * e], x[2 * e + 1]}, s, false);
+                }
+            } else {
+                float v[E];
+                Unpack<T>::run(raw[q], v);
+#pragma unroll
+                for (int e = 0; e < E; ++e) s = fmaf(cgv[e], v[e], s);
+            }
             s += quad_xor1(s);
             s += quad_xor2(s);
             S[q] = s;
@@ -1665,9 +1709,9 @@ void dcn2_bwd_fused_kernel(const BwdParams p) {
     // ---- phase B ----------------------------------------------------------------
     // grad_mask / grad_offset of pixel `lane` of tile t from both K blocks'
     // corner sums (wave kFinisher; pixels past N store to dcn2_trash).
-    auto finish_sums = [&](int buf, int t) __attribute__((always_inline)) {
-        const int b = t / tpi;
-        const int nr = (t - b * tpi) * BN + lane;
+    auto finish_sums = [&](int buf, const TileId &id) __attribute__((always_inline)) {
+        const int b = id.b;
+        const int nr = id.n0 + lane;
         const f32x4 S = sS[0][lane] + sS[1][lane];
         const f32x4 d1 = sD[buf][lane][1];
         const int valid = sV[buf][lane];
@@ -1737,49 +1781,65 @@ void dcn2_bwd_fused_kernel(const BwdParams p) {
     // gradient; corner gathers: one buffer per wave, the next tile's issued
     // during grad_weight (after the tile's own were read).  Everything a tile
     // loads is waited for once, before its last barrier.
+    // Descriptors: two buffers, tile t's in sD[(t - t_begin) % 2]; the
+    // sampler writes tile t+1's in phase A of tile t, whose phase B issues
+    // tile t+1's gathers.  The sampler's offsets of tile t+1 are loaded at the
+    // top of tile t-1 into the register set of tile t+1's parity (the loop is
+    // unrolled by two), so the end-of-tile wait has covered them when they
+    // are used and no register copy or early wait is needed.
     auto tiles = [&](auto bias_c) __attribute__((always_inline)) {
-        OM om, om2;  // offsets of the tile sampled next, and of the one after
+        OM om[2];
+        const TileId id0 = tile_id(t_begin);
         if (wave == kSampler) {
-            load_om(t_begin, om);
-            sample(t_begin, om, 0);
-            load_om(min(t_begin + 1, t_last), om);
+            load_om(id0, om[0]);
+            sample(t_begin, id0, om[0], 0);
+            load_om(tile_id(min(t_begin + 1, t_last)), om[1]);
         }
         __syncthreads();  // descriptors of the first tile
         {
             const f32x4 goff = gather_offsets(0);
+            const __amdgpu_buffer_rsrc_t grs = go_rsrc(id0), xrs = xt_rsrc(id0);
 #pragma unroll
-            for (int q = 0; q < 4; ++q) dma16(go_src(t_begin, q), go_lds(0) + q * 1024);
+            for (int q = 0; q < 4; ++q) dma16(grs, go_off(id0, q), go_lds(0) + q * 1024);
 #pragma unroll
-            for (int q = 0; q < 4; ++q) dma16(gather_src(t_begin, q, goff), k_lds + q * 1024);
+            for (int q = 0; q < 4; ++q) dma16(xrs, gather_off(q, goff), k_lds + q * 1024);
         }
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the stage loads
         __syncthreads();
-        for (int t = t_begin; t < t_end; ++t) {
-            const int buf = (t - t_begin) & 1;
+        // tile t, buffer parity `buf` = (t - t_begin) % 2
+        auto step = [&](auto buf_c, int t) __attribute__((always_inline)) {
+            constexpr int buf = decltype(buf_c)::value;
             const int tn = min(t + 1, t_last);
+            const TileId it = tile_id(t), itn = tile_id(tn);
             const unsigned gl = go_lds(buf ^ 1);
-            if (wave == kSampler) load_om(min(t + 2, t_last), om2);
+            const __amdgpu_buffer_rsrc_t grs = go_rsrc(itn), xrs = xt_rsrc(itn);
+            if (wave == kSampler)  // tile t+2 has t's parity
+                load_om(tile_id(min(t + 2, t_last)), om[buf]);
             colgrad(buf, [&](int s) __attribute__((always_inline)) {
-                if (s & 1) dma16(go_src(tn, s >> 1), gl + (s >> 1) * 1024);
+                if (s & 1) dma16(grs, go_off(itn, s >> 1), gl + (s >> 1) * 1024);
             });
             uint4 raw[4];
 #pragma unroll
             for (int q = 0; q < 4; ++q) raw[q] = sK[wave][q][lane];
-            if (wave == kSampler) {  // the next tile's descriptors (its offsets were loaded a tile ago)
-                sample(tn, om, buf ^ 1);
-                om = om2;
-            }
-            __syncthreads();  // cg partials of both M halves; the next tile's descriptors
-            consume(buf, raw);
+            if (wave == kSampler) sample(tn, itn, om[buf ^ 1], buf ^ 1);
+            __syncthreads();  // cg partials of both M halves; tile t+1's descriptors
+            consume(buf, buf, raw);
             __syncthreads();  // sums, columns; the gather buffers are free
-            if (wave == kFinisher) finish_sums(buf, t);
+            if (wave == kFinisher) finish_sums(buf, it);
             const f32x4 goff = gather_offsets(buf ^ 1);
             gradw(buf, bias_c, [&](int s) __attribute__((always_inline)) {
-                if (s & 1) dma16(gather_src(tn, s >> 1, goff), k_lds + (s >> 1) * 1024);
+                if (s & 1) dma16(xrs, gather_off(s >> 1, goff), k_lds + (s >> 1) * 1024);
             });
             __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the next tile's loads
             __syncthreads();
+        };
+        // pairs of steps with no condition inside; an odd last tile is peeled
+        int t = t_begin;
+        for (; t + 1 < t_end; t += 2) {
+            step(std::integral_constant<int, 0>{}, t);
+            step(std::integral_constant<int, 1>{}, t + 1);
         }
+        if (t < t_end) step(std::integral_constant<int, 0>{}, t);
     };
     if (do_bias) tiles(std::true_type{});
     else tiles(std::false_type{});
@@ -2243,15 +2303,16 @@ static hipError_t backward_t(const Geo &g, const BwdParams &p0, void *grad_input
         ncu <= 0)
         ncu = 256;
     // The fused kernel (column gradient and grad_weight in one pass) serves
-    // 2-byte types with Mp == 256, one K chunk per deformable group and gO
-    // rows that take 16-byte loads.
+    // 2-byte types with Mp == 256, one K chunk per deformable group, gO rows
+    // that take 16-byte loads, and images of gO and xt below 2 GiB each.
     // DCN2_BWD_FUSED=0 in the environment selects the two-kernel path for
     // every shape (the tests compare both paths).
     bool fused = false;
     const char *fenv = std::getenv("DCN2_BWD_FUSED");
     if constexpr (sizeof(T) == 2)
         fused = !(fenv && fenv[0] == '0') && g.Mp == 256 && g.Cgp == g.KC && p.go_vec &&
-                (long long)g.Cout * g.N * (long long)sizeof(T) <= kGoOutOfRange;
+                (long long)g.Cout * g.N * (long long)sizeof(T) <= kGoOutOfRange &&
+                (long long)g.H * g.W * g.cs * (long long)sizeof(T) <= kGoOutOfRange;
     if (g.B > 0) {
         // 2. column gradient: grad_offset, grad_mask, grad_input accumulation
         //    (and grad_weight / grad_bias when fused)
