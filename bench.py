@@ -121,15 +121,21 @@ def _traffic():
 
 def _stage_report(w, stages):
     """Per-stage ms; for the MFMA stages also TFLOP/s and fraction of the dense
-    fp16/bf16 (fp32) peak on the algorithmic GEMM FLOPs of one pass."""
+    fp16/bf16 (fp32) peak on the algorithmic GEMM FLOPs of one pass.  When the
+    backward ran its fused kernel (no ``bwd_gradw`` launch), ``bwd_colgrad``
+    holds both backward GEMMs and is credited with twice the FLOPs."""
     import torch
     peak = PEAK_FP32_TFLOPS if w.dtype == torch.float32 else PEAK_FP16_TFLOPS
+    fused = "bwd_colgrad" in stages and "bwd_gradw" not in stages
     out = {}
     for k, ms in stages.items():
         e = {"ms": round(ms, 5)}
         if k in MFMA_STAGES:
-            tf = w.gemm_flops() / (ms * 1e-3) / 1e12
+            gemms = 2 if (fused and k == "bwd_colgrad") else 1
+            tf = gemms * w.gemm_flops() / (ms * 1e-3) / 1e12
             e.update(tflops=round(tf, 1), frac=round(tf / peak, 4))
+            if gemms == 2:
+                e["note"] = "fused kernel: column gradient and grad_weight / grad_bias"
         out[k] = e
     return out
 

@@ -338,7 +338,7 @@ def version() -> str:
 
 
 STAGES = ("fwd_pack", "fwd_main", "bwd_pack", "bwd_colgrad", "bwd_gradw", "bwd_gather",
-          "bwd_final")
+          "bwd_final", "bwd_bucket")
 
 
 def profile_enable(on: bool = True) -> None:

@@ -2316,7 +2316,7 @@ static hipError_t backward_t(const Geo &g, const BwdParams &p0, void *grad_input
     if (g.B > 0) {
         // 2. column gradient: grad_offset, grad_mask, grad_input accumulation
         //    (and grad_weight / grad_bias when fused)
-        prof_begin(DCN2_STAGE_BWD_COLGRAD, s);
+        prof_begin(DCN2_STAGE_BWD_BUCKET, s);
         {
             // buckets: count, scan, place (exact sizes, see dcn2_bucket_kernel)
             const int f32 = sizeof(T) == 4, isbf = std::is_same<T, bf16>::value;
@@ -2331,6 +2331,10 @@ static hipError_t backward_t(const Geo &g, const BwdParams &p0, void *grad_input
             if (tab) dcn2_bucket_kernel<true><<<bgrid, 256, 0, s>>>(p, p.offset, f32, isbf);
             else dcn2_bucket_global_kernel<true><<<bgrid, 256, 0, s>>>(p, p.offset, f32, isbf);
             if ((e = hipGetLastError()) != hipSuccess) return e;
+        }
+        prof_end(DCN2_STAGE_BWD_BUCKET, s);
+        prof_begin(DCN2_STAGE_BWD_COLGRAD, s);
+        {
             if constexpr (sizeof(T) == 2) {
                 if (fused) {
                     // one workgroup per CU: each K chunk gets CUs/nch ranges of

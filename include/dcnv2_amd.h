@@ -161,11 +161,15 @@ enum dcn2_stage {
     DCN2_STAGE_FWD_PACK = 0,     /* input / weight repacking of the forward      */
     DCN2_STAGE_FWD_MAIN = 1,     /* fused sampling + MFMA forward kernel          */
     DCN2_STAGE_BWD_PACK = 2,     /* repacking and accumulator clearing            */
-    DCN2_STAGE_BWD_COLGRAD = 3,  /* column gradient, grad_offset, grad_mask       */
+    DCN2_STAGE_BWD_COLGRAD = 3,  /* column gradient, grad_offset, grad_mask; with
+                                    the fused backward kernel also grad_weight /
+                                    grad_bias (DCN2_STAGE_BWD_GRADW then records
+                                    no launch)                                   */
     DCN2_STAGE_BWD_GRADW = 4,    /* grad_weight / grad_bias                        */
     DCN2_STAGE_BWD_GATHER = 5,   /* grad_input accumulation                       */
     DCN2_STAGE_BWD_FINAL = 6,    /* conversion to the caller's dtype and layout   */
-    DCN2_STAGE_COUNT = 7
+    DCN2_STAGE_BWD_BUCKET = 7,   /* grad_input bucket passes (count, scan, place) */
+    DCN2_STAGE_COUNT = 8
 };
 DCN2_API int dcn2_profile_enable(int on);
 DCN2_API int dcn2_profile_read(int stage, double *total_ms, int *launches);
