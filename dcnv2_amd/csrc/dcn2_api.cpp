@@ -356,6 +356,8 @@ int dcn2_backward_om(const dcn2_desc *d, const void *input, const void *weight, 
 
 const char *dcn2_last_error(void) { return g_last_error.c_str(); }
 
-const char *dcn2_version(void) { return "dcnv2_amd 2 gfx950"; }
+#define DCN2_STR_(x) #x
+#define DCN2_STR(x) DCN2_STR_(x)
+const char *dcn2_version(void) { return "dcnv2_amd " DCN2_STR(DCN2_ABI_VERSION) " gfx950"; }
 
 }  // extern "C"

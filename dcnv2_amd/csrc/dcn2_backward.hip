@@ -6,20 +6,23 @@
 // second im2col (com.cu:637-706) and two more cuBLAS calls for grad_weight and
 // grad_bias (com.cu:829-835).  Here the whole batch is one launch per stage:
 //
-//  colgrad kernel  (grid: pixel tiles x batch)
+//  bucket passes   each sample (image, offset plane, pixel) gets a row in the
+//                  bucket of the 16x16 cell tile its bilinear cell lies in
+//                  (count, scan, place; the rows are sized exactly)
+//  fused kernel    (2-byte types, 128 < Cout <= 256, one K chunk per group)
 //     cg[k][n] = sum_m Wt[k][m] * gO[m][n]            MFMA, kept on chip (LDS)
 //     grad_mask / grad_offset  via the corner sums    S_q = sum_c cg_c * x_c(corner q)
 //         grad_mask = sum_q w_q S_q,  grad_off_y = mask * sum_q dw_q/dy S_q, ...
-//       (4 FMAs per channel instead of re-evaluating bilinear and both
-//        coordinate weights per channel as com.cu:486-492 does)
-//     grad_input  scatter with fp32 atomics, lanes = channels so one wave
-//       instruction updates a contiguous channel run of one corner.
-//  gradw kernels   (grid: pixel-tile splits x K chunks x M chunks)
-//     gW[m][k] += sum_n gO[m][n] * col[k][n]           MFMA over re-sampled
-//       columns in LDS; partial tiles are added to an fp32 accumulator.
-//     grad_bias from the same gO fragments.  For 2-byte types gO is read in
-//     whole 128-byte lines and rearranged into MFMA fragments through LDS.
-//  finalize kernels: fp32 accumulators -> caller dtype and layout.
+//       (4 multiply-adds per channel instead of re-evaluating bilinear and
+//        both coordinate weights per channel as com.cu:486-492 does)
+//     the masked cg row of each sample -> its bucket row
+//     gW[m][k] += sum_n gO[m][n] * col[k][n]           MFMA over the columns
+//       blended from the same corner gathers; grad_bias from the same gO
+//  otherwise       dcn2_colgrad_kernel (all but grad_weight) and a grad_weight
+//                  kernel that re-samples the columns
+//  gather          grad_input pulled per pixel from the bucket rows of each
+//                  cell tile (no atomics), border rings merged afterwards
+//  finalize        fp32 accumulators -> caller dtype and layout.
 #include <algorithm>
 #include <cstddef>
 #include <cstdlib>
@@ -1296,45 +1299,49 @@ __global__ __launch_bounds__(512) void dcn2_gradw_line_kernel(const BwdParams p)
 // deformable group (Cgp == KC) and gO rows that take 16-byte loads; other
 // shapes run dcn2_colgrad_kernel and a grad_weight kernel.
 //
-// Grid: pixel-tile ranges x K chunks, one workgroup of 4 waves per CU (one
-// wave per SIMD, so each wave has the whole register file of its SIMD).  A
-// workgroup keeps one K chunk, i.e. one (tap, group): its W'^T fragments stay
-// in registers and its grad_weight block gW[256][64] is accumulated in
-// registers over all of its tiles, then added to the fp32 accumulator once.
-// Wave w = (K block kb = w%2, pixel half P = w/2) of a tile of BN = 64 pixels
-// of one image.  Per tile, with the tile's gO [256][64] and the corner
-// gathers of its samples already in LDS:
-//   top      the loads of the next tile are issued (straight into the other
-//            LDS buffers): each wave's 64 gO rows, and the corner gathers of
-//            its 32 pixels x 32 channels, whose addresses come from the
-//            sampling descriptors computed here (one lane per pixel);
-//   phase A  cg[k][n] = sum_m W'^T[k][m] gO[m][n] for the wave's K block and
-//            pixels (MFMA), handed to the lanes through a wave-local LDS area;
-//            lane (pixel pair, 8 channels): partial corner sums
-//            S_q = sum_c cg_c x_c(corner q) -> LDS, the masked cg row of the
-//            sample's grad_input bucket -> memory, the blended columns -> LDS;
-//   phase B  grad_mask / grad_offset from both K blocks' corner sums (as in
-//            dcn2_colgrad_kernel); gW[m][k] += sum_n gO[m][n] col[k][n] (MFMA;
-//            wave w: gO rows 64w.., both K blocks).
-// The loads of a tile are issued a whole tile ahead and waited for once, at
-// the end of the tile before its last barrier.  A gather lane group of 4
-// lanes reads 64 contiguous bytes of one corner, so an instruction touches
-// 16 cache lines.
+// Grid: pixel-tile ranges x K chunks, one workgroup of 8 waves per CU (two
+// per SIMD).  A workgroup keeps one K chunk, i.e. one (tap, group), and walks
+// consecutive tiles of BN = 64 pixels.  Its grad_weight block gW[256][64] is
+// accumulated in registers (rows 32w.. in wave w) over all of its tiles and
+// added to the fp32 accumulator once.  Wave w owns K block kb = w%2 (32
+// channels), pixel half P = (w/2)%2 and M half mh = w/4 of the column-gradient
+// GEMM, whose W'^T fragments stay in its registers.  Per tile, with the tile's
+// gO [256][64], its sampling descriptors and each wave's corner gathers
+// already in LDS:
+//   colgrad  partial cg[k][n] = sum over m in half mh of W'^T[k][m] gO[m][n]
+//            for (kb, P) on MFMA -> LDS; between the MFMAs the next tile's gO
+//            rows are loaded straight into the other LDS buffer.  The sampler
+//            wave then writes the next tile's descriptors, a lane per pixel.
+//   consume  lane (pixel px0 + l/4, 8 channels of K block kb) adds the two M
+//            halves' partials, then: corner sums S_q = sum_c cg_c x_c(corner q)
+//            over its channels, reduced over the pixel's 4 lanes -> LDS; the
+//            masked cg row -> the sample's grad_input bucket row; the blended
+//            column -> LDS.
+//   gradw    the finisher wave turns both K blocks' corner sums into
+//            grad_offset / grad_mask (a lane per pixel, as dcn2_colgrad_kernel
+//            does); every wave accumulates gW[m][k] += sum_n gO[m][n] col[k][n]
+//            on MFMA, and between the MFMAs the next tile's corner gathers are
+//            loaded straight into LDS.
+// Everything a tile loads is waited for once, before its last barrier; the
+// sampler's offsets are loaded two tiles ahead.  A gather lane group of 4
+// lanes reads 64 contiguous bytes of one corner, so an instruction touches 16
+// cache lines.
 //
 // LDS layouts (16-byte pieces XOR-permuted per line so that the transposing
 // 8-byte reads, the 16-byte reads and the 16-byte stores are free of bank
 // conflicts; a wave's 1 KiB load lands on consecutive LDS bytes, so each lane
 // loads the piece that belongs at its LDS slot):
 //   NCHW gO          [256 rows m][64 pixels], piece j of row r at
-//                    j ^ fused_swz(r); rows 64w.. are wave w's.
+//                    j ^ fused_swz(r); wave w loads rows 32w ...
 //   channels-last gO [8 row blocks][64 pixels][32 rows], piece j (rows
 //                    8j..8j+7 of the block) of pixel n at j ^ fused_swz_cl(n);
-//                    blocks 2w, 2w+1 are wave w's.
+//                    wave w loads block w.
 //   columns          [64 pixels][64 channels], piece j of pixel n at
 //                    j ^ fused_swz_c(n), read as grad_weight B fragments by
 //                    transposing reads.
-//   corner gathers   per wave [corner q][pixel group i][lane] 16-byte slots;
-//                    after they are read, the same bytes hold the wave's cg.
+//   corner gathers   per wave [corner q][lane] 16-byte slots: lanes 4i..4i+3
+//                    hold the wave's 32 channels of pixel px0 + i.
+//   cg partials      [M half][block (kb, P)][32 pixels][32 channels + 4].
 __device__ __forceinline__ int fused_swz(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
 __device__ __forceinline__ int fused_swz_cl(int n) { return (((n >> 1) & 1) << 1) | ((n >> 2) & 1); }
 __device__ __forceinline__ int fused_swz_c(int n) { return ((n & 3) << 1) | ((n >> 1) & 1); }

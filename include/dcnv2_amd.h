@@ -25,8 +25,13 @@
  *   input  [B, C, H, W]            weight [Cout, C/weight_groups, kh, kw]    bias [Cout]
  *   offset [B, 2*G*kh*kw, Ho, Wo]  mask   [B, G*kh*kw, Ho, Wo]    output [B, Cout, Ho, Wo]
  *   Ho = (H + 2*pad_h - (dilation_h*(kh-1) + 1)) / stride_h + 1   (likewise Wo)
- * All tensors of one call share the dtype in dcn2_desc.dtype; the GEMM
- * accumulates in fp32 and the sampling arithmetic is fp32 for every dtype.
+ * All tensors of one call share the dtype in dcn2_desc.dtype.  Every GEMM
+ * takes its operands in that dtype and accumulates in fp32 (the sampled
+ * columns are rounded to it once, as com.cu:83, 87 rounds them to half); the
+ * bilinear sampling arithmetic is fp32.  Intermediate roundings of the
+ * backward, for fp16 only: the column gradient handed to the grad_input pass
+ * and the one multiplied into the corner sums of grad_offset / grad_mask are
+ * rounded to fp16 (products and sums stay fp32).
  *
  * Return value of every int function: 0 = success, otherwise a DCN2_E* code;
  * dcn2_last_error() then describes the failure.  This replaces the reference's

@@ -72,7 +72,13 @@ def test_exports_every_declared_symbol(L):
 
 
 def test_version(L):
-    assert L.dcn2_version().decode().startswith("dcnv2_amd")
+    """The version string carries the header's ABI version, and the Python
+    descriptor has the header's field count."""
+    abi = re.search(r"#define DCN2_ABI_VERSION (\d+)", open(HEADER).read()).group(1)
+    assert L.dcn2_version().decode() == f"dcnv2_amd {abi} gfx950"
+    struct = re.search(r"typedef struct dcn2_desc \{(.*?)\} dcn2_desc;", open(HEADER).read(), re.S)
+    fields = re.findall(r"\b(\w+)\s*[,;]", re.sub(r"/\*.*?\*/", "", struct.group(1)))
+    assert [f for f, _ in _C.Desc._fields_] == fields
 
 
 @pytest.mark.parametrize("geo", [
