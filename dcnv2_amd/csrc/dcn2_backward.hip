@@ -1349,35 +1349,12 @@ __device__ __forceinline__ int fused_swz_c(int n) { return ((n & 3) << 1) | ((n 
 // Trash bytes each lane of the fused kernel may write (its widest hand-off row).
 constexpr int kFusedTrashLane = 32;
 
-// Buffer -> LDS copy of 16 bytes per lane: lane i's 16 bytes at byte offset
-// `off` of the buffer resource land at LDS byte lds + 16*i (lds is
-// wave-uniform; an offset at or past the resource's size reads zeros).
-// Written as inline assembly so that the compiler does not make later LDS
-// reads wait for it (it cannot tell which LDS bytes it writes); the kernel
-// waits for it explicitly (s_waitcnt vmcnt(0)) before the barrier after which
-// the bytes are read, and the bytes it overwrites were last read before the
-// previous barrier.  (A volatile asm statement stays between the barriers
-// around it; without a memory clobber, LDS reads of the other buffer may be
-// scheduled across it.)  M0 holds the LDS base and is set right before the
-// load.
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rs, int off, unsigned lds) {
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %2, 0 offen lds"
-                 :
-                 : "v"(off), "s"(lds), "s"(rs)
-                 : "m0");
-}
-#pragma clang diagnostic pop
 // Value of lane l ^ 1 / l ^ 2 (within each group of 4 lanes), by DPP quad permutes.
 __device__ __forceinline__ float quad_xor1(float v) {
     return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, true));
 }
 __device__ __forceinline__ float quad_xor2(float v) {
     return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, true));
-}
-__device__ __forceinline__ unsigned lds_addr(const void *p) {
-    return (unsigned)(size_t)(__attribute__((address_space(3))) const void *)p;
 }
 
 template <typename T, bool GN>

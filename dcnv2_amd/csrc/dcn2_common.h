@@ -145,4 +145,29 @@ __device__ __forceinline__ int xcd_remap(int id, int n) {
 }
 __host__ __device__ constexpr inline int round_up(int a, int b) { return ceil_div(a, b) * b; }
 
+// Buffer -> LDS copy of 16 bytes per lane: lane i's 16 bytes at byte offset
+// `off` of the buffer resource land at LDS byte lds + 16*i (lds is
+// wave-uniform; an offset at or past the resource's size reads zeros).
+// Written as inline assembly so that the compiler does not make later LDS
+// reads wait for it (it cannot tell which LDS bytes it writes); a kernel
+// waits for it explicitly (s_waitcnt vmcnt(0)) before the barrier or flag
+// after which the bytes are read, and the bytes it overwrites were last read
+// before an earlier barrier.  (A volatile asm statement stays between the
+// barriers around it; without a memory clobber, LDS reads of other buffers
+// may be scheduled across it.)  M0 holds the LDS base and is set right
+// before the load.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rs, int off, unsigned lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %2, 0 offen lds"
+                 :
+                 : "v"(off), "s"(lds), "s"(rs)
+                 : "m0");
+}
+#pragma clang diagnostic pop
+// LDS byte address of a __shared__ object.
+__device__ __forceinline__ unsigned lds_addr(const void *p) {
+    return (unsigned)(size_t)(__attribute__((address_space(3))) const void *)p;
+}
+
 }  // namespace dcn2
