@@ -190,8 +190,8 @@ __device__ __forceinline__ float shfl_xor_f(float v, int mask) {
 // (workgroup, cell tile) adds its count (count pass) or claims a range of the
 // bucket's rows (place pass).  Claiming rows with one global atomic per wave
 // instead serialises thousands of atomics on each bucket counter.
-constexpr int kBucketTab = 16384;  // cell tiles of one image the LDS table holds
-constexpr int kBucketSPT = 16;     // samples per thread
+constexpr int kBucketTab = 16384;  // cell tiles of one image the LDS table may hold
+constexpr int kBucketSPT = 4;      // samples per thread
 
 struct BucketSample {
     SamplePos sp;
@@ -245,7 +245,7 @@ __device__ __forceinline__ int place_sample(const BwdParams &p, const BucketSamp
 template <bool PLACE>
 __global__ __launch_bounds__(256) void dcn2_bucket_kernel(const BwdParams p, const void *offset_v,
                                                           int esz_is_f32, int is_bf16) {
-    __shared__ int tab[kBucketTab];
+    extern __shared__ int tab[];  // [nty * ntx]: sized at launch, so small images run many workgroups per CU
     const int N = p.Ho * p.Wo, KK = p.kh * p.kw;
     const int tid = threadIdx.x, ntile = p.nty * p.ntx;
     const int plane = blockIdx.y, b = blockIdx.z, g = plane / KK;
@@ -2063,16 +2063,18 @@ __global__ __launch_bounds__(512) void dcn2_gi_gather_kernel(const BwdParams p) 
                     __builtin_amdgcn_sched_barrier(0);
                 }
                 // Interior pixels (reachable from this tile's cells only) are this
-                // block's alone: a plain read-modify-write.  The accumulator's
-                // padding channels (Cg..Cgp of a group) are never read back (and
-                // receive zeros), so whole 16-byte pieces are updated (a guarded
-                // update per channel made every channel a separate round trip).
+                // block's alone: the first batch writes them (zeros included, so
+                // the accumulator needs no clearing), later batches add.  The
+                // accumulator's padding channels (Cg..Cgp of a group) are never
+                // read back (and receive zeros), so whole 16-byte pieces are
+                // written (a guarded update per channel made every channel a
+                // separate round trip).
                 if (py >= 1 && py <= TS - 1 && px >= 1 && px <= TS - 1) {
-                    if (tot == 0) continue;
+                    if (!live || (!first && tot == 0)) continue;
                     f32x4 *d4 = reinterpret_cast<f32x4 *>(gi + ((size_t)Y * p.W + X) * cs + cc * KC + co * EPL);
                     f32x4 acc4[EPL / 4];
 #pragma unroll
-                    for (int i = 0; i < EPL / 4; ++i) acc4[i] = d4[i];
+                    for (int i = 0; i < EPL / 4; ++i) acc4[i] = first ? f32x4{0.0f, 0.0f, 0.0f, 0.0f} : d4[i];
 #pragma unroll
                     for (int i = 0; i < EPL / 4; ++i) {
 #pragma unroll
@@ -2098,12 +2100,21 @@ __global__ __launch_bounds__(512) void dcn2_gi_gather_kernel(const BwdParams p) 
 }
 
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void fill_zero_kernel(float4 *__restrict__ p, size_t n4) {
+// Zeroes three buffers (blockIdx.y picks one; an empty one has n4 == 0).  A
+// kernel rather than hipMemsetAsync, so that a captured graph stays valid.
+struct FillArgs {
+    float4 *p[3];
+    size_t n4[3];
+};
+__global__ __launch_bounds__(256) void fill_zero3_kernel(const FillArgs a) {
+    float4 *__restrict__ p = a.p[blockIdx.y];
+    const size_t n4 = a.n4[blockIdx.y];
     for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (size_t)gridDim.x * 256)
         p[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 }
 
-// Adds the gather's border-ring partials into gi_acc.  The tile-boundary
+// Writes the sums of the gather's border-ring partials into gi_acc (the
+// gather writes every other pixel, so gi_acc is never cleared).  The tile-boundary
 // pixels are those with (Y+1) % TS == 0 or (X+1) % TS == 0: the whole rows
 // Y = TS*k + TS-1 (nrow of them) first, then the columns X = TS*k + TS-1
 // (ncol) without those rows.  Pixel (Y, X) is (py, px) = ((Y+1) % TS,
@@ -2111,7 +2122,7 @@ __global__ __launch_bounds__(256) void fill_zero_kernel(float4 *__restrict__ p, 
 // of the tile above when py == 0 and column TS of the tile to the left when
 // px == 0; it is on the ring of each of those windows.  One thread per pixel
 // and 4 padded channels; every pixel has exactly one thread, so the update is
-// a plain read-modify-write.
+// a plain write.
 __global__ __launch_bounds__(256) void ring_merge_kernel(float *__restrict__ gi_acc,
                                                          const float *__restrict__ ring, int H,
                                                          int W, int cs, int Cgp, int G, int nty,
@@ -2136,7 +2147,7 @@ __global__ __launch_bounds__(256) void ring_merge_kernel(float *__restrict__ gi_
     const int g = cp / Cgp, ci = cp - g * Cgp;
     const int py = (Y + 1) % TS, ty = (Y + 1) / TS, px = (X + 1) % TS, tx = (X + 1) / TS;
     f32x4 *dst = reinterpret_cast<f32x4 *>(gi_acc + (((size_t)b * H + Y) * W + X) * cs + cp);
-    f32x4 v = *dst;
+    f32x4 v = f32x4{0.0f, 0.0f, 0.0f, 0.0f};  // the gather never writes these pixels
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
         if (i == 1 && (py != 0 || ty == 0)) continue;
@@ -2263,20 +2274,24 @@ static hipError_t backward_t(const Geo &g, const BwdParams &p0, void *grad_input
                              void *grad_weight, void *grad_bias, hipStream_t s) {
     BwdParams p = p0;
     hipError_t e;
-    // 1. zero the fp32 accumulators
+    // 1. zero the fp32 grad_weight / grad_bias accumulators and the bucket
+    //    counts in one launch (gi_acc needs no clearing: the gather writes
+    //    every interior pixel and ring_merge_kernel every boundary pixel)
     prof_begin(DCN2_STAGE_BWD_PACK, s);
     {
-        const size_t n_gi = (size_t)g.B * g.H * g.W * g.cs;
-        const size_t n_gw = (size_t)g.Mp * g.Kp;
+        FillArgs fa;
         // gb_acc is null when the caller wants no grad_bias; nothing reads it then.
-        float *bufs[4] = {p.gi_acc, p.gw_acc, p.gb_acc, (float *)p.bcnt};
-        const size_t counts[4] = {n_gi, n_gw, (size_t)g.Mp,
-                                  (size_t)g.B * g.G * p.nty * p.ntx};
-        for (int i = 0; i < 4; ++i) {
-            const size_t n4 = (counts[i] + 3) / 4;
-            if (n4 == 0 || bufs[i] == nullptr) continue;
-            const unsigned blocks = (unsigned)std::min<size_t>((n4 + 255) / 256, 4096);
-            fill_zero_kernel<<<blocks, 256, 0, s>>>((float4 *)bufs[i], n4);
+        float *bufs[3] = {p.gw_acc, p.gb_acc, (float *)p.bcnt};
+        const size_t counts[3] = {(size_t)g.Mp * g.Kp, (size_t)g.Mp, (size_t)g.B * g.G * p.nty * p.ntx};
+        size_t most = 0;
+        for (int i = 0; i < 3; ++i) {
+            fa.p[i] = (float4 *)bufs[i];
+            fa.n4[i] = bufs[i] ? (counts[i] + 3) / 4 : 0;
+            most = std::max(most, fa.n4[i]);
+        }
+        if (most) {
+            const unsigned blocks = (unsigned)std::min<size_t>((most + 255) / 256, 4096);
+            fill_zero3_kernel<<<dim3(blocks, 3), 256, 0, s>>>(fa);
             if ((e = hipGetLastError()) != hipSuccess) return e;
         }
     }
@@ -2307,12 +2322,13 @@ static hipError_t backward_t(const Geo &g, const BwdParams &p0, void *grad_input
             const int nbuckets = g.B * g.G * p.nty * p.ntx;
             const bool tab = (long)p.nty * p.ntx <= kBucketTab;
             const dim3 bgrid(ceil_div(g.N, tab ? 256 * kBucketSPT : 256), g.G * g.KK, g.B);
-            if (tab) dcn2_bucket_kernel<false><<<bgrid, 256, 0, s>>>(p, p.offset, f32, isbf);
+            const size_t tab_bytes = (size_t)p.nty * p.ntx * sizeof(int);
+            if (tab) dcn2_bucket_kernel<false><<<bgrid, 256, tab_bytes, s>>>(p, p.offset, f32, isbf);
             else dcn2_bucket_global_kernel<false><<<bgrid, 256, 0, s>>>(p, p.offset, f32, isbf);
             if ((e = hipGetLastError()) != hipSuccess) return e;
             dcn2_bucket_scan_kernel<<<1, 1024, 0, s>>>(p.bcnt, p.bstart, p.bcur, nbuckets);
             if ((e = hipGetLastError()) != hipSuccess) return e;
-            if (tab) dcn2_bucket_kernel<true><<<bgrid, 256, 0, s>>>(p, p.offset, f32, isbf);
+            if (tab) dcn2_bucket_kernel<true><<<bgrid, 256, tab_bytes, s>>>(p, p.offset, f32, isbf);
             else dcn2_bucket_global_kernel<true><<<bgrid, 256, 0, s>>>(p, p.offset, f32, isbf);
             if ((e = hipGetLastError()) != hipSuccess) return e;
         }
