@@ -259,9 +259,19 @@ static int backward_impl(const Geo &g, const void *input, const void *weight, co
     char *base = (char *)workspace;
     const void *xt = g.xt_direct ? input : base + ws.xt;
     void *wt = base + ws.wt, *tab = base + ws.tab;
+    // the pack launch also zeroes the grad_weight / grad_bias accumulators and
+    // the bucket counts
+    const GatherGeo gg = gather_geometry(g);
+    ClearList clr;
+    clr.p[0] = (float *)(base + ws.gw_acc);
+    clr.n[0] = (size_t)g.Mp * g.Kp;
+    clr.p[1] = (float *)(base + ws.gb_acc);
+    clr.n[1] = grad_bias ? (size_t)g.Mp : 0;
+    clr.p[2] = (float *)(base + ws.bcnt);
+    clr.n[2] = g.B > 0 ? (size_t)gg.nbuckets : 0;
     prof_begin(DCN2_STAGE_BWD_PACK, s);
     if ((rc = check_launch(launch_pack(g, g.xt_direct ? nullptr : input, (void *)xt, weight, wt,
-                                       tab, true, s), "pack")))
+                                       tab, true, s, &clr), "pack")))
         return rc;
     prof_end(DCN2_STAGE_BWD_PACK, s);
     return check_launch(launch_backward(g, xt, wt, tab, offset, mask, grad_output,

@@ -2100,19 +2100,6 @@ __global__ __launch_bounds__(512) void dcn2_gi_gather_kernel(const BwdParams p) 
 }
 
 // ---------------------------------------------------------------------------
-// Zeroes three buffers (blockIdx.y picks one; an empty one has n4 == 0).  A
-// kernel rather than hipMemsetAsync, so that a captured graph stays valid.
-struct FillArgs {
-    float4 *p[3];
-    size_t n4[3];
-};
-__global__ __launch_bounds__(256) void fill_zero3_kernel(const FillArgs a) {
-    float4 *__restrict__ p = a.p[blockIdx.y];
-    const size_t n4 = a.n4[blockIdx.y];
-    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (size_t)gridDim.x * 256)
-        p[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-}
-
 // Writes the sums of the gather's border-ring partials into gi_acc (the
 // gather writes every other pixel, so gi_acc is never cleared).  The tile-boundary
 // pixels are those with (Y+1) % TS == 0 or (X+1) % TS == 0: the whole rows
@@ -2162,6 +2149,36 @@ __global__ __launch_bounds__(256) void ring_merge_kernel(float *__restrict__ gi_
     *dst = v;
 }
 
+// gw_acc [Mp][Kp] (K order tap, group, channel) -> grad_weight [Cout][C][kh][kw];
+// gb_acc -> grad_bias.  nblk workgroups of 256 threads; the grad_input
+// finalisation kernels run them as extra workgroups of their own launch.
+template <typename T> struct GwFinal {
+    const float *gwa, *gba;
+    T *gw, *gb;
+    int Cout, Cw, mpg, KK, Cg, Cgp, G, Kp;
+    long nblk;
+};
+template <typename T>
+__device__ __forceinline__ void finalize_gw_block(const GwFinal<T> &f, long blk) {
+    // grad_weight [Cout][Cw][KK]: row m's channel cl is input channel
+    // (m / mpg) * Cw + cl, the diagonal block of the block-diagonal W'.
+    const long idx = blk * 256 + threadIdx.x;
+    const long total = (long)f.Cout * f.Cw * f.KK;
+    if (idx < total) {
+        const int m = (int)(idx / ((long)f.Cw * f.KK));
+        const int r = (int)(idx - (long)m * f.Cw * f.KK);
+        const int cl = r / f.KK, tap = r - cl * f.KK;
+        const int c = (m / f.mpg) * f.Cw + cl;
+        const int g = c / f.Cg, ci = c - g * f.Cg;
+        f.gw[idx] = (T)f.gwa[(size_t)m * f.Kp + ((size_t)tap * f.G + g) * f.Cgp + ci];
+    }
+    if (f.gb && idx < f.Cout) f.gb[idx] = (T)f.gba[idx];
+}
+template <typename T>
+__global__ __launch_bounds__(256) void finalize_gw_kernel(const GwFinal<T> f) {
+    finalize_gw_block(f, blockIdx.x);
+}
+
 // gi_acc [B][HW][cs] fp32 -> grad_input [B][C][HW] T; 64 pixels x 32 padded
 // channels per block, transposed through LDS.  Loads: 8 lanes per pixel, 16
 // bytes (4 channels) each.  Stores: 8 lanes per channel row, 8 consecutive
@@ -2170,8 +2187,14 @@ __global__ __launch_bounds__(256) void ring_merge_kernel(float *__restrict__ gi_
 template <typename T>
 __global__ __launch_bounds__(256) void finalize_gi_kernel(const float *__restrict__ acc,
                                                           T *__restrict__ gi, int C, int HW,
-                                                          int Cg, int Cgp, int cs, int vec) {
+                                                          int Cg, int Cgp, int cs, int vec, int B,
+                                                          const GwFinal<T> f) {
     __shared__ float tile[64][33];
+    if ((int)blockIdx.z >= B) {  // z slices past the batch: grad_weight / grad_bias
+        const long blk = blockIdx.x + (long)gridDim.x * (blockIdx.y + (long)gridDim.y * (blockIdx.z - B));
+        if (blk < f.nblk) finalize_gw_block(f, blk);
+        return;
+    }
     const int px0 = blockIdx.x * 64, cp0 = blockIdx.y * 32, b = blockIdx.z;
     const int tid = threadIdx.x;
 #pragma unroll
@@ -2218,8 +2241,13 @@ template <typename T>
 __global__ __launch_bounds__(256) void finalize_gi_nhwc_kernel(const float *__restrict__ acc,
                                                                T *__restrict__ gi, long total,
                                                                int C, int Cg, int Cgp, int cs,
-                                                               int vec4) {
-    const long stride = (long)gridDim.x * 256;
+                                                               int vec4, int nmain,
+                                                               const GwFinal<T> f) {
+    if ((int)blockIdx.x >= nmain) {  // workgroups past nmain: grad_weight / grad_bias
+        finalize_gw_block(f, blockIdx.x - nmain);
+        return;
+    }
+    const long stride = (long)nmain * 256;
     if (vec4) {
         for (long i4 = (long)blockIdx.x * 256 + threadIdx.x; i4 < total / 4; i4 += stride) {
             const long idx = i4 * 4;
@@ -2245,57 +2273,15 @@ __global__ __launch_bounds__(256) void finalize_gi_nhwc_kernel(const float *__re
     }
 }
 
-// gw_acc [Mp][Kp] (K order tap, group, channel) -> grad_weight [Cout][C][kh][kw];
-// gb_acc -> grad_bias.
-template <typename T>
-__global__ __launch_bounds__(256) void finalize_gw_kernel(const float *__restrict__ gwa,
-                                                          const float *__restrict__ gba,
-                                                          T *__restrict__ gw, T *__restrict__ gb,
-                                                          int Cout, int Cw, int mpg, int KK,
-                                                          int Cg, int Cgp, int G, int Kp) {
-    // grad_weight [Cout][Cw][KK]: row m's channel cl is input channel
-    // (m / mpg) * Cw + cl, the diagonal block of the block-diagonal W'.
-    const long idx = (long)blockIdx.x * 256 + threadIdx.x;
-    const long total = (long)Cout * Cw * KK;
-    if (idx < total) {
-        const int m = (int)(idx / ((long)Cw * KK));
-        const int r = (int)(idx - (long)m * Cw * KK);
-        const int cl = r / KK, tap = r - cl * KK;
-        const int c = (m / mpg) * Cw + cl;
-        const int g = c / Cg, ci = c - g * Cg;
-        gw[idx] = (T)gwa[(size_t)m * Kp + ((size_t)tap * G + g) * Cgp + ci];
-    }
-    if (gb && idx < Cout) gb[idx] = (T)gba[idx];
-}
-
 // ---------------------------------------------------------------------------
 template <typename T>
 static hipError_t backward_t(const Geo &g, const BwdParams &p0, void *grad_input,
                              void *grad_weight, void *grad_bias, hipStream_t s) {
     BwdParams p = p0;
     hipError_t e;
-    // 1. zero the fp32 grad_weight / grad_bias accumulators and the bucket
-    //    counts in one launch (gi_acc needs no clearing: the gather writes
-    //    every interior pixel and ring_merge_kernel every boundary pixel)
-    prof_begin(DCN2_STAGE_BWD_PACK, s);
-    {
-        FillArgs fa;
-        // gb_acc is null when the caller wants no grad_bias; nothing reads it then.
-        float *bufs[3] = {p.gw_acc, p.gb_acc, (float *)p.bcnt};
-        const size_t counts[3] = {(size_t)g.Mp * g.Kp, (size_t)g.Mp, (size_t)g.B * g.G * p.nty * p.ntx};
-        size_t most = 0;
-        for (int i = 0; i < 3; ++i) {
-            fa.p[i] = (float4 *)bufs[i];
-            fa.n4[i] = bufs[i] ? (counts[i] + 3) / 4 : 0;
-            most = std::max(most, fa.n4[i]);
-        }
-        if (most) {
-            const unsigned blocks = (unsigned)std::min<size_t>((most + 255) / 256, 4096);
-            fill_zero3_kernel<<<dim3(blocks, 3), 256, 0, s>>>(fa);
-            if ((e = hipGetLastError()) != hipSuccess) return e;
-        }
-    }
-    prof_end(DCN2_STAGE_BWD_PACK, s);
+    // (the fp32 grad_weight / grad_bias accumulators and the bucket counts
+    // were zeroed by the pack launch; gi_acc needs no clearing: the gather
+    // writes every interior pixel and ring_merge_kernel every boundary pixel)
     int dev = 0, ncu = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
@@ -2306,6 +2292,22 @@ static hipError_t backward_t(const Geo &g, const BwdParams &p0, void *grad_input
     // that take 16-byte loads, and images of gO and xt below 2 GiB each.
     // DCN2_BWD_FUSED=0 in the environment selects the two-kernel path for
     // every shape (the tests compare both paths).
+    // grad_weight / grad_bias finalisation (run by the grad_input finalisation
+    // launch, or alone for an empty batch)
+    GwFinal<T> gwf;
+    gwf.gwa = p.gw_acc;
+    gwf.gba = p.gb_acc;
+    gwf.gw = (T *)grad_weight;
+    gwf.gb = (T *)grad_bias;
+    gwf.Cout = g.Cout;
+    gwf.Cw = g.Cw;
+    gwf.mpg = g.Cout / g.WG;
+    gwf.KK = g.KK;
+    gwf.Cg = g.Cg;
+    gwf.Cgp = g.Cgp;
+    gwf.G = g.G;
+    gwf.Kp = g.Kp;
+    gwf.nblk = (std::max<long>((long)g.Cout * g.Cw * g.KK, g.Cout) + 255) / 256;
     bool fused = false;
     const char *fenv = std::getenv("DCN2_BWD_FUSED");
     if constexpr (sizeof(T) == 2)
@@ -2449,29 +2451,27 @@ static hipError_t backward_t(const Geo &g, const BwdParams &p0, void *grad_input
                 const int vec4 = g.C % 4 == 0 && g.Cg % 4 == 0 &&
                                  ((uintptr_t)grad_input % (4 * sizeof(T))) == 0;
                 const long work = vec4 ? total / 4 : total;
-                const unsigned blocks = (unsigned)std::min<long>((work + 255) / 256, 16384);
-                finalize_gi_nhwc_kernel<T><<<blocks, 256, 0, s>>>(
-                    p.gi_acc, (T *)grad_input, total, g.C, g.Cg, g.Cgp, g.cs, vec4);
+                const int nmain = (int)std::min<long>((work + 255) / 256, 16384);
+                finalize_gi_nhwc_kernel<T><<<(unsigned)(nmain + gwf.nblk), 256, 0, s>>>(
+                    p.gi_acc, (T *)grad_input, total, g.C, g.Cg, g.Cgp, g.cs, vec4, nmain, gwf);
             } else {
-                dim3 grid(ceil_div(HW, 64), g.cs / 32, g.B);
+                // grad_weight's workgroups in extra z slices of the same grid
+                const unsigned gx = ceil_div(HW, 64), gy = g.cs / 32;
+                const unsigned zw = (unsigned)((gwf.nblk + (long)gx * gy - 1) / ((long)gx * gy));
                 const int vec = HW % 8 == 0 && ((uintptr_t)grad_input & 15) == 0;
-                finalize_gi_kernel<T><<<grid, 256, 0, s>>>(p.gi_acc, (T *)grad_input, g.C, HW,
-                                                           g.Cg, g.Cgp, g.cs, vec);
+                finalize_gi_kernel<T><<<dim3(gx, gy, g.B + zw), 256, 0, s>>>(
+                    p.gi_acc, (T *)grad_input, g.C, HW, g.Cg, g.Cgp, g.cs, vec, g.B, gwf);
             }
             if ((e = hipGetLastError()) != hipSuccess) return e;
         }
         prof_end(DCN2_STAGE_BWD_FINAL, s);
-    }
-    // 5. grad_weight / grad_bias to the caller's layout
-    prof_begin(DCN2_STAGE_BWD_FINAL, s);
-    {
-        const long total = std::max<long>((long)g.Cout * g.Cw * g.KK, g.Cout);
-        finalize_gw_kernel<T><<<(unsigned)((total + 255) / 256), 256, 0, s>>>(
-            p.gw_acc, p.gb_acc, (T *)grad_weight, (T *)grad_bias, g.Cout, g.Cw, g.Cout / g.WG,
-            g.KK, g.Cg, g.Cgp, g.G, g.Kp);
+    } else {
+        // 5. (empty batch) grad_weight / grad_bias alone
+        prof_begin(DCN2_STAGE_BWD_FINAL, s);
+        finalize_gw_kernel<T><<<(unsigned)gwf.nblk, 256, 0, s>>>(gwf);
         if ((e = hipGetLastError()) != hipSuccess) return e;
+        prof_end(DCN2_STAGE_BWD_FINAL, s);
     }
-    prof_end(DCN2_STAGE_BWD_FINAL, s);
     return hipSuccess;
 }
 

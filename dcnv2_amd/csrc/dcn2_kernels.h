@@ -76,8 +76,14 @@ GatherGeo gather_geometry(const Geo &g);
 // dcn2_pack.hip: input -> xt (skipped when input is null) and weight -> wp +
 // chunk table in one launch; transpose selects the backward's W'^T fragment
 // order.  The input is NCHW, or channels-last when g.nhwc.
+// Up to three fp32 buffers the pack launch also zeroes (extra workgroups), so
+// the backward's accumulators need no launch of their own; n = 0 skips one.
+struct ClearList {
+    float *p[3];
+    size_t n[3];
+};
 hipError_t launch_pack(const Geo &g, const void *input, void *xt, const void *weight, void *wp,
-                       void *tab, bool transpose, hipStream_t s);
+                       void *tab, bool transpose, hipStream_t s, const ClearList *clear = nullptr);
 
 // dcn2_forward.hip
 hipError_t launch_forward(const Geo &g, const void *xt, const void *wp, const void *tab,

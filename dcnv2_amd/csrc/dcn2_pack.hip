@@ -32,7 +32,12 @@ struct PackParams {
     int kc, kstep, kpl, Mp, Kp;    // MFMA packing
     int transpose;                 // 0: forward A fragments, 1: backward W'^T fragments
     int nhwc;                      // input is channels-last [B][HW][C]
+    int nw;                        // weight blocks
+    float4 *clr[3];                // buffers to zero, 16-byte pieces each
+    long clr_n4[3];
+    int clr_blk[4];                // first clearing block of each buffer (prefix sums)
 };
+constexpr int kClearPieces = 1024;  // 16-byte pieces zeroed per clearing block
 
 // Channels-last input [B][HW][C] -> xt [B][HW][cs]: the same tile of 64
 // pixels x CT padded channels, one element per thread and step (consecutive
@@ -179,13 +184,21 @@ __global__ __launch_bounds__(256) void pack_kernel(const PackParams p) {
             pack_input_block_nhwc<T>(p, blk);
         else
             pack_input_block<T>(p, blk);
-    } else
+    } else if (blk < p.nin + p.nw) {
         pack_weight_block<T>(p, blk - p.nin);
+    } else {
+        // zero kClearPieces 16-byte pieces of one of the clear-list buffers
+        const int cb = blk - p.nin - p.nw;
+        const int i = cb < p.clr_blk[1] ? 0 : (cb < p.clr_blk[2] ? 1 : 2);
+        const long base = (long)(cb - p.clr_blk[i]) * kClearPieces;
+        for (int k = threadIdx.x; k < kClearPieces; k += 256)
+            if (base + k < p.clr_n4[i]) p.clr[i][base + k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
 }
 
 template <typename T>
 static hipError_t pack_t(const Geo &g, const void *input, void *xt, const void *weight,
-                         void *wp, void *tab, bool transpose, hipStream_t s) {
+                         void *wp, void *tab, bool transpose, hipStream_t s, const ClearList *clear) {
     constexpr int E = 16 / sizeof(T), CT = 128 / sizeof(T);
     PackParams p;
     p.in = input;
@@ -219,18 +232,26 @@ static hipError_t pack_t(const Geo &g, const void *input, void *xt, const void *
     p.transpose = transpose ? 1 : 0;
     p.nhwc = g.nhwc;
     const long nw = ((long)g.Mp * g.Kp + 255) / 256;
-    const long blocks = p.nin + nw;
+    p.nw = (int)nw;
+    p.clr_blk[0] = 0;
+    for (int i = 0; i < 3; ++i) {
+        const size_t n = clear ? clear->n[i] : 0;
+        p.clr[i] = n ? (float4 *)clear->p[i] : nullptr;
+        p.clr_n4[i] = (long)((n + 3) / 4);
+        p.clr_blk[i + 1] = p.clr_blk[i] + (int)((p.clr_n4[i] + kClearPieces - 1) / kClearPieces);
+    }
+    const long blocks = p.nin + nw + p.clr_blk[3];
     pack_kernel<T><<<(unsigned)blocks, 256, 0, s>>>(p);
     return hipGetLastError();
 }
 
 hipError_t launch_pack(const Geo &g, const void *input, void *xt, const void *weight, void *wp,
-                       void *tab, bool transpose, hipStream_t s) {
+                       void *tab, bool transpose, hipStream_t s, const ClearList *clear) {
     if (g.B == 0) input = nullptr;  // weight packing only (also for an input read in place)
     switch (g.dtype) {
-    case DCN2_F16: return pack_t<f16>(g, input, xt, weight, wp, tab, transpose, s);
-    case DCN2_BF16: return pack_t<bf16>(g, input, xt, weight, wp, tab, transpose, s);
-    default: return pack_t<float>(g, input, xt, weight, wp, tab, transpose, s);
+    case DCN2_F16: return pack_t<f16>(g, input, xt, weight, wp, tab, transpose, s, clear);
+    case DCN2_BF16: return pack_t<bf16>(g, input, xt, weight, wp, tab, transpose, s, clear);
+    default: return pack_t<float>(g, input, xt, weight, wp, tab, transpose, s, clear);
     }
 }
 
