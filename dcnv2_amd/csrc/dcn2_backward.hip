@@ -1377,10 +1377,10 @@ void dcn2_bwd_fused_kernel(const BwdParams p) {
     __shared__ __attribute__((aligned(16))) T sG[2][MP * BN];         // gO stage (double)
     __shared__ __attribute__((aligned(16))) uint4 sK[8][4][64];       // corner gathers per wave
     __shared__ __attribute__((aligned(16))) float sX[2][4][32][LDX];  // cg partials [M half][block]
-    __shared__ __attribute__((aligned(16))) T sC[BN][KC];             // blended columns
+    __shared__ __attribute__((aligned(16))) T sC[2][BN][KC];          // blended columns (double)
     __shared__ __attribute__((aligned(16))) f32x4 sS[2][BN];          // corner sums per K block
-    __shared__ __attribute__((aligned(16))) f32x4 sD[2][BN][3];       // sampling descriptors
-    __shared__ int sV[2][BN];                                         // corner validity bits
+    __shared__ __attribute__((aligned(16))) f32x4 sD[3][BN][3];       // sampling descriptors
+    __shared__ int sV[3][BN];                                         // corner validity bits
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1470,8 +1470,8 @@ void dcn2_bwd_fused_kernel(const BwdParams p) {
         return &sG[buf][(m >> 5) * (BN * 32) + n * 32 + ((((m >> 3) & 3) ^ fused_swz_cl(n)) << 3) +
                         (m & 7)];
     };
-    auto at_c = [&](int n, int k) __attribute__((always_inline)) {
-        return &sC[n][(((k >> 3) ^ fused_swz_c(n)) << 3) + (k & 7)];
+    auto at_c = [&](int cb, int n, int k) __attribute__((always_inline)) {
+        return &sC[cb][n][(((k >> 3) ^ fused_swz_c(n)) << 3) + (k & 7)];
     };
     // Transposing read (ds_read_b64_tr_b16: within 16 lanes, lane i receives
     // element i%4 of the 4-element pieces that lanes i/4, 4 + i/4, 8 + i/4,
@@ -1623,8 +1623,15 @@ void dcn2_bwd_fused_kernel(const BwdParams p) {
     };
     // Lane (pixel px0 + l/4, channels 32kb + 8(l%4) ..): corner sums, hand-off
     // and blend.  raw: the lane's corner gathers (read before the barrier).
+    // between(j), j = 0..7, runs at eight points of the work, each fenced by
+    // scheduling barriers (it issues the MFMAs that overlap this VALU work).
     const int pq = lane >> 2, cq = lane & 3;
-    auto consume = [&](int buf, int dbuf, const uint4 (&raw)[4]) __attribute__((always_inline)) {
+    auto consume = [&](int buf, int dbuf, const uint4 (&raw)[4], auto between) __attribute__((always_inline)) {
+        auto at = [&](int j) __attribute__((always_inline)) {
+            __builtin_amdgcn_sched_barrier(0);
+            between(j);
+            __builtin_amdgcn_sched_barrier(0);
+        };
         const int px = px0 + pq;
         const f32x4 d0 = sD[dbuf][px][0], d1 = sD[dbuf][px][1];
         float cgv[E];
@@ -1635,6 +1642,7 @@ void dcn2_bwd_fused_kernel(const BwdParams p) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) cgv[4 * h + e] = v[e];
         }
+        at(0);
         // corner sums over the lane's 8 channels, then over the 4 lanes of the
         // pixel.  f16: 2-element dot products (v_dot2_f32_f16) of the corner
         // values with the column gradient rounded to f16, accumulated in fp32
@@ -1661,8 +1669,10 @@ void dcn2_bwd_fused_kernel(const BwdParams p) {
             s += quad_xor1(s);
             s += quad_xor2(s);
             S[q] = s;
+            if (q < 3) at(1 + q);
         }
         if (cq == 0) sS[kb][px] = S;
+        at(4);
         // masked column-gradient row
         {
             const int srow = __float_as_int(d1[1]);
@@ -1675,6 +1685,7 @@ void dcn2_bwd_fused_kernel(const BwdParams p) {
 #pragma unroll
             for (int u = 0; u < NST; ++u) row[u] = pack16<R>(mrow + u * (16 / sizeof(R)));
         }
+        at(5);
         // blended columns
         {
             float col[E], v[E];
@@ -1685,9 +1696,11 @@ void dcn2_bwd_fused_kernel(const BwdParams p) {
                 Unpack<T>::run(raw[q], v);
 #pragma unroll
                 for (int e = 0; e < E; ++e) col[e] = fmaf(d0[q], v[e], col[e]);
+                if (q == 1) at(6);
             }
-            *reinterpret_cast<uint4 *>(at_c(px, kb * 32 + cq * E)) = pack16<T>(col);
+            *reinterpret_cast<uint4 *>(at_c(buf, px, kb * 32 + cq * E)) = pack16<T>(col);
         }
+        at(7);
     };
 
     // ---- phase B ----------------------------------------------------------------
@@ -1737,40 +1750,57 @@ void dcn2_bwd_fused_kernel(const BwdParams p) {
         }
         return acc;
     };
-    // (grad_bias: compile-time switch, so no branch sits between the MFMAs;
-    // after(s) runs after MFMA s = 2 ks + i)
-    auto gradw = [&](int buf, auto bias_c, auto after) __attribute__((always_inline)) {
-        frag a[NKS], bf[NKS][2];
-        auto rd = [&](int ks) __attribute__((always_inline)) {
-            a[ks] = go_afrag(buf, ks);
+    // grad_weight A fragments of the wave's own gO rows (rows 32 wave ..,
+    // which only this wave loads) of the tile in sG[buf]
+    auto read_afrags = [&](int buf, frag (&a)[NKS]) __attribute__((always_inline)) {
 #pragma unroll
-            for (int i = 0; i < 2; ++i) bf[ks][i] = tr_frag(at_c, ks * KSTEP, i * 32);
-        };
-        rd(0);
+        for (int ks = 0; ks < NKS; ++ks) a[ks] = go_afrag(buf, ks);
+    };
+    // grad_weight B fragments (columns of the tile in sC[cb]) and MFMA j =
+    // 2 ks + i of gW += gO cols^T (grad_bias: compile-time switch, so no
+    // branch sits between the MFMAs)
+    auto read_bfrags = [&](int cb, frag (&b)[NKS][2]) __attribute__((always_inline)) {
+        const auto atc = [&](int n, int k) __attribute__((always_inline)) { return at_c(cb, n, k); };
 #pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) {
-            if (ks + 1 < NKS) rd(ks + 1);
+        for (int ks = 0; ks < NKS; ++ks)
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                gacc[i] = M::mma(a[ks], bf[ks][i], gacc[i]);
-                after(2 * ks + i);
-            }
-            if constexpr (decltype(bias_c)::value) bsum = sum8(a[ks], bsum);
-            __builtin_amdgcn_sched_barrier(0);
-        }
+            for (int i = 0; i < 2; ++i) b[ks][i] = tr_frag(atc, ks * KSTEP, i * 32);
+    };
+    auto gradw_mma = [&](const frag (&a)[NKS], const frag (&b)[NKS][2], int j, auto bias_c)
+        __attribute__((always_inline)) {
+        const int ks = j >> 1, i = j & 1;
+        gacc[i] = M::mma(a[ks], b[ks][i], gacc[i]);
+        if constexpr (decltype(bias_c)::value)
+            if (i == 1) bsum = sum8(a[ks], bsum);
+    };
+    auto gradw = [&](const frag (&a)[NKS], int cb, auto bias_c) __attribute__((always_inline)) {
+        frag b[NKS][2];
+        read_bfrags(cb, b);
+#pragma unroll
+        for (int j = 0; j < 2 * NKS; ++j) gradw_mma(a, b, j, bias_c);
     };
 
     // ---- the tiles ----------------------------------------------------------------
-    // gO: double-buffered, the next tile's rows loaded during the column
-    // gradient; corner gathers: one buffer per wave, the next tile's issued
-    // during grad_weight (after the tile's own were read).  Everything a tile
-    // loads is waited for once, before its last barrier.
-    // Descriptors: two buffers, tile t's in sD[(t - t_begin) % 2]; the
-    // sampler writes tile t+1's in phase A of tile t, whose phase B issues
-    // tile t+1's gathers.  The sampler's offsets of tile t+1 are loaded at the
-    // top of tile t-1 into the register set of tile t+1's parity (the loop is
-    // unrolled by two), so the end-of-tile wait has covered them when they
-    // are used and no register copy or early wait is needed.
+    // Two phases per tile t, one barrier after each:
+    //   A  column gradient of t (MFMA) -> sX, with t+1's gO rows loaded
+    //      between the MFMAs; the wave's corner gathers of t read from LDS;
+    //      the sampler writes t+1's descriptors; the finisher turns t-1's
+    //      corner sums into grad_offset / grad_mask.
+    //   B  t+1's corner gathers are loaded into the wave's gather area;
+    //      consume(t) (VALU: corner sums, hand-off, blend -> sC[t % 2]) runs
+    //      beside grad_weight of t-1 (MFMA, columns from sC[(t - 1) % 2]), so
+    //      one wave's VALU overlaps the other's MFMAs; then the wave reads
+    //      t's grad_weight A fragments from its own gO rows into registers.
+    // gO: double-buffered; a buffer is reloaded (in phase A of t+1) only with
+    // the rows of the waves that already hold its A fragments, which each
+    // wave reads from its own rows only.  Columns: double-buffered.
+    // Descriptors: three buffers, tile t's in sD[(t - t_begin) % 3] (written
+    // in phase A of t-1, read until phase A of t+1).  Everything a tile loads
+    // is waited for once, before its last barrier.  The sampler's offsets of
+    // tile t+1 are loaded at the top of tile t-1 into the register set of
+    // tile t+1's parity (the loop is unrolled by two), so the end-of-tile wait
+    // has covered them when they are used and no register copy or early wait
+    // is needed.
     auto tiles = [&](auto bias_c) __attribute__((always_inline)) {
         OM om[2];
         const TileId id0 = tile_id(t_begin);
@@ -1790,40 +1820,66 @@ void dcn2_bwd_fused_kernel(const BwdParams p) {
         }
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the stage loads
         __syncthreads();
-        // tile t, buffer parity `buf` = (t - t_begin) % 2
-        auto step = [&](auto buf_c, int t) __attribute__((always_inline)) {
+        int d3 = 0;    // (t - t_begin) % 3
+        frag ga[NKS];  // grad_weight A fragments of the previous tile
+        // tile t, buffer parity `buf` = (t - t_begin) % 2; `first`: t == t_begin
+        auto step = [&](auto buf_c, auto first_c, int t) __attribute__((always_inline)) {
             constexpr int buf = decltype(buf_c)::value;
+            constexpr bool first = decltype(first_c)::value;
+            const int d3n = d3 == 2 ? 0 : d3 + 1, d3p = d3 == 0 ? 2 : d3 - 1;
             const int tn = min(t + 1, t_last);
-            const TileId it = tile_id(t), itn = tile_id(tn);
-            const unsigned gl = go_lds(buf ^ 1);
-            const __amdgpu_buffer_rsrc_t grs = go_rsrc(itn), xrs = xt_rsrc(itn);
+            const TileId itn = tile_id(tn);
             if (wave == kSampler)  // tile t+2 has t's parity
                 load_om(tile_id(min(t + 2, t_last)), om[buf]);
-            colgrad(buf, [&](int s) __attribute__((always_inline)) {
-                if (s & 1) dma16(grs, go_off(itn, s >> 1), gl + (s >> 1) * 1024);
-            });
+            // phase A
+            {
+                const __amdgpu_buffer_rsrc_t grs = go_rsrc(itn);
+                const unsigned gl = go_lds(buf ^ 1);
+                colgrad(buf, [&](int s) __attribute__((always_inline)) {
+                    if (s & 1) dma16(grs, go_off(itn, s >> 1), gl + (s >> 1) * 1024);
+                });
+            }
             uint4 raw[4];
 #pragma unroll
             for (int q = 0; q < 4; ++q) raw[q] = sK[wave][q][lane];
-            if (wave == kSampler) sample(tn, itn, om[buf ^ 1], buf ^ 1);
+            if (wave == kSampler) sample(tn, itn, om[buf ^ 1], d3n);
+            if constexpr (!first)
+                if (wave == kFinisher) finish_sums(d3p, tile_id(t - 1));
             __syncthreads();  // cg partials of both M halves; tile t+1's descriptors
-            consume(buf, buf, raw);
-            __syncthreads();  // sums, columns; the gather buffers are free
-            if (wave == kFinisher) finish_sums(buf, it);
-            const f32x4 goff = gather_offsets(buf ^ 1);
-            gradw(buf, bias_c, [&](int s) __attribute__((always_inline)) {
-                if (s & 1) dma16(xrs, gather_off(s >> 1, goff), k_lds + (s >> 1) * 1024);
+            // phase B
+            {
+                const __amdgpu_buffer_rsrc_t xrs = xt_rsrc(itn);
+                const f32x4 goff = gather_offsets(d3n);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) dma16(xrs, gather_off(q, goff), k_lds + q * 1024);
+            }
+            frag gb[NKS][2];
+            if constexpr (!first) read_bfrags(buf ^ 1, gb);
+            consume(buf, d3, raw, [&](int j) __attribute__((always_inline)) {
+                if constexpr (!first) gradw_mma(ga, gb, j, bias_c);
             });
-            __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the next tile's loads
-            __syncthreads();
+            read_afrags(buf, ga);
+            // The loads of the next tile's gO rows and gathers were issued
+            // before the NST hand-off stores of consume(): waiting until at
+            // most NST memory operations are outstanding waits for all of them
+            // and leaves the stores in flight.
+            __builtin_amdgcn_s_waitcnt(0x0F70 | NST);
+            __syncthreads();  // sums, columns, the next tile's gO rows and gathers
+            d3 = d3n;
         };
-        // pairs of steps with no condition inside; an odd last tile is peeled
-        int t = t_begin;
+        // the first tile peeled, then pairs of steps with no condition inside;
+        // an odd last tile is peeled
+        step(std::integral_constant<int, 0>{}, std::true_type{}, t_begin);
+        int t = t_begin + 1;
         for (; t + 1 < t_end; t += 2) {
-            step(std::integral_constant<int, 0>{}, t);
-            step(std::integral_constant<int, 1>{}, t + 1);
+            step(std::integral_constant<int, 1>{}, std::false_type{}, t);
+            step(std::integral_constant<int, 0>{}, std::false_type{}, t + 1);
         }
-        if (t < t_end) step(std::integral_constant<int, 0>{}, t);
+        if (t < t_end) step(std::integral_constant<int, 1>{}, std::false_type{}, t);
+        // the last tile's grad_offset / grad_mask and grad_weight
+        const int db = d3 == 0 ? 2 : d3 - 1;  // the last tile's descriptors
+        if (wave == kFinisher) finish_sums(db, tile_id(t_last));
+        gradw(ga, (t_last - t_begin) & 1, bias_c);
     };
     if (do_bias) tiles(std::true_type{});
     else tiles(std::false_type{});
