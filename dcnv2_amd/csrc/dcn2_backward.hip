@@ -2156,6 +2156,250 @@ __global__ __launch_bounds__(512) void dcn2_gi_gather_kernel(const BwdParams p) 
 }
 
 // ---------------------------------------------------------------------------
+// grad_input by cells (the default; dcn2_gi_gather_kernel is the per-pixel
+// form).  One block per bucket (image, group, 16x16 cell tile).  For each
+// chunk of KC channels, the window of (TS+1)^2 pixels the tile's corners can
+// reach is accumulated in LDS in fp32, so every hand-off row is read once:
+// the bucket's records are counting-sorted by cell (in batches of up to
+// kGatherBatch; a bucket of one batch is sorted once for all its chunks), and
+// a group of 8 lanes (lane = EPL-channel slice) takes one cell, sums its rows
+// into the cell's four corner sums S_q = sum over the cell's records of
+// (bilinear corner weight q) x (masked column-gradient row), and adds S_q to
+// pixel (cy + q/2, cx + q%2) of the window by a plain read-add-write, with no
+// atomics: wave w takes cell row 2w, then (after a barrier) 2w + 1, 8 cells
+// at a time, so no two waves touch one window row at once, and within the
+// wave the four corners are added one after another (a wave's LDS operations
+// complete in order, so the neighbouring group's add to a shared pixel is
+// seen).  Then interior pixels (reachable from this tile's cells only) are
+// written to gi_acc and the one-pixel border ring, shared with the
+// neighbouring tiles, to the bucket's ring, once each, every entry every call
+// (zeros included), for ring_merge_kernel.  The reference scatters one global
+// atomic per (sample, corner, channel) (com.cu:553-609).
+// Mean samples per bucket from which the host takes dcn2_gi_push_kernel.
+constexpr int kPushMinPerBucket = 1024;
+
+template <typename T>
+__global__ __launch_bounds__(512) void dcn2_gi_push_kernel(const BwdParams p) {
+    constexpr int KC = Mma<T>::KC;  // channels per pass
+    constexpr int TS = kCellTile, TW = TS + 1, NCELL = TS * TS;
+    constexpr int RPT = kGatherBatch / 512;
+    typedef typename RowOf<T>::type R;   // element type of the rows
+    constexpr int EPL = 16 / sizeof(T);  // channels per lane
+    constexpr int LPR = KC / EPL;        // lanes per row (8)
+    constexpr int NLD = EPL * sizeof(R) / 16;  // 16-byte loads per lane per row
+    constexpr int RPB = NLD == 1 ? 8 : 4;      // rows per batch of a lane group
+    constexpr int EU = 16 / sizeof(R);         // channels per 16-byte load
+    constexpr int NPC = EPL / 4;               // 16-byte window pieces per lane
+    static_assert(LPR == 8 && RPB <= LPR && TS == 2 * 8, "8-lane groups; two cell rows per wave");
+    __shared__ int ccnt[NCELL];
+    __shared__ int cstart[NCELL + 1];
+    __shared__ unsigned short sslot[kGatherBatch];  // row in the batch, sorted by cell
+    __shared__ float2 sfrac[kGatherBatch];          // (ly, lx), sorted by cell
+    // window [pixel][KC channels]: the lane's piece h (channels co*EPL + 4h ..)
+    // at 16-byte slot h*LPR + co of its pixel, so the 8 lanes of a group
+    // touch 8 consecutive slots per access
+    __shared__ __attribute__((aligned(16))) float win[TW * TW * KC];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nb = p.B * p.G * p.nty * p.ntx;
+    const int bucket = xcd_remap(blockIdx.x, nb);
+    const int tx = bucket % p.ntx, ty = (bucket / p.ntx) % p.nty;
+    const int bg = bucket / (p.ntx * p.nty), b = bg / p.G, g = bg - b * p.G;
+    const int row0 = p.bstart[bucket], count = p.bstart[bucket + 1] - row0;
+    const int oy = ty * TS - 1, ox = tx * TS - 1;  // pixel of local (0, 0)
+    const int cs = p.G * p.Cgp, cpg = p.Cgp / KC;
+    const int co = lane % LPR, gq = lane / LPR;
+    const int row_bytes = p.Cgp * (int)sizeof(R);
+    const int slice = co * 16 * NLD;
+    auto piece = [&](int pix, int h) __attribute__((always_inline)) {
+        return reinterpret_cast<f32x4 *>(win + pix * KC) + h * LPR + co;
+    };
+    typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+    for (int cc = 0; cc < cpg; ++cc) {
+        if (cc > 0) __syncthreads();  // the previous chunk's window is written out
+        for (int i = tid; i < TW * TW * KC / 4; i += 512)
+            reinterpret_cast<f32x4 *>(win)[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int base = 0; base < count; base += kGatherBatch) {
+            const int nrec = min(count - base, kGatherBatch);
+            __syncthreads();  // the window is clear / the previous batch is done with the LDS arrays
+            if (cc == 0 || count > kGatherBatch) {
+                // 1. counting sort by cell (cell = local row * TS + local column)
+                const int4 *__restrict__ recs = p.rec + (size_t)row0 + base;
+                for (int i = tid; i < NCELL; i += 512) ccnt[i] = 0;
+                __syncthreads();
+                int key[RPT];  // (cell << 16) | rank, or -1
+                float2 fr[RPT];
+#pragma unroll
+                for (int k = 0; k < RPT; ++k) {
+                    const int r = tid + k * 512;
+                    key[k] = -1;
+                    fr[k] = make_float2(0.f, 0.f);
+                    if (r < nrec) {
+                        const int4 rc = recs[r];
+                        const int cy = (int)(short)(rc.y & 0xffff) - oy, cx = (rc.y >> 16) - ox;  // [0, TS)
+                        const int cell = cy * TS + cx;
+                        fr[k] = make_float2(__int_as_float(rc.z), __int_as_float(rc.w));
+                        key[k] = (cell << 16) | atomicAdd(&ccnt[cell], 1);
+                    }
+                }
+                __syncthreads();
+                if (wave == 0) {  // exclusive scan of the 256 counts: 4 per lane + wave scan
+                    int v[4], sc = 0;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        v[i] = ccnt[lane * 4 + i];
+                        sc += v[i];
+                    }
+                    int incl = sc;
+#pragma unroll
+                    for (int d = 1; d < 64; d <<= 1) {
+                        const int o = __shfl_up(incl, d, 64);
+                        if (lane >= d) incl += o;
+                    }
+                    int run = incl - sc;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        cstart[lane * 4 + i] = run;
+                        run += v[i];
+                    }
+                    if (lane == 63) cstart[NCELL] = run;
+                }
+                __syncthreads();
+#pragma unroll
+                for (int k = 0; k < RPT; ++k) {
+                    if (key[k] < 0) continue;
+                    const int pos = cstart[key[k] >> 16] + (key[k] & 0xffff);
+                    sslot[pos] = (unsigned short)(tid + k * 512);
+                    sfrac[pos] = fr[k];
+                }
+                __syncthreads();
+            }
+
+            // 2. the cells.  Rows come in batches of RPB per lane group from
+            //    buffer loads over the batch's rows: a row index past the cell's
+            //    count reads 0 through an out-of-range offset, so no load sits in
+            //    a branch, and the next batch is in flight while one is summed
+            //    (two register sets, the loop unrolled by two).  Lane co of the
+            //    group works out row jb + co (co < RPB); the batch's loads take
+            //    each row's offset and fractions from that lane (ds_swizzle in
+            //    bit mode: lane (l & 0x18) | u of every 32-lane half).
+            const R *rows = (const R *)p.cgm + ((size_t)row0 + base) * p.Cgp + cc * KC;
+            const __amdgpu_buffer_rsrc_t rrs = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<R *>(rows), (short)0, nrec * row_bytes, 0x00020000);
+            for (int r = 0; r < 4; ++r) {  // cell row 2 wave + r / 2, cells 8 (r % 2) ..
+                if (r == 2) __syncthreads();  // the even cell rows' window rows are done
+                const int cy = 2 * wave + (r >> 1), cx = 8 * (r & 1) + gq, cell = cy * TS + cx;
+                const int beg = cstart[cell], tot = cstart[cell + 1] - beg;
+                float S[4][EPL];
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+#pragma unroll
+                    for (int e = 0; e < EPL; ++e) S[q][e] = 0.0f;
+                auto row_info = [&](int jb, int &off, float &ly, float &lx) __attribute__((always_inline)) {
+                    const int j = jb + co;
+                    const bool ok = co < RPB && j < tot;
+                    const int pos = ok ? beg + j : 0;
+                    const float2 f = sfrac[pos];
+                    ly = ok ? f.x : 0.0f;
+                    lx = ok ? f.y : 0.0f;
+                    off = ok ? (int)sslot[pos] * row_bytes : kGatherOutOfRange;
+                };
+                auto fetch = [&](int off, float ly, float lx, u32x4 (&raw)[RPB][NLD], float (&fy)[RPB],
+                                 float (&fx)[RPB]) __attribute__((always_inline)) {
+                    static_for<0, RPB>([&](auto uc) __attribute__((always_inline)) {
+                        constexpr int u = decltype(uc)::value;
+                        const int ou = __builtin_amdgcn_ds_swizzle(off, (u << 5) | 0x18);
+                        fy[u] = __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(ly), (u << 5) | 0x18));
+                        fx[u] = __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(lx), (u << 5) | 0x18));
+                        // row_bytes is a multiple of 128 * NLD (the slice's range)
+                        // and the marker has the low bits set, so OR-ing the slice
+                        // in keeps either in range
+#pragma unroll
+                        for (int h = 0; h < NLD; ++h)
+                            raw[u][h] = __builtin_amdgcn_raw_buffer_load_b128(rrs, ou | (slice + 16 * h), 0, 0);
+                    });
+                };
+                auto accumulate = [&](const u32x4 (&raw)[RPB][NLD], const float (&fy)[RPB],
+                                      const float (&fx)[RPB]) __attribute__((always_inline)) {
+#pragma unroll
+                    for (int u = 0; u < RPB; ++u) {
+                        const float hy = 1.0f - fy[u], hx = 1.0f - fx[u];
+                        const float w[4] = {hy * hx, hy * fx[u], fy[u] * hx, fy[u] * fx[u]};
+#pragma unroll
+                        for (int h = 0; h < NLD; ++h) {
+                            float v[EU];
+                            Unpack<R>::run(make_uint4(raw[u][h].x, raw[u][h].y, raw[u][h].z, raw[u][h].w), v);
+#pragma unroll
+                            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                                for (int e = 0; e < EU; ++e) S[q][h * EU + e] = fmaf(w[q], v[e], S[q][h * EU + e]);
+                        }
+                    }
+                };
+                u32x4 ra[RPB][NLD], rb[RPB][NLD];
+                float ya[RPB], xa[RPB], yb[RPB], xb[RPB];
+                int oa, ob;
+                float la, lb, ma, mb;
+                // (scheduling barriers keep each batch's loads ahead of the sums of
+                // the previous one)
+                row_info(0, oa, la, ma);
+                fetch(oa, la, ma, ra, ya, xa);
+                for (int j0 = 0; j0 < tot; j0 += 2 * RPB) {
+                    row_info(j0 + RPB, ob, lb, mb);
+                    fetch(ob, lb, mb, rb, yb, xb);
+                    __builtin_amdgcn_sched_barrier(0);
+                    accumulate(ra, ya, xa);
+                    __builtin_amdgcn_sched_barrier(0);
+                    row_info(j0 + 2 * RPB, oa, la, ma);
+                    fetch(oa, la, ma, ra, ya, xa);
+                    __builtin_amdgcn_sched_barrier(0);
+                    accumulate(rb, yb, xb);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                // corner q of the group's cell: pixel (cy + q/2, cx + q%2); corner 01
+                // of this group and corner 00 of the next group share a pixel, so the
+                // corners go one after another (the compiler barrier keeps each
+                // corner's reads after the previous corner's writes)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int pix = (cy + (q >> 1)) * TW + cx + (q & 1);
+                    f32x4 t[NPC];
+#pragma unroll
+                    for (int h = 0; h < NPC; ++h) t[h] = *piece(pix, h);
+#pragma unroll
+                    for (int h = 0; h < NPC; ++h) {
+#pragma unroll
+                        for (int k = 0; k < 4; ++k) t[h][k] += S[q][4 * h + k];
+                        *piece(pix, h) = t[h];
+                    }
+                    asm volatile("" ::: "memory");
+                }
+            }
+        }  // batches
+        __syncthreads();
+
+        // 3. the window: interior pixels to gi_acc, the border ring to the
+        //    bucket's ring.  Lane (pixel slot gq, channel slice co).
+        float *__restrict__ gi = p.gi_acc + (size_t)b * p.H * p.W * cs + g * p.Cgp + cc * KC + co * EPL;
+        for (int pl = 8 * wave + gq; pl < TW * TW; pl += 64) {
+            const int py = pl / TW, px = pl - py * TW;
+            const int Y = oy + py, X = ox + px;
+            f32x4 *d4;
+            if (py >= 1 && py <= TS - 1 && px >= 1 && px <= TS - 1) {
+                if (Y >= p.H || X >= p.W) continue;  // (Y, X >= 0 here)
+                d4 = reinterpret_cast<f32x4 *>(gi + ((size_t)Y * p.W + X) * cs);
+            } else {
+                d4 = reinterpret_cast<f32x4 *>(p.ring + ((size_t)bucket * kRing + ring_index(py, px)) * p.Cgp +
+                                               cc * KC + co * EPL);
+            }
+#pragma unroll
+            for (int h = 0; h < NPC; ++h) d4[h] = *piece(pl, h);
+        }
+    }  // channel chunks
+}
+
+// ---------------------------------------------------------------------------
 // Writes the sums of the gather's border-ring partials into gi_acc (the
 // gather writes every other pixel, so gi_acc is never cleared).  The tile-boundary
 // pixels are those with (Y+1) % TS == 0 or (X+1) % TS == 0: the whole rows
@@ -2441,8 +2685,21 @@ static hipError_t backward_t(const Geo &g, const BwdParams &p0, void *grad_input
                 hipDeviceGetAttribute(&lds_cu, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor,
                                       dev) != hipSuccess)
                 lds_cu = 0;
-            const int pad = std::max(0, lds_cu / 3 + 256 - kGatherStaticLds);
-            dcn2_gi_gather_kernel<T><<<g.B * g.G * p.nty * p.ntx, 512, pad, s>>>(p);
+            // By cells (each row read once, one block per CU) when the buckets
+            // are full enough to amortise a block's fixed work; per pixel
+            // otherwise.  DCN2_GI_PUSH=1 / 0 forces either.  Measured: c2 68
+            // against 72 us, c3 ~190 against 282 us (2304 samples per
+            // bucket); c4 (576 per bucket) ~118 against 73 us.
+            const int nbk = g.B * g.G * p.nty * p.ntx;
+            const char *genv = std::getenv("DCN2_GI_PUSH");
+            const long samples = (long)g.B * g.G * g.KK * g.N;
+            const bool push = genv ? genv[0] != '0' : samples >= (long)kPushMinPerBucket * nbk;
+            if (push) {
+                dcn2_gi_push_kernel<T><<<nbk, 512, 0, s>>>(p);
+            } else {
+                const int pad = std::max(0, lds_cu / 3 + 256 - kGatherStaticLds);
+                dcn2_gi_gather_kernel<T><<<nbk, 512, pad, s>>>(p);
+            }
             if ((e = hipGetLastError()) != hipSuccess) return e;
             // the windows' border rings into gi_acc (tile-boundary pixels only)
             const int nrow = g.H / kCellTile, ncol = g.W / kCellTile;

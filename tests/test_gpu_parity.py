@@ -506,3 +506,43 @@ def test_fused_backward(dtype, case):
         for name, g, r in zip(GRADS, grads, rg):
             if g is not None:
                 check(f"{name} ({'fused' if fused else 'two kernels'})", g, r, TOL[dtype])
+
+
+# --------------------------------------------------------------------------- grad_input kernels
+def _with_env(name, value, fn):
+    prev = os.environ.get(name)
+    os.environ[name] = value
+    try:
+        return fn()
+    finally:
+        if prev is None:
+            del os.environ[name]
+        else:
+            os.environ[name] = prev
+
+
+@pytest.mark.parametrize("case", [
+    # C, deformable groups, Cout, H, W, kernel, stride, offset scale, clustered
+    (24, 2, 20, 37, 45, 3, 1, 3.0, False),    # partial edge tiles, two groups, padded channels
+    (128, 1, 32, 33, 20, 3, 2, 4.0, False),   # two channel chunks per group, stride 2
+    (64, 2, 32, 40, 40, 3, 1, 0.0, True),     # one crowded bucket: several record batches
+    (16, 1, 8, 70, 70, 1, 1, 1.0, False),     # many buckets, 1x1 kernel, nearly empty cells
+], ids=["edges_dg2", "two_chunks_s2", "clustered", "sparse_1x1"])
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+def test_grad_input_by_cells_and_by_pixels(dtype, case):
+    """grad_input from the per-cell kernel (rows read once, window summed in
+    LDS) and from the per-pixel kernel (DCN2_GI_PUSH=1 / 0; the host picks by
+    samples per bucket): all five gradients against the oracle for both."""
+    C, G, Cout, H, W, k, st, osc, clustered = case
+    if clustered:
+        w, t = _clustered(dtype, B=1, C=C, H=H, W=W, Cout=Cout, G=G, target=(20.3, 17.6),
+                          spread=3.0, seed=23)
+    else:
+        w, t = _small(dtype, B=2, C=C, H=H, W=W, Cout=Cout, k=k, p=k // 2, s=st, G=G, osc=osc, seed=23)
+    geo = w.geometry()
+    rg = oracle_backward(t, geo)
+    for push in ("1", "0"):
+        grads = _with_env("DCN2_GI_PUSH", push, lambda: gpu_backward(t, geo))
+        torch.cuda.synchronize()
+        for name, g, r in zip(GRADS, grads, rg):
+            check(f"{name} (push={push})", g, r, TOL[dtype])
