@@ -1305,27 +1305,28 @@ __global__ __launch_bounds__(512) void dcn2_gradw_line_kernel(const BwdParams p)
 // accumulated in registers (rows 32w.. in wave w) over all of its tiles and
 // added to the fp32 accumulator once.  Wave w owns K block kb = w%2 (32
 // channels), pixel half P = (w/2)%2 and M half mh = w/4 of the column-gradient
-// GEMM, whose W'^T fragments stay in its registers.  Per tile, with the tile's
-// gO [256][64], its sampling descriptors and each wave's corner gathers
-// already in LDS:
-//   colgrad  partial cg[k][n] = sum over m in half mh of W'^T[k][m] gO[m][n]
-//            for (kb, P) on MFMA -> LDS; between the MFMAs the next tile's gO
-//            rows are loaded straight into the other LDS buffer.  The sampler
-//            wave then writes the next tile's descriptors, a lane per pixel.
-//   consume  lane (pixel px0 + l/4, 8 channels of K block kb) adds the two M
-//            halves' partials, then: corner sums S_q = sum_c cg_c x_c(corner q)
-//            over its channels, reduced over the pixel's 4 lanes -> LDS; the
-//            masked cg row -> the sample's grad_input bucket row; the blended
-//            column -> LDS.
-//   gradw    the finisher wave turns both K blocks' corner sums into
-//            grad_offset / grad_mask (a lane per pixel, as dcn2_colgrad_kernel
-//            does); every wave accumulates gW[m][k] += sum_n gO[m][n] col[k][n]
-//            on MFMA, and between the MFMAs the next tile's corner gathers are
-//            loaded straight into LDS.
-// Everything a tile loads is waited for once, before its last barrier; the
-// sampler's offsets are loaded two tiles ahead.  A gather lane group of 4
-// lanes reads 64 contiguous bytes of one corner, so an instruction touches 16
-// cache lines.
+// GEMM, whose W'^T fragments stay in its registers.  Each tile t takes two
+// phases, with the tile's gO [256][64] and sampling descriptors in LDS and
+// the wave's corner gathers in registers:
+//   A  colgrad: partial cg[k][n] = sum over m in half mh of W'^T[k][m]
+//      gO[m][n] for (kb, P) on MFMA -> LDS; between the MFMAs the next tile's
+//      gO rows are loaded straight into the other LDS buffer.  The sampler
+//      wave writes the next tile's descriptors (a lane per pixel); the
+//      finisher wave turns the previous tile's corner sums into grad_offset /
+//      grad_mask (a lane per pixel, as dcn2_colgrad_kernel does).
+//   B  the next tile's corner gathers are loaded into the other register
+//      set; consume: lane (pixel px0 + l/4, 8 channels of K block kb) adds the
+//      two M halves' partials, then corner sums S_q = sum_c cg_c x_c(corner q)
+//      over its channels, reduced over the pixel's 4 lanes -> LDS; the masked
+//      cg row -> the sample's grad_input bucket row; the blended column ->
+//      LDS.  Between these pieces the wave issues the MFMAs of the previous
+//      tile's gW[m][k] += sum_n gO[m][n] col[k][n], so one wave's VALU runs
+//      beside the other's MFMAs.
+// The gO loads of a tile are waited for once, before its last barrier; the
+// corner gathers and the sampler's offsets are waited for where they are
+// used, a tile after they are issued.  A gather lane group of 4 lanes reads
+// 64 contiguous bytes of one corner, so an instruction touches 16 cache
+// lines.
 //
 // LDS layouts (16-byte pieces XOR-permuted per line so that the transposing
 // 8-byte reads, the 16-byte reads and the 16-byte stores are free of bank
@@ -1339,8 +1340,6 @@ __global__ __launch_bounds__(512) void dcn2_gradw_line_kernel(const BwdParams p)
 //   columns          [64 pixels][64 channels], piece j of pixel n at
 //                    j ^ fused_swz_c(n), read as grad_weight B fragments by
 //                    transposing reads.
-//   corner gathers   per wave [corner q][lane] 16-byte slots: lanes 4i..4i+3
-//                    hold the wave's 32 channels of pixel px0 + i.
 //   cg partials      [M half][block (kb, P)][32 pixels][32 channels + 4].
 __device__ __forceinline__ int fused_swz(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
 __device__ __forceinline__ int fused_swz_cl(int n) { return (((n >> 1) & 1) << 1) | ((n >> 2) & 1); }
@@ -1375,7 +1374,6 @@ void dcn2_bwd_fused_kernel(const BwdParams p) {
     static_assert(KC == 64 && Unpack<T>::E == E && NST * 16 <= kFusedTrashLane, "geometry");
 
     __shared__ __attribute__((aligned(16))) T sG[2][MP * BN];         // gO stage (double)
-    __shared__ __attribute__((aligned(16))) uint4 sK[8][4][64];       // corner gathers per wave
     __shared__ __attribute__((aligned(16))) float sX[2][4][32][LDX];  // cg partials [M half][block]
     __shared__ __attribute__((aligned(16))) T sC[2][BN][KC];          // blended columns (double)
     __shared__ __attribute__((aligned(16))) f32x4 sS[2][BN];          // corner sums per K block
@@ -1587,7 +1585,16 @@ void dcn2_bwd_fused_kernel(const BwdParams p) {
     auto gather_off = [&](int q, const f32x4 &goff) __attribute__((always_inline)) {
         return __float_as_int(goff[q]) * (int)sizeof(T) + gather_lane;
     };
-    const unsigned k_lds = lds_addr(&sK[wave][0][0]);
+    typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+    // the lane's corner gathers of tile t (load q: corner q) into registers
+    auto gather = [&](const __amdgpu_buffer_rsrc_t &xrs, const f32x4 &goff, uint4 (&raw)[4])
+        __attribute__((always_inline)) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(xrs, gather_off(q, goff), 0, 0);
+            raw[q] = make_uint4(v.x, v.y, v.z, v.w);
+        }
+    };
 
     // this lane's kFusedTrashLane bytes of dcn2_trash
     constexpr int kTrashWaves = kTrashBytes / (64 * kFusedTrashLane);
@@ -1803,6 +1810,7 @@ void dcn2_bwd_fused_kernel(const BwdParams p) {
     // is needed.
     auto tiles = [&](auto bias_c) __attribute__((always_inline)) {
         OM om[2];
+        uint4 rawset[2][4];  // corner gathers of the tiles of either parity
         const TileId id0 = tile_id(t_begin);
         if (wave == kSampler) {
             load_om(id0, om[0]);
@@ -1815,8 +1823,7 @@ void dcn2_bwd_fused_kernel(const BwdParams p) {
             const __amdgpu_buffer_rsrc_t grs = go_rsrc(id0), xrs = xt_rsrc(id0);
 #pragma unroll
             for (int q = 0; q < 4; ++q) dma16(grs, go_off(id0, q), go_lds(0) + q * 1024);
-#pragma unroll
-            for (int q = 0; q < 4; ++q) dma16(xrs, gather_off(q, goff), k_lds + q * 1024);
+            gather(xrs, goff, rawset[0]);
         }
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the stage loads
         __syncthreads();
@@ -1839,31 +1846,25 @@ void dcn2_bwd_fused_kernel(const BwdParams p) {
                     if (s & 1) dma16(grs, go_off(itn, s >> 1), gl + (s >> 1) * 1024);
                 });
             }
-            uint4 raw[4];
-#pragma unroll
-            for (int q = 0; q < 4; ++q) raw[q] = sK[wave][q][lane];
             if (wave == kSampler) sample(tn, itn, om[buf ^ 1], d3n);
             if constexpr (!first)
                 if (wave == kFinisher) finish_sums(d3p, tile_id(t - 1));
             __syncthreads();  // cg partials of both M halves; tile t+1's descriptors
             // phase B
-            {
-                const __amdgpu_buffer_rsrc_t xrs = xt_rsrc(itn);
-                const f32x4 goff = gather_offsets(d3n);
-#pragma unroll
-                for (int q = 0; q < 4; ++q) dma16(xrs, gather_off(q, goff), k_lds + q * 1024);
-            }
+            // tile t+1's corner gathers into the other register set: nothing
+            // waits for them before tile t+1's phase B
+            gather(xt_rsrc(itn), gather_offsets(d3n), rawset[buf ^ 1]);
             frag gb[NKS][2];
             if constexpr (!first) read_bfrags(buf ^ 1, gb);
-            consume(buf, d3, raw, [&](int j) __attribute__((always_inline)) {
+            consume(buf, d3, rawset[buf], [&](int j) __attribute__((always_inline)) {
                 if constexpr (!first) gradw_mma(ga, gb, j, bias_c);
             });
             read_afrags(buf, ga);
-            // The loads of the next tile's gO rows and gathers were issued
-            // before the NST hand-off stores of consume(): waiting until at
-            // most NST memory operations are outstanding waits for all of them
-            // and leaves the stores in flight.
-            __builtin_amdgcn_s_waitcnt(0x0F70 | NST);
+            // The next tile's gO rows were loaded in phase A, before its four
+            // corner gathers and the NST hand-off stores of consume():
+            // waiting until at most 4 + NST memory operations are outstanding
+            // waits for the gO rows and leaves the gathers and stores in flight.
+            __builtin_amdgcn_s_waitcnt(0x0F70 | (4 + NST));
             __syncthreads();  // sums, columns, the next tile's gO rows and gathers
             d3 = d3n;
         };
