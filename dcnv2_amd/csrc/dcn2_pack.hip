@@ -10,10 +10,11 @@
 //         row m holds its group's C/WG channels and zeros for all others, so
 //         the GEMMs need no notion of groups.
 //
-// Blocks [0, nin) transpose 64 pixels x CT channels of the input each (CT*esz
-// = 128 bytes, one channel chunk of a pixel); blocks [nin, nin + nw) pack 256
-// weight elements each.  Both halves are independent, so the (small, latency
-// bound) weight packing overlaps the (bandwidth bound) input transpose.
+// Blocks [0, nw) pack 256 16-byte pieces of the weight each; blocks
+// [nw, nw + nin) transpose 64 pixels x CT channels of the input each (CT*esz
+// = 128 bytes, one channel chunk of a pixel); the rest clear accumulators.
+// The halves are independent, so the (small, latency bound) weight packing,
+// dispatched first, overlaps the (bandwidth bound) input transpose.
 #include "dcn2_common.h"
 #include "dcn2_kernels.h"
 #include "../../include/dcnv2_amd.h"
@@ -115,12 +116,16 @@ __device__ __forceinline__ void pack_input_block(const PackParams &p, int blk) {
     }
 }
 
-// One thread per packed weight element.  transpose 0 (forward): MFMA
-// A-fragment order, dst[((rb*nch + ch)*nks + ks)*64 + lane][e] holds
+// One thread per 16-byte piece (EPT = 16/esz consecutive elements) of the
+// packed weight.  transpose 0 (forward): MFMA A-fragment order,
+// dst[((rb*nch + ch)*nks + ks)*64 + lane][e] holds
 // W'[32*rb + lane%32][ch*kc + ks*kstep + (lane/32)*kpl + e], so one wave's
 // fragment load is one contiguous run; transpose 1 (backward): the same for
 // W'^T (rows k, reduction m): dst[((kb*(Mp/kstep) + ms)*64 + lane)][e] holds
-// W'[ms*kstep + (lane/32)*kpl + e][32*kb + lane%32].
+// W'[ms*kstep + (lane/32)*kpl + e][32*kb + lane%32].  For 2-byte types a
+// piece is the kpl = 8 elements e of one lane; for fp32 (kpl = 1) it is
+// 4 consecutive lanes.  All index math is 32-bit (the host bounds Mp*Kp
+// below 2^31).
 // The first nch threads also write the chunk table: for chunk ch of the K
 // order (tap, group, channel chunk of kc channels) tab[ch] = {offset/mask
 // plane g*KK + tap, row term ki*dh, column term kj*dw, channel base
@@ -128,64 +133,77 @@ __device__ __forceinline__ void pack_input_block(const PackParams &p, int blk) {
 // dividing the chunk index every step.
 template <typename T>
 __device__ __forceinline__ void pack_weight_block(const PackParams &p, int blk) {
+    constexpr int EPT = 16 / sizeof(T);
     const T *__restrict__ w = (const T *)p.w;
     T *__restrict__ dst = (T *)p.wp;
-    const long idx = (long)blk * 256 + threadIdx.x;
+    const int t = blk * 256 + threadIdx.x;
     const int nch = p.Kp / p.kc;
-    if (p.tab && idx < nch) {
+    if (p.tab && t < nch) {
         const int cpg = p.Cgp / p.kc;
-        const int tg = (int)idx / cpg, cc = (int)idx - tg * cpg;
+        const int tg = t / cpg, cc = t - tg * cpg;
         const int tap = tg / p.G, g = tg - tap * p.G;
         const int ki = tap / p.kw, kj = tap - ki * p.kw;
-        p.tab[idx] = make_int4(g * p.KK + tap, ki * p.dh, kj * p.dw, g * p.Cgp + cc * p.kc);
+        p.tab[t] = make_int4(g * p.KK + tap, ki * p.dh, kj * p.dw, g * p.Cgp + cc * p.kc);
     }
-    if (idx >= (long)p.Mp * p.Kp) return;
-    int m, k;
+    const int idx0 = t * EPT;
+    if (idx0 >= p.Mp * p.Kp) return;
     const int kpl = p.kpl, kstep = p.kstep;
+    // fragment coordinates of element idx0: e0, lane0 and the fragment index
+    const int e0 = idx0 % kpl;
+    int r = idx0 / kpl;
+    const int lane0 = r % 64;
+    r /= 64;
+    int a = 0, bq = 0;  // transpose 0: (ks, ch, rb); 1: (ms, kb)
+    int ks = 0, ch = 0;
     if (p.transpose) {
         const int nms = p.Mp / kstep;
-        const int e = (int)(idx % kpl);
-        long r = idx / kpl;
-        const int lane = (int)(r % 64);
-        r /= 64;
-        const int ms = (int)(r % nms);
-        const int kb = (int)(r / nms);
-        k = kb * 32 + (lane & 31);
-        m = ms * kstep + (lane >> 5) * kpl + e;
+        a = r % nms;  // ms
+        bq = r / nms; // kb
     } else {
         const int nks = p.kc / kstep;
-        const int e = (int)(idx % kpl);
-        long r = idx / kpl;
-        const int lane = (int)(r % 64);
-        r /= 64;
-        const int ks = (int)(r % nks);
+        ks = r % nks;
         r /= nks;
-        const int ch = (int)(r % nch);
-        const int rb = (int)(r / nch);
-        m = rb * 32 + (lane & 31);
-        k = ch * p.kc + ks * kstep + (lane >> 5) * kpl + e;
+        ch = r % nch;
+        bq = r / nch; // rb
     }
     const int gc = p.G * p.Cgp;
-    const int tap = k / gc, r = k - tap * gc;
-    const int g = r / p.Cgp, c = r - g * p.Cgp;
-    T v = (T)0.0f;
-    // input channel g*Cg + c, as channel cl of row m's weight group
-    const int cl = g * p.Cg + c - (m / p.mpg) * p.Cw;
-    if (m < p.Cout && c < p.Cg && (unsigned)cl < (unsigned)p.Cw)
-        v = w[((size_t)m * p.Cw + cl) * p.KK + tap];
-    dst[idx] = v;
+    T v[EPT];
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+        // element idx0 + j: the next e of the same lane (kpl > 1) or the next lane (kpl == 1)
+        const int e = kpl > 1 ? e0 + j : 0;
+        const int lane = kpl > 1 ? lane0 : lane0 + j;
+        int m, k;
+        if (p.transpose) {
+            k = bq * 32 + (lane & 31);
+            m = a * kstep + (lane >> 5) * kpl + e;
+        } else {
+            m = bq * 32 + (lane & 31);
+            k = ch * p.kc + ks * kstep + (lane >> 5) * kpl + e;
+        }
+        const int tap = k / gc, rr = k - tap * gc;
+        const int g = rr / p.Cgp, c = rr - g * p.Cgp;
+        // input channel g*Cg + c, as channel cl of row m's weight group
+        const int cl = g * p.Cg + c - (m / p.mpg) * p.Cw;
+        v[j] = (m < p.Cout && c < p.Cg && (unsigned)cl < (unsigned)p.Cw)
+                   ? w[((size_t)m * p.Cw + cl) * p.KK + tap]
+                   : (T)0.0f;
+    }
+    *reinterpret_cast<uint4 *>(dst + idx0) = __builtin_bit_cast(uint4, v);
 }
 
 template <typename T>
 __global__ __launch_bounds__(256) void pack_kernel(const PackParams p) {
+    // weight blocks first: they are latency bound, so they are dispatched
+    // ahead of (and overlap) the bandwidth-bound input transpose
     const int blk = blockIdx.x;
-    if (blk < p.nin) {
+    if (blk < p.nw) {
+        pack_weight_block<T>(p, blk);
+    } else if (blk < p.nw + p.nin) {
         if (p.nhwc)
-            pack_input_block_nhwc<T>(p, blk);
+            pack_input_block_nhwc<T>(p, blk - p.nw);
         else
-            pack_input_block<T>(p, blk);
-    } else if (blk < p.nin + p.nw) {
-        pack_weight_block<T>(p, blk - p.nin);
+            pack_input_block<T>(p, blk - p.nw);
     } else {
         // zero kClearPieces 16-byte pieces of one of the clear-list buffers
         const int cb = blk - p.nin - p.nw;
@@ -231,7 +249,8 @@ static hipError_t pack_t(const Geo &g, const void *input, void *xt, const void *
     p.Kp = g.Kp;
     p.transpose = transpose ? 1 : 0;
     p.nhwc = g.nhwc;
-    const long nw = ((long)g.Mp * g.Kp + 255) / 256;
+    // one thread per 16-byte piece of the packed weight (Mp*Kp is a multiple of 16/esz)
+    const long nw = ((long)g.Mp * g.Kp / E + 255) / 256;
     p.nw = (int)nw;
     p.clr_blk[0] = 0;
     for (int i = 0; i < 3; ++i) {
