@@ -174,13 +174,13 @@ BwdWorkspace bwd_workspace(const Geo &g) {
     o += align256((size_t)g.Mp * g.Kp * g.esz);
     w.tab = o;
     o += align256((size_t)(g.Kp / g.KC) * 16);
-    w.gi_acc = o;
-    o += align256((size_t)g.B * g.H * g.W * g.cs * sizeof(float));
+    const GatherGeo gg = gather_geometry(g);
+    w.gi_acc = o;  // (the by-cells grad_input writes the caller's buffer directly)
+    if (!gg.by_cells) o += align256((size_t)g.B * g.H * g.W * g.cs * sizeof(float));
     w.gw_acc = o;
     o += align256((size_t)g.Mp * g.Kp * sizeof(float));
     w.gb_acc = o;
     o += align256((size_t)g.Mp * sizeof(float));
-    const GatherGeo gg = gather_geometry(g);
     w.cgm = o;
     o += align256((size_t)gg.rows * g.Cgp * gg.row_esz);
     w.rec = o;

@@ -59,6 +59,13 @@ struct BwdParams {
     int *sidx;          // [B][G*KK][N] bucket row of each sample; -1 no corner inside
     int ntx, nty;       // cell tiles per row / column
     float *ring;        // [nbuckets][kRing][Cgp] grad_input sums of each window's border ring
+    // grad_input written directly by the per-cell kernel and ring_final_kernel
+    // (no fp32 accumulator): the caller's buffer, whether it is channels-last
+    // [B][H][W][C] (else [B][C][H][W]), and whether 8-element runs take vector
+    // stores there (NCHW: W % 8 == 0; channels-last: C and C/G multiples of
+    // 8; both with a 16-byte aligned base)
+    void *gi_out;
+    int gi_nhwc, gi_vec;
     // offset / mask (and grad_offset / grad_mask) elements between images, and
     // whether the mask buffer holds logits (see mask_value; grad_mask is then
     // the gradient of the logits)
@@ -71,6 +78,17 @@ struct BwdParams {
     // weight are zero and their grad_weight is not kept).
     int gw_nch, gw_cpt, gw_cpw, gw_cog;
 };
+
+// Eight consecutive elements as 16-byte stores (dst 16-byte aligned).
+template <typename T> __device__ __forceinline__ void store8(T *dst, const T (&v)[8]) {
+    if constexpr (sizeof(T) == 2) {
+        *reinterpret_cast<uint4 *>(dst) = __builtin_bit_cast(uint4, v);
+    } else {
+        uint4 *d = reinterpret_cast<uint4 *>(dst);
+        d[0] = make_uint4(__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3]));
+        d[1] = make_uint4(__float_as_uint(v[4]), __float_as_uint(v[5]), __float_as_uint(v[6]), __float_as_uint(v[7]));
+    }
+}
 
 // Packed chunk index of the j-th grad_weight chunk of the M chunk at row m0.
 __device__ __forceinline__ int gw_chunk(const BwdParams &p, int j, int m0) {
@@ -2288,80 +2306,82 @@ __global__ __launch_bounds__(512) void dcn2_gi_push_kernel(const BwdParams p) {
             const R *rows = (const R *)p.cgm + ((size_t)row0 + base) * p.Cgp + cc * KC;
             const __amdgpu_buffer_rsrc_t rrs = __builtin_amdgcn_make_buffer_rsrc(
                 const_cast<R *>(rows), (short)0, nrec * row_bytes, 0x00020000);
-            for (int r = 0; r < 4; ++r) {  // cell row 2 wave + r / 2, cells 8 (r % 2) ..
-                if (r == 2) __syncthreads();  // the even cell rows' window rows are done
-                const int cy = 2 * wave + (r >> 1), cx = 8 * (r & 1) + gq, cell = cy * TS + cx;
-                const int beg = cstart[cell], tot = cstart[cell + 1] - beg;
-                float S[4][EPL];
+            // The group's four cells (round r: cell row 2 wave + r / 2, cells
+            // 8 (r % 2) ..) form one stream of row batches: every round takes
+            // the wave's largest cell in ceil(max / RPB) batches (at least one,
+            // so every round reaches its window adds and round 1 its barrier),
+            // and the batch after the one being summed is always in flight,
+            // also across a round's window adds and the barrier (which waits
+            // for LDS operations only).  So a wave's rounds do not each wait
+            // for a round trip to memory.
+            int rbeg[4], rtot[4], nbat[4];
 #pragma unroll
-                for (int q = 0; q < 4; ++q)
+            for (int r = 0; r < 4; ++r) {
+                const int cell = (2 * wave + (r >> 1)) * TS + 8 * (r & 1) + gq;
+                rbeg[r] = cstart[cell];
+                rtot[r] = cstart[cell + 1] - rbeg[r];
+                int tmax = rtot[r];
 #pragma unroll
-                    for (int e = 0; e < EPL; ++e) S[q][e] = 0.0f;
-                auto row_info = [&](int jb, int &off, float &ly, float &lx) __attribute__((always_inline)) {
-                    const int j = jb + co;
-                    const bool ok = co < RPB && j < tot;
-                    const int pos = ok ? beg + j : 0;
-                    const float2 f = sfrac[pos];
-                    ly = ok ? f.x : 0.0f;
-                    lx = ok ? f.y : 0.0f;
-                    off = ok ? (int)sslot[pos] * row_bytes : kGatherOutOfRange;
-                };
-                auto fetch = [&](int off, float ly, float lx, u32x4 (&raw)[RPB][NLD], float (&fy)[RPB],
-                                 float (&fx)[RPB]) __attribute__((always_inline)) {
-                    static_for<0, RPB>([&](auto uc) __attribute__((always_inline)) {
-                        constexpr int u = decltype(uc)::value;
-                        const int ou = __builtin_amdgcn_ds_swizzle(off, (u << 5) | 0x18);
-                        fy[u] = __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(ly), (u << 5) | 0x18));
-                        fx[u] = __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(lx), (u << 5) | 0x18));
-                        // row_bytes is a multiple of 128 * NLD (the slice's range)
-                        // and the marker has the low bits set, so OR-ing the slice
-                        // in keeps either in range
+                for (int d = 8; d < 64; d <<= 1) tmax = max(tmax, __shfl_xor(tmax, d, 64));
+                nbat[r] = max(1, (tmax + RPB - 1) / RPB);  // wave-uniform
+            }
+            const int nstream = nbat[0] + nbat[1] + nbat[2] + nbat[3];
+            auto pick = [](const int (&a)[4], int r) __attribute__((always_inline)) {
+                return r == 0 ? a[0] : (r == 1 ? a[1] : (r == 2 ? a[2] : a[3]));
+            };
+            // batch jb of round r: the row offset, fractions of row jb*RPB + co
+            auto row_info = [&](int r, int jb, int &off, float &ly, float &lx) __attribute__((always_inline)) {
+                const int j = jb * RPB + co;
+                const bool ok = co < RPB && j < pick(rtot, r);
+                const int pos = ok ? pick(rbeg, r) + j : 0;
+                const float2 f = sfrac[pos];
+                ly = ok ? f.x : 0.0f;
+                lx = ok ? f.y : 0.0f;
+                off = ok ? (int)sslot[pos] * row_bytes : kGatherOutOfRange;
+            };
+            auto fetch = [&](int off, float ly, float lx, u32x4 (&raw)[RPB][NLD], float (&fy)[RPB],
+                             float (&fx)[RPB]) __attribute__((always_inline)) {
+                static_for<0, RPB>([&](auto uc) __attribute__((always_inline)) {
+                    constexpr int u = decltype(uc)::value;
+                    const int ou = __builtin_amdgcn_ds_swizzle(off, (u << 5) | 0x18);
+                    fy[u] = __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(ly), (u << 5) | 0x18));
+                    fx[u] = __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(lx), (u << 5) | 0x18));
+                    // row_bytes is a multiple of 128 * NLD (the slice's range)
+                    // and the marker has the low bits set, so OR-ing the slice
+                    // in keeps either in range
 #pragma unroll
-                        for (int h = 0; h < NLD; ++h)
-                            raw[u][h] = __builtin_amdgcn_raw_buffer_load_b128(rrs, ou | (slice + 16 * h), 0, 0);
-                    });
-                };
-                auto accumulate = [&](const u32x4 (&raw)[RPB][NLD], const float (&fy)[RPB],
-                                      const float (&fx)[RPB]) __attribute__((always_inline)) {
+                    for (int h = 0; h < NLD; ++h)
+                        raw[u][h] = __builtin_amdgcn_raw_buffer_load_b128(rrs, ou | (slice + 16 * h), 0, 0);
+                });
+            };
+            float S[4][EPL];
 #pragma unroll
-                    for (int u = 0; u < RPB; ++u) {
-                        const float hy = 1.0f - fy[u], hx = 1.0f - fx[u];
-                        const float w[4] = {hy * hx, hy * fx[u], fy[u] * hx, fy[u] * fx[u]};
+            for (int q = 0; q < 4; ++q)
 #pragma unroll
-                        for (int h = 0; h < NLD; ++h) {
-                            float v[EU];
-                            Unpack<R>::run(make_uint4(raw[u][h].x, raw[u][h].y, raw[u][h].z, raw[u][h].w), v);
+                for (int e = 0; e < EPL; ++e) S[q][e] = 0.0f;
+            auto accumulate = [&](const u32x4 (&raw)[RPB][NLD], const float (&fy)[RPB],
+                                  const float (&fx)[RPB]) __attribute__((always_inline)) {
 #pragma unroll
-                            for (int q = 0; q < 4; ++q)
+                for (int u = 0; u < RPB; ++u) {
+                    const float hy = 1.0f - fy[u], hx = 1.0f - fx[u];
+                    const float w[4] = {hy * hx, hy * fx[u], fy[u] * hx, fy[u] * fx[u]};
 #pragma unroll
-                                for (int e = 0; e < EU; ++e) S[q][h * EU + e] = fmaf(w[q], v[e], S[q][h * EU + e]);
-                        }
+                    for (int h = 0; h < NLD; ++h) {
+                        float v[EU];
+                        Unpack<R>::run(make_uint4(raw[u][h].x, raw[u][h].y, raw[u][h].z, raw[u][h].w), v);
+#pragma unroll
+                        for (int q = 0; q < 4; ++q)
+#pragma unroll
+                            for (int e = 0; e < EU; ++e) S[q][h * EU + e] = fmaf(w[q], v[e], S[q][h * EU + e]);
                     }
-                };
-                u32x4 ra[RPB][NLD], rb[RPB][NLD];
-                float ya[RPB], xa[RPB], yb[RPB], xb[RPB];
-                int oa, ob;
-                float la, lb, ma, mb;
-                // (scheduling barriers keep each batch's loads ahead of the sums of
-                // the previous one)
-                row_info(0, oa, la, ma);
-                fetch(oa, la, ma, ra, ya, xa);
-                for (int j0 = 0; j0 < tot; j0 += 2 * RPB) {
-                    row_info(j0 + RPB, ob, lb, mb);
-                    fetch(ob, lb, mb, rb, yb, xb);
-                    __builtin_amdgcn_sched_barrier(0);
-                    accumulate(ra, ya, xa);
-                    __builtin_amdgcn_sched_barrier(0);
-                    row_info(j0 + 2 * RPB, oa, la, ma);
-                    fetch(oa, la, ma, ra, ya, xa);
-                    __builtin_amdgcn_sched_barrier(0);
-                    accumulate(rb, yb, xb);
-                    __builtin_amdgcn_sched_barrier(0);
                 }
-                // corner q of the group's cell: pixel (cy + q/2, cx + q%2); corner 01
-                // of this group and corner 00 of the next group share a pixel, so the
-                // corners go one after another (the compiler barrier keeps each
-                // corner's reads after the previous corner's writes)
+            };
+            // corner q of the group's cell of round r: pixel (cy + q/2, cx + q%2);
+            // corner 01 of this group and corner 00 of the next group share a
+            // pixel, so the corners go one after another (the compiler barrier
+            // keeps each corner's reads after the previous corner's writes)
+            auto window_add = [&](int r) __attribute__((always_inline)) {
+                const int cy = 2 * wave + (r >> 1), cx = 8 * (r & 1) + gq;
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     const int pix = (cy + (q >> 1)) * TW + cx + (q & 1);
@@ -2371,17 +2391,131 @@ __global__ __launch_bounds__(512) void dcn2_gi_push_kernel(const BwdParams p) {
 #pragma unroll
                     for (int h = 0; h < NPC; ++h) {
 #pragma unroll
-                        for (int k = 0; k < 4; ++k) t[h][k] += S[q][4 * h + k];
+                        for (int k = 0; k < 4; ++k) {
+                            t[h][k] += S[q][4 * h + k];
+                            S[q][4 * h + k] = 0.0f;
+                        }
                         *piece(pix, h) = t[h];
                     }
                     asm volatile("" ::: "memory");
                 }
+            };
+            // stream cursors (wave-uniform): fetch point (fr, fj), sum point (cr, cj)
+            int fr = 0, fj = 0, cr = 0, cj = 0;
+            auto fetch_next = [&](u32x4 (&raw)[RPB][NLD], float (&fy)[RPB], float (&fx)[RPB])
+                __attribute__((always_inline)) {
+                if (fr < 4) {
+                    int off;
+                    float ly, lx;
+                    row_info(fr, fj, off, ly, lx);
+                    fetch(off, ly, lx, raw, fy, fx);
+                    if (++fj == pick(nbat, fr)) {
+                        ++fr;
+                        fj = 0;
+                    }
+                }
+            };
+            // after summing batch (cr, cj): at a round's end, its window adds;
+            // after round 1, the barrier between the even and the odd cell rows
+            auto sum_done = [&]() __attribute__((always_inline)) {
+                if (++cj == pick(nbat, cr)) {
+                    window_add(cr);
+                    if (cr == 1) __syncthreads();  // the even cell rows' window rows are done
+                    ++cr;
+                    cj = 0;
+                }
+            };
+            u32x4 ra[RPB][NLD], rb[RPB][NLD];
+            float ya[RPB], xa[RPB], yb[RPB], xb[RPB];
+            // (scheduling barriers keep each batch's loads ahead of the sums of
+            // the previous one)
+            fetch_next(ra, ya, xa);
+            for (int sidx = 0; sidx < nstream; sidx += 2) {
+                fetch_next(rb, yb, xb);
+                __builtin_amdgcn_sched_barrier(0);
+                accumulate(ra, ya, xa);
+                sum_done();
+                __builtin_amdgcn_sched_barrier(0);
+                if (sidx + 1 >= nstream) break;
+                fetch_next(ra, ya, xa);
+                __builtin_amdgcn_sched_barrier(0);
+                accumulate(rb, yb, xb);
+                sum_done();
+                __builtin_amdgcn_sched_barrier(0);
             }
         }  // batches
         __syncthreads();
 
-        // 3. the window: interior pixels to gi_acc, the border ring to the
-        //    bucket's ring.  Lane (pixel slot gq, channel slice co).
+        // 3. the window: the border ring to the bucket's ring (for
+        //    ring_final_kernel / ring_merge_kernel); then either the interior
+        //    pixels to gi_acc (lane: pixel slot gq, channel slice co) or, with
+        //    gi_out, the tile's pixels (16ty .. +15, 16tx .. +15) = window
+        //    (1 .. TS, 1 .. TS) straight to grad_input in the caller's type
+        //    and layout.  Of those, the pixels on row or column TS are
+        //    partial sums here; ring_final_kernel, launched after this kernel,
+        //    overwrites every such (tile-boundary) pixel with the full sum.
+        if (p.gi_out) {
+            for (int pl = 8 * wave + gq; pl < TW * TW; pl += 64) {
+                const int py = pl / TW, px = pl - py * TW;
+                if (py >= 1 && py <= TS - 1 && px >= 1 && px <= TS - 1) continue;
+                f32x4 *d4 = reinterpret_cast<f32x4 *>(
+                    p.ring + ((size_t)bucket * kRing + ring_index(py, px)) * p.Cgp + cc * KC + co * EPL);
+#pragma unroll
+                for (int h = 0; h < NPC; ++h) d4[h] = *piece(pl, h);
+            }
+            // window value of channel cl (of this chunk) at pixel slot pix: cl =
+            // co * EPL + 4h + k lives at 16-byte slot h * LPR + co, element k
+            auto win_at = [&](int pix, int cl) __attribute__((always_inline)) {
+                const int c_o = cl / EPL, rem = cl - c_o * EPL;
+                return win[pix * KC + ((rem >> 2) * LPR + c_o) * 4 + (rem & 3)];
+            };
+            T *const gout = (T *)p.gi_out;
+            const int C = p.G * p.Cg;
+            if (p.gi_nhwc) {
+                // item: pixel (yy, xx) of the tile, 8 channels 8j ..
+                constexpr int NPP = KC / 8;
+                for (int it = tid; it < TS * TS * NPP; it += 512) {
+                    const int j = it % NPP, pl = it / NPP;
+                    const int yy = pl / TS, xx = pl - yy * TS;
+                    const int Y = ty * TS + yy, X = tx * TS + xx, c0 = cc * KC + 8 * j;
+                    if (Y >= p.H || X >= p.W || c0 >= p.Cg) continue;
+                    const int pix = (yy + 1) * TW + xx + 1;
+                    T v[8];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) v[e] = from_f32<T>(win_at(pix, 8 * j + e));
+                    T *dst = gout + (((size_t)b * p.H + Y) * p.W + X) * C + g * p.Cg + c0;
+                    if (p.gi_vec && c0 + 8 <= p.Cg) {
+                        store8(dst, v);
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 8; ++e)
+                            if (c0 + e < p.Cg) dst[e] = v[e];
+                    }
+                }
+            } else {
+                // item: channel cl (consecutive lanes: consecutive channels),
+                // row yy of the tile, pixels 8hx .. 8hx + 7
+                for (int it = tid; it < KC * TS * 2; it += 512) {
+                    const int cl = it % KC, r2 = it / KC;
+                    const int yy = r2 >> 1, hx = r2 & 1;
+                    const int Y = ty * TS + yy, X0 = tx * TS + 8 * hx, cg = cc * KC + cl;
+                    if (Y >= p.H || X0 >= p.W || cg >= p.Cg) continue;
+                    const int pix = (yy + 1) * TW + 8 * hx + 1;
+                    T v[8];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) v[e] = from_f32<T>(win_at(pix + e, cl));
+                    T *dst = gout + (((size_t)b * C + g * p.Cg + cg) * p.H + Y) * p.W + X0;
+                    if (p.gi_vec && X0 + 8 <= p.W) {
+                        store8(dst, v);
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 8; ++e)
+                            if (X0 + e < p.W) dst[e] = v[e];
+                    }
+                }
+            }
+            continue;  // (the chunk loop's barrier orders these reads before the next clear)
+        }
         float *__restrict__ gi = p.gi_acc + (size_t)b * p.H * p.W * cs + g * p.Cgp + cc * KC + co * EPL;
         for (int pl = 8 * wave + gq; pl < TW * TW; pl += 64) {
             const int py = pl / TW, px = pl - py * TW;
@@ -2463,11 +2597,13 @@ template <typename T>
 __device__ __forceinline__ void finalize_gw_block(const GwFinal<T> &f, long blk) {
     // grad_weight [Cout][Cw][KK]: row m's channel cl is input channel
     // (m / mpg) * Cw + cl, the diagonal block of the block-diagonal W'.
-    const long idx = blk * 256 + threadIdx.x;
-    const long total = (long)f.Cout * f.Cw * f.KK;
+    // (32-bit index math: the host bounds Mp * Kp, and so Cout * Cw * KK,
+    // below 2^31)
+    const int idx = (int)blk * 256 + (int)threadIdx.x;
+    const int total = f.Cout * f.Cw * f.KK;
     if (idx < total) {
-        const int m = (int)(idx / ((long)f.Cw * f.KK));
-        const int r = (int)(idx - (long)m * f.Cw * f.KK);
+        const int m = idx / (f.Cw * f.KK);
+        const int r = idx - m * f.Cw * f.KK;
         const int cl = r / f.KK, tap = r - cl * f.KK;
         const int c = (m / f.mpg) * f.Cw + cl;
         const int g = c / f.Cg, ci = c - g * f.Cg;
@@ -2478,6 +2614,131 @@ __device__ __forceinline__ void finalize_gw_block(const GwFinal<T> &f, long blk)
 template <typename T>
 __global__ __launch_bounds__(256) void finalize_gw_kernel(const GwFinal<T> f) {
     finalize_gw_block(f, blockIdx.x);
+}
+
+// The tile-boundary pixels of a directly written grad_input (see
+// dcn2_gi_push_kernel with gi_out): the sums of the border rings that hold
+// each pixel, written in the caller's type and layout over the per-tile
+// partial value the per-cell kernel left there.  Pixel (Y, X) is a boundary
+// pixel when Y % TS == TS-1 (a boundary row) or X % TS == TS-1 (a boundary
+// column); it is (py, px) = ((Y+1) % TS, (X+1) % TS) of the window of tile
+// ((Y+1) / TS, (X+1) / TS), and also row TS of the tile above when py == 0
+// and column TS of the tile to the left when px == 0.  One launch, 256
+// threads per block, three block ranges:
+//   [0, nb_rows)  NCHW boundary rows: 64 pixels x 32 padded channels per
+//                 block, ring sums -> LDS -> 16-byte stores of 8 pixels of
+//                 one channel (stores along pixels, as the rows are
+//                 contiguous in NCHW);
+//   then          the other boundary pixels (all of them for channels-last),
+//                 one thread per pixel and 4 padded channels;
+//   then          grad_weight / grad_bias (their accumulators are complete
+//                 when this kernel runs).
+struct RingFinal {
+    int nrow, ncol;       // boundary rows and columns of an image
+    int xblk, cblk;       // NCHW row part: 64-pixel blocks per row, 32-channel blocks
+    long nb_rows;         // blocks of the NCHW row part
+    long items;           // items of the per-thread part
+    long nb_items;        // its blocks
+};
+__device__ __forceinline__ f32x4 ring_sum(const BwdParams &p, int b, int g, int ci, int Y, int X) {
+    constexpr int TS = kCellTile;
+    const int py = (Y + 1) % TS, ty = (Y + 1) / TS, px = (X + 1) % TS, tx = (X + 1) / TS;
+    f32x4 v = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        if (i == 1 && (py != 0 || ty == 0)) continue;
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) {
+            if (jj == 1 && (px != 0 || tx == 0)) continue;
+            const long bucket = (((long)b * p.G + g) * p.nty + (ty - i)) * p.ntx + (tx - jj);
+            v += *reinterpret_cast<const f32x4 *>(
+                p.ring + (bucket * kRing + ring_index(i ? TS : py, jj ? TS : px)) * p.Cgp + ci);
+        }
+    }
+    return v;
+}
+template <typename T>
+__global__ __launch_bounds__(256) void ring_final_kernel(const BwdParams p, const RingFinal r,
+                                                         const GwFinal<T> f) {
+    constexpr int TS = kCellTile;
+    const int H = p.H, W = p.W, Cgp = p.Cgp, cs = p.G * p.Cgp, q4 = cs / 4;
+    const int C = p.G * p.Cg;
+    T *const gout = (T *)p.gi_out;
+    const long blk = blockIdx.x;
+    if (blk < r.nb_rows) {
+        __shared__ float tile[64][33];
+        const int xb = (int)(blk % r.xblk);
+        long rest = blk / r.xblk;
+        const int cb = (int)(rest % r.cblk);
+        rest /= r.cblk;
+        const int k = (int)(rest % r.nrow), b = (int)(rest / r.nrow);
+        const int Y = TS * k + TS - 1, X0 = xb * 64, cp0 = cb * 32;
+        const int tid = threadIdx.x;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int pl = (tid >> 3) + 32 * i, c4 = (tid & 7) * 4;
+            const int X = X0 + pl, cp = cp0 + c4, g = cp / Cgp, ci = cp - g * Cgp;
+            const f32x4 v = X < W ? ring_sum(p, b, g, ci, Y, X) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) tile[pl][c4 + e] = v[e];
+        }
+        __syncthreads();
+        const int cl = tid >> 3, p8 = (tid & 7) * 8;
+        const int cp = cp0 + cl, g = cp / Cgp, ci = cp - g * Cgp;
+        const int X = X0 + p8;
+        if (ci >= p.Cg || X >= W) return;
+        T v[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = from_f32<T>(tile[p8 + e][cl]);
+        T *dst = gout + (((size_t)b * C + g * p.Cg + ci) * H + Y) * W + X;
+        if (p.gi_vec && X + 8 <= W) {
+            store8(dst, v);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                if (X + e < W) dst[e] = v[e];
+        }
+        return;
+    }
+    if (blk < r.nb_rows + r.nb_items) {
+        const long item = (blk - r.nb_rows) * 256 + threadIdx.x;
+        if (item >= r.items) return;
+        // pixels: (NHWC only) the boundary rows, then the boundary columns
+        // outside the boundary rows, image by image
+        const long k0 = item / q4;
+        const int cp = (int)(item - k0 * q4) * 4;
+        const long rows_px = p.gi_nhwc ? (long)r.nrow * W : 0;
+        const long per_img = rows_px + (long)(H - r.nrow) * r.ncol;
+        const int b = (int)(k0 / per_img);
+        const long k = k0 - (long)b * per_img;
+        int Y, X;
+        if (k < rows_px) {
+            Y = TS * (int)(k / W) + TS - 1;
+            X = (int)(k % W);
+        } else {
+            const long k2 = k - rows_px;
+            const int c = (int)(k2 / (H - r.nrow)), j = (int)(k2 % (H - r.nrow));
+            Y = j + j / (TS - 1);  // the j-th row that is not a boundary row
+            X = TS * c + TS - 1;
+        }
+        const int g = cp / Cgp, ci = cp - g * Cgp;
+        if (ci >= p.Cg) return;  // padding channels only
+        const f32x4 v = ring_sum(p, b, g, ci, Y, X);
+        if (p.gi_nhwc) {
+            T *dst = gout + (((size_t)b * H + Y) * W + X) * C + g * p.Cg + ci;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (ci + e < p.Cg) dst[e] = from_f32<T>(v[e]);
+        } else {
+            T *dst = gout + (((size_t)b * C + g * p.Cg + ci) * H + Y) * W + X;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (ci + e < p.Cg) dst[(size_t)e * H * W] = from_f32<T>(v[e]);
+        }
+        return;
+    }
+    const long gb = blk - r.nb_rows - r.nb_items;
+    if (gb < f.nblk) finalize_gw_block(f, gb);
 }
 
 // gi_acc [B][HW][cs] fp32 -> grad_input [B][C][HW] T; 64 pixels x 32 padded
@@ -2675,46 +2936,8 @@ static hipError_t backward_t(const Geo &g, const BwdParams &p0, void *grad_input
             if ((e = hipGetLastError()) != hipSuccess) return e;
         }
         prof_end(DCN2_STAGE_BWD_COLGRAD, s);
-        prof_begin(DCN2_STAGE_BWD_GATHER, s);
-        {
-            // At most two workgroups per CU (extra LDS reserved at launch): each
-            // bucket's rows are read once per corner, and with three buckets per
-            // CU the rows in use no longer fit an XCD's L2 (measured at c2:
-            // 138 us at three per CU, 113 us at two, 119 us at one).
-            int dev = 0, lds_cu = 0;
-            if (hipGetDevice(&dev) != hipSuccess ||
-                hipDeviceGetAttribute(&lds_cu, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor,
-                                      dev) != hipSuccess)
-                lds_cu = 0;
-            // By cells (each row read once, one block per CU) when the buckets
-            // are full enough to amortise a block's fixed work; per pixel
-            // otherwise.  DCN2_GI_PUSH=1 / 0 forces either.  Measured: c2 68
-            // against 72 us, c3 ~190 against 282 us (2304 samples per
-            // bucket); c4 (576 per bucket) ~118 against 73 us.
-            const int nbk = g.B * g.G * p.nty * p.ntx;
-            const char *genv = std::getenv("DCN2_GI_PUSH");
-            const long samples = (long)g.B * g.G * g.KK * g.N;
-            const bool push = genv ? genv[0] != '0' : samples >= (long)kPushMinPerBucket * nbk;
-            if (push) {
-                dcn2_gi_push_kernel<T><<<nbk, 512, 0, s>>>(p);
-            } else {
-                const int pad = std::max(0, lds_cu / 3 + 256 - kGatherStaticLds);
-                dcn2_gi_gather_kernel<T><<<nbk, 512, pad, s>>>(p);
-            }
-            if ((e = hipGetLastError()) != hipSuccess) return e;
-            // the windows' border rings into gi_acc (tile-boundary pixels only)
-            const int nrow = g.H / kCellTile, ncol = g.W / kCellTile;
-            const long items = ((long)nrow * g.W + (long)(g.H - nrow) * ncol) * (g.cs / 4);
-            if (items > 0) {
-                dim3 rgrid((unsigned)((items + 255) / 256), g.B);
-                ring_merge_kernel<<<rgrid, 256, 0, s>>>(p.gi_acc, p.ring, g.H, g.W, g.cs, g.Cgp, g.G,
-                                                        p.nty, p.ntx, nrow, ncol);
-            }
-        }
-        if ((e = hipGetLastError()) != hipSuccess) return e;
-        prof_end(DCN2_STAGE_BWD_GATHER, s);
-        // 3. grad_weight / grad_bias
-        if (!fused) {
+        // 3. grad_weight / grad_bias of the two-kernel path
+        auto run_gradw = [&]() -> hipError_t {
             prof_begin(DCN2_STAGE_BWD_GRADW, s);
             // weight groups split per group (Geo::gsplit): an M chunk must lie
             // in one group, whose rows are a multiple of 128
@@ -2753,12 +2976,64 @@ static hipError_t backward_t(const Geo &g, const BwdParams &p0, void *grad_input
             if (!line) DCN2_GRADW_MB(dcn2_gradw_kernel);
 #undef DCN2_GRADW_MB
 #undef DCN2_GRADW
-            if ((e = hipGetLastError()) != hipSuccess) return e;
+            const hipError_t ge = hipGetLastError();
             prof_end(DCN2_STAGE_BWD_GRADW, s);
-        }
-        // 4. grad_input to the caller's layout
-        prof_begin(DCN2_STAGE_BWD_FINAL, s);
-        {
+            return ge;
+        };
+        const GatherGeo gg = gather_geometry(g);
+        const int nbk = (int)gg.nbuckets;
+        const int nrow = g.H / kCellTile, ncol = g.W / kCellTile;
+        const long ring_items = ((long)nrow * g.W + (long)(g.H - nrow) * ncol) * (g.cs / 4);
+        if (gg.by_cells) {
+            // grad_weight first (when not fused), so that its finalisation can
+            // ride in the last launch, ring_final_kernel
+            if (!fused && (e = run_gradw()) != hipSuccess) return e;
+            prof_begin(DCN2_STAGE_BWD_GATHER, s);
+            p.gi_out = grad_input;
+            p.gi_nhwc = g.nhwc;
+            const int align16 = ((uintptr_t)grad_input & 15) == 0;
+            p.gi_vec = align16 && (g.nhwc ? g.C % 8 == 0 && g.Cg % 8 == 0 : g.W % 8 == 0);
+            dcn2_gi_push_kernel<T><<<nbk, 512, 0, s>>>(p);
+            if ((e = hipGetLastError()) != hipSuccess) return e;
+            // the tile-boundary pixels from the border rings, and grad_weight /
+            // grad_bias (see ring_final_kernel)
+            RingFinal rf;
+            rf.nrow = nrow;
+            rf.ncol = ncol;
+            rf.xblk = ceil_div(g.W, 64);
+            rf.cblk = g.cs / 32;
+            rf.nb_rows = g.nhwc ? 0 : (long)g.B * nrow * rf.xblk * rf.cblk;
+            rf.items = (long)g.B * ((g.nhwc ? (long)nrow * g.W : 0) + (long)(g.H - nrow) * ncol) *
+                       (g.cs / 4);
+            rf.nb_items = (rf.items + 255) / 256;
+            const long rblocks = rf.nb_rows + rf.nb_items + gwf.nblk;
+            ring_final_kernel<T><<<(unsigned)rblocks, 256, 0, s>>>(p, rf, gwf);
+            if ((e = hipGetLastError()) != hipSuccess) return e;
+            prof_end(DCN2_STAGE_BWD_GATHER, s);
+        } else {
+            prof_begin(DCN2_STAGE_BWD_GATHER, s);
+            // At most two workgroups per CU (extra LDS reserved at launch): each
+            // bucket's rows are read once per corner, and with three buckets per
+            // CU the rows in use no longer fit an XCD's L2 (measured at c2:
+            // 138 us at three per CU, 113 us at two, 119 us at one).
+            int lds_cu = 0;
+            if (hipDeviceGetAttribute(&lds_cu, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor,
+                                      dev) != hipSuccess)
+                lds_cu = 0;
+            const int pad = std::max(0, lds_cu / 3 + 256 - kGatherStaticLds);
+            dcn2_gi_gather_kernel<T><<<nbk, 512, pad, s>>>(p);
+            if ((e = hipGetLastError()) != hipSuccess) return e;
+            // the windows' border rings into gi_acc (tile-boundary pixels only)
+            if (ring_items > 0) {
+                dim3 rgrid((unsigned)((ring_items + 255) / 256), g.B);
+                ring_merge_kernel<<<rgrid, 256, 0, s>>>(p.gi_acc, p.ring, g.H, g.W, g.cs, g.Cgp, g.G,
+                                                        p.nty, p.ntx, nrow, ncol);
+            }
+            if ((e = hipGetLastError()) != hipSuccess) return e;
+            prof_end(DCN2_STAGE_BWD_GATHER, s);
+            if (!fused && (e = run_gradw()) != hipSuccess) return e;
+            // 4. grad_input to the caller's layout (and grad_weight / grad_bias)
+            prof_begin(DCN2_STAGE_BWD_FINAL, s);
             const int HW = g.H * g.W;
             if (g.nhwc) {
                 const long total = (long)g.B * HW * g.C;
@@ -2777,8 +3052,8 @@ static hipError_t backward_t(const Geo &g, const BwdParams &p0, void *grad_input
                     p.gi_acc, (T *)grad_input, g.C, HW, g.Cg, g.Cgp, g.cs, vec, g.B, gwf);
             }
             if ((e = hipGetLastError()) != hipSuccess) return e;
+            prof_end(DCN2_STAGE_BWD_FINAL, s);
         }
-        prof_end(DCN2_STAGE_BWD_FINAL, s);
     } else {
         // 5. (empty batch) grad_weight / grad_bias alone
         prof_begin(DCN2_STAGE_BWD_FINAL, s);
@@ -2799,6 +3074,13 @@ GatherGeo gather_geometry(const Geo &g) {
     gg.row_esz = row_elem_bytes(g.dtype);
     gg.batch_bytes = (long)kGatherBatch * g.Cgp * gg.row_esz;
     gg.max_batch_bytes = kGatherOutOfRange;
+    // By cells (each row read once, one block per CU) when the buckets are
+    // full enough to amortise a block's fixed work; per pixel otherwise.
+    // DCN2_GI_PUSH=1 / 0 in the environment forces either.  Measured: c2 68
+    // against 72 us, c3 ~190 against 282 us (2304 samples per bucket); c4
+    // (576 per bucket) ~118 against 73 us.
+    const char *genv = std::getenv("DCN2_GI_PUSH");
+    gg.by_cells = genv ? genv[0] != '0' : gg.rows >= (long)kPushMinPerBucket * gg.nbuckets;
     return gg;
 }
 
@@ -2857,6 +3139,8 @@ hipError_t launch_backward(const Geo &g, const void *xt, const void *wt, const v
     p.ntx = gg.ntx;
     p.nty = gg.nty;
     p.ring = ring;
+    p.gi_out = nullptr;  // (set by the by-cells grad_input)
+    p.gi_nhwc = p.gi_vec = 0;
     switch (g.dtype) {
     case DCN2_F16: return backward_t<f16>(g, p, grad_input, grad_weight, grad_bias, s);
     case DCN2_BF16: return backward_t<bf16>(g, p, grad_input, grad_weight, grad_bias, s);

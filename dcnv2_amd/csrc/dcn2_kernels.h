@@ -70,6 +70,10 @@ struct GatherGeo {
     int ntx, nty, row_esz;
     long nbuckets, rows;
     long batch_bytes, max_batch_bytes;
+    // grad_input by cells (dcn2_gi_push_kernel, written straight into the
+    // caller's grad_input; no fp32 accumulator in the workspace) or by pixels
+    // (dcn2_gi_gather_kernel into gi_acc, then a finalisation pass)
+    bool by_cells;
 };
 GatherGeo gather_geometry(const Geo &g);
 

@@ -132,20 +132,25 @@ def test_workspace_sizes(L):
     assert L.dcn2_forward_workspace_bytes(ctypes.byref(desc(B=0))) > 0
 
 
-def test_backward_workspace_is_exact_size(L):
+def test_backward_workspace_is_exact_size(L, monkeypatch):
     """The grad_input buckets hold one row per sample (B*G*kh*kw*Ho*Wo rows of
     Cg rounded to 64 channels), however the samples cluster, so the c2 shape
-    (B8 C64 128x128 Cout256 fp16) needs about 236 MB: channels-last input
-    copy 16.8 MB, fp32 grad_input accumulator 33.6 MB, rows 151 MB, records
-    18.9 MB, sample rows 4.7 MB, border rings 10.6 MB, packed weights and
-    grad_weight accumulator 0.9 MB."""
+    (B8 C64 128x128 Cout256 fp16) needs about 203 MB: channels-last input
+    copy 16.8 MB, rows 151 MB, records 18.9 MB, sample rows 4.7 MB, border
+    rings 10.6 MB, packed weights and grad_weight accumulator 0.9 MB.  Its
+    buckets are full enough for the by-cells grad_input, which writes the
+    caller's grad_input directly; the per-pixel form (forced with
+    DCN2_GI_PUSH=0) adds the fp32 grad_input accumulator, 33.6 MB."""
     d = desc(B=8, C=64, H=128, W=128, Co=256, dtype=1)
     nbytes = L.dcn2_backward_workspace_bytes(ctypes.byref(d))
     rows = 8 * 9 * 128 * 128
-    assert rows * (64 * 2 + 16) < nbytes < 240e6
+    assert rows * (64 * 2 + 16) < nbytes < 205e6
     # bf16 hands fp32 rows to the gather: twice the row bytes
     d16 = desc(B=8, C=64, H=128, W=128, Co=256, dtype=2)
     assert L.dcn2_backward_workspace_bytes(ctypes.byref(d16)) - nbytes == rows * 64 * 2
+    monkeypatch.setenv("DCN2_GI_PUSH", "0")
+    acc = 8 * 128 * 128 * 64 * 4
+    assert L.dcn2_backward_workspace_bytes(ctypes.byref(d)) - nbytes == acc
 
 
 def test_entry_points_reject_before_any_launch(L):
