@@ -2339,19 +2339,25 @@ __global__ __launch_bounds__(512) void dcn2_gi_push_kernel(const BwdParams p) {
                 lx = ok ? f.y : 0.0f;
                 off = ok ? (int)sslot[pos] * row_bytes : kGatherOutOfRange;
             };
-            auto fetch = [&](int off, float ly, float lx, u32x4 (&raw)[RPB][NLD], float (&fy)[RPB],
-                             float (&fx)[RPB]) __attribute__((always_inline)) {
+            // A batch in flight: the RPB rows' loads (each lane's slice of
+            // row u comes from lane u of its group) and this lane's own row's
+            // fractions, handed out to the group when the batch is summed.
+            struct Batch {
+                u32x4 raw[RPB][NLD];
+                float ly, lx;
+            };
+            auto fetch = [&](int off, float ly, float lx, Batch &bt) __attribute__((always_inline)) {
+                bt.ly = ly;
+                bt.lx = lx;
                 static_for<0, RPB>([&](auto uc) __attribute__((always_inline)) {
                     constexpr int u = decltype(uc)::value;
                     const int ou = __builtin_amdgcn_ds_swizzle(off, (u << 5) | 0x18);
-                    fy[u] = __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(ly), (u << 5) | 0x18));
-                    fx[u] = __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(lx), (u << 5) | 0x18));
                     // row_bytes is a multiple of 128 * NLD (the slice's range)
                     // and the marker has the low bits set, so OR-ing the slice
                     // in keeps either in range
 #pragma unroll
                     for (int h = 0; h < NLD; ++h)
-                        raw[u][h] = __builtin_amdgcn_raw_buffer_load_b128(rrs, ou | (slice + 16 * h), 0, 0);
+                        bt.raw[u][h] = __builtin_amdgcn_raw_buffer_load_b128(rrs, ou | (slice + 16 * h), 0, 0);
                 });
             };
             float S[4][EPL];
@@ -2359,22 +2365,23 @@ __global__ __launch_bounds__(512) void dcn2_gi_push_kernel(const BwdParams p) {
             for (int q = 0; q < 4; ++q)
 #pragma unroll
                 for (int e = 0; e < EPL; ++e) S[q][e] = 0.0f;
-            auto accumulate = [&](const u32x4 (&raw)[RPB][NLD], const float (&fy)[RPB],
-                                  const float (&fx)[RPB]) __attribute__((always_inline)) {
-#pragma unroll
-                for (int u = 0; u < RPB; ++u) {
-                    const float hy = 1.0f - fy[u], hx = 1.0f - fx[u];
-                    const float w[4] = {hy * hx, hy * fx[u], fy[u] * hx, fy[u] * fx[u]};
+            auto accumulate = [&](const Batch &bt) __attribute__((always_inline)) {
+                static_for<0, RPB>([&](auto uc) __attribute__((always_inline)) {
+                    constexpr int u = decltype(uc)::value;
+                    const float fy = __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(bt.ly), (u << 5) | 0x18));
+                    const float fx = __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(bt.lx), (u << 5) | 0x18));
+                    const float hy = 1.0f - fy, hx = 1.0f - fx;
+                    const float w[4] = {hy * hx, hy * fx, fy * hx, fy * fx};
 #pragma unroll
                     for (int h = 0; h < NLD; ++h) {
                         float v[EU];
-                        Unpack<R>::run(make_uint4(raw[u][h].x, raw[u][h].y, raw[u][h].z, raw[u][h].w), v);
+                        Unpack<R>::run(make_uint4(bt.raw[u][h].x, bt.raw[u][h].y, bt.raw[u][h].z, bt.raw[u][h].w), v);
 #pragma unroll
                         for (int q = 0; q < 4; ++q)
 #pragma unroll
                             for (int e = 0; e < EU; ++e) S[q][h * EU + e] = fmaf(w[q], v[e], S[q][h * EU + e]);
                     }
-                }
+                });
             };
             // corner q of the group's cell of round r: pixel (cy + q/2, cx + q%2);
             // corner 01 of this group and corner 00 of the next group share a
@@ -2402,13 +2409,12 @@ __global__ __launch_bounds__(512) void dcn2_gi_push_kernel(const BwdParams p) {
             };
             // stream cursors (wave-uniform): fetch point (fr, fj), sum point (cr, cj)
             int fr = 0, fj = 0, cr = 0, cj = 0;
-            auto fetch_next = [&](u32x4 (&raw)[RPB][NLD], float (&fy)[RPB], float (&fx)[RPB])
-                __attribute__((always_inline)) {
+            auto fetch_next = [&](Batch &bt) __attribute__((always_inline)) {
                 if (fr < 4) {
                     int off;
                     float ly, lx;
                     row_info(fr, fj, off, ly, lx);
-                    fetch(off, ly, lx, raw, fy, fx);
+                    fetch(off, ly, lx, bt);
                     if (++fj == pick(nbat, fr)) {
                         ++fr;
                         fj = 0;
@@ -2425,21 +2431,28 @@ __global__ __launch_bounds__(512) void dcn2_gi_push_kernel(const BwdParams p) {
                     cj = 0;
                 }
             };
-            u32x4 ra[RPB][NLD], rb[RPB][NLD];
-            float ya[RPB], xa[RPB], yb[RPB], xb[RPB];
-            // (scheduling barriers keep each batch's loads ahead of the sums of
-            // the previous one)
-            fetch_next(ra, ya, xa);
-            for (int sidx = 0; sidx < nstream; sidx += 2) {
-                fetch_next(rb, yb, xb);
+            // three batches rotate: while one is summed, the next two are in
+            // flight (scheduling barriers keep each batch's loads ahead of the
+            // sums of the previous one)
+            Batch ba, bb, bc;
+            fetch_next(ba);
+            fetch_next(bb);
+            for (int sidx = 0; sidx < nstream; sidx += 3) {
+                fetch_next(bc);
                 __builtin_amdgcn_sched_barrier(0);
-                accumulate(ra, ya, xa);
+                accumulate(ba);
                 sum_done();
                 __builtin_amdgcn_sched_barrier(0);
                 if (sidx + 1 >= nstream) break;
-                fetch_next(ra, ya, xa);
+                fetch_next(ba);
                 __builtin_amdgcn_sched_barrier(0);
-                accumulate(rb, yb, xb);
+                accumulate(bb);
+                sum_done();
+                __builtin_amdgcn_sched_barrier(0);
+                if (sidx + 2 >= nstream) break;
+                fetch_next(bb);
+                __builtin_amdgcn_sched_barrier(0);
+                accumulate(bc);
                 sum_done();
                 __builtin_amdgcn_sched_barrier(0);
             }
