@@ -532,8 +532,14 @@ __global__ __launch_bounds__(512) void dcn2_fwd_ws_kernel(const FwdParams p) {
             const uint4 wq = Blend8<T>::weights(cr.w);
             const bool vy = dhalf ? sp.vy1 : sp.vy0;
             RingHalf hd;
-            hd.o0 = vy && sp.vx0 ? (dhalf ? cr.off[2] : cr.off[0]) * (int)sizeof(T) : (int)img_bytes;
-            hd.o1 = vy && sp.vx1 ? (dhalf ? cr.off[3] : cr.off[1]) * (int)sizeof(T) : (int)img_bytes;
+            // (bit selects: written as conditional expressions these became a
+            // divergent branch, which split the step's scheduling region and
+            // left the descriptor VALU after the MFMAs instead of between them)
+            const int oa = (dhalf ? cr.off[2] : cr.off[0]) * (int)sizeof(T);
+            const int ob = (dhalf ? cr.off[3] : cr.off[1]) * (int)sizeof(T);
+            const int ma = -(int)(vy && sp.vx0), mb = -(int)(vy && sp.vx1);
+            hd.o0 = (oa & ma) | ((int)img_bytes & ~ma);
+            hd.o1 = (ob & mb) | ((int)img_bytes & ~mb);
             hd.w0 = dhalf ? wq.z : wq.x;
             hd.w1 = dhalf ? wq.w : wq.y;
             ring[R][dpix].h[dhalf] = hd;
@@ -729,6 +735,22 @@ __global__ __launch_bounds__(512) void dcn2_fwd_ws_kernel(const FwdParams p) {
             mfma_stage(std::integral_constant<int, S_>{});
             put_desc(S_ ^ 1, cd);
             load_om(co);
+            // Interleave (one scheduling region: the step has no divergent
+            // branch up to here): the B fragments of ks 0 and 1, then per ks
+            // eight MFMAs with up to three VALU instructions of the
+            // descriptors after each, and the B fragments of ks + 2.  The MFMA
+            // pipe holds the wave's issue for most of the step, so the
+            // descriptor arithmetic rides in its gaps.
+            __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+#pragma unroll
+            for (int ks = 0; ks < NKS; ++ks) {
+#pragma unroll
+                for (int m = 0; m < IB * JB; ++m) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+                }
+                if (ks + 2 < NKS) __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+            }
             if (cur.j == last) {  // tile done: write it, start the next one at its bias
                 store_tile(cur);
                 if (nxt.k < my_tiles) init_acc(nxt.m0);
