@@ -329,6 +329,37 @@ def test_channels_last_input(case):
             check(f"{name} ({tag})", g, r, TOL[dtype])
 
 
+@pytest.mark.parametrize("case", [
+    # dtype, C, deformable groups, Cout, H, W: images with tile-boundary rows and
+    # columns (every 16th pixel), so the boundary pixels come from the rings
+    (torch.float16, 64, 1, 40, 37, 35),    # read in place, 16-byte stores of 8 channels
+    (torch.bfloat16, 24, 2, 40, 33, 40),   # padded groups (12 channels): element-wise stores
+    (torch.float32, 64, 2, 24, 34, 33),    # fp32 (32-channel chunks), two groups
+    (torch.bfloat16, 18, 2, 24, 35, 34),   # 9 channels per group
+], ids=["f16_c64", "bf16_c24_dg2", "f32_c64_dg2", "bf16_c18_dg2"])
+def test_grad_input_channels_last_by_cells(case):
+    """A channels_last grad_input written directly by the per-cell kernel and
+    ring_final_kernel (DCN2_GI_PUSH=1), and by the per-pixel kernel with its
+    finalisation (DCN2_GI_PUSH=0): all five gradients against the oracle, for
+    either grad_output layout."""
+    dtype, C, G, Cout, H, W = case
+    w, t = _small(dtype, B=2, C=C, H=H, W=W, Cout=Cout, G=G, osc=3.0, seed=29)
+    geo = w.geometry()
+    cl = torch.channels_last
+    x_cl = t["input"].to(DEV).to(memory_format=cl)
+    args = [None if t[k] is None else t[k].to(DEV) for k in IN5]
+    go = t["grad_output"].to(DEV)
+    rgrads = oracle_backward(t, geo)
+    for push in ("1", "0"):
+        for go_t, tag in ((go.to(memory_format=cl), "grad_output channels_last"), (go, "grad_output NCHW")):
+            grads = _with_env("DCN2_GI_PUSH", push,
+                              lambda: _C.dcn_v2_backward(x_cl, *args[1:], go_t, *_args(geo)))
+            torch.cuda.synchronize()
+            assert grads[0].is_contiguous(memory_format=cl)
+            for name, g, r in zip(GRADS, grads, rgrads):
+                check(f"{name} (push={push}, {tag})", g, r, TOL[dtype])
+
+
 def test_channels_last_predictor_output_path():
     """dcn_v2_forward_om / dcn_v2_backward_om with a channels_last input match
     the same calls on the NCHW copy."""
