@@ -171,8 +171,11 @@ enum dcn2_stage {
                                     grad_bias (DCN2_STAGE_BWD_GRADW then records
                                     no launch)                                   */
     DCN2_STAGE_BWD_GRADW = 4,    /* grad_weight / grad_bias                        */
-    DCN2_STAGE_BWD_GATHER = 5,   /* grad_input accumulation                       */
-    DCN2_STAGE_BWD_FINAL = 6,    /* conversion to the caller's dtype and layout   */
+    DCN2_STAGE_BWD_GATHER = 5,   /* grad_input; by cells (dense buckets) it is
+                                    written in the caller's dtype and layout here,
+                                    grad_weight / grad_bias finalised with it     */
+    DCN2_STAGE_BWD_FINAL = 6,    /* conversion to the caller's dtype and layout
+                                    (per-pixel grad_input only)                  */
     DCN2_STAGE_BWD_BUCKET = 7,   /* grad_input bucket passes (count, scan, place) */
     DCN2_STAGE_COUNT = 8
 };
