@@ -208,7 +208,7 @@ __device__ __forceinline__ float shfl_xor_f(float v, int mask) {
 // (workgroup, cell tile) adds its count (count pass) or claims a range of the
 // bucket's rows (place pass).  Claiming rows with one global atomic per wave
 // instead serialises thousands of atomics on each bucket counter.
-constexpr int kBucketTab = 16384;  // cell tiles of one image the LDS table may hold
+constexpr int kBucketTab = 8192;  // cell tiles of one image the LDS tables may hold (two in the place pass: 64 KB)
 constexpr int kBucketSPT = 4;      // samples per thread
 
 struct BucketSample {
@@ -263,25 +263,33 @@ __device__ __forceinline__ int place_sample(const BwdParams &p, const BucketSamp
 template <bool PLACE>
 __global__ __launch_bounds__(256) void dcn2_bucket_kernel(const BwdParams p, const void *offset_v,
                                                           int esz_is_f32, int is_bf16) {
-    extern __shared__ int tab[];  // [nty * ntx]: sized at launch, so small images run many workgroups per CU
+    // [nty * ntx] per-tile counts, then (place pass) first rows; the place
+    // pass also keeps each tile's bucket end.  Sized at launch, so small
+    // images run many workgroups per CU.
+    extern __shared__ int tab[];
     const int N = p.Ho * p.Wo, KK = p.kh * p.kw;
     const int tid = threadIdx.x, ntile = p.nty * p.ntx;
+    int *const tend = tab + ntile;  // (place pass only)
     const int plane = blockIdx.y, b = blockIdx.z, g = plane / KK;
     const int n_base = blockIdx.x * 256 * kBucketSPT;
     for (int i = tid; i < ntile; i += 256) tab[i] = 0;
     __syncthreads();
     int rank[kBucketSPT];
+    BucketSample bsk[kBucketSPT];  // the place pass keeps the positions (no second computation)
 #pragma unroll
     for (int k = 0; k < kBucketSPT; ++k) {
         const BucketSample bs =
             bucket_sample(p, offset_v, esz_is_f32, is_bf16, b, plane, n_base + k * 256 + tid);
         rank[k] = bs.any ? atomicAdd(tab + bs.tkey, 1) : -1;
+        if constexpr (PLACE) bsk[k] = bs;
     }
     __syncthreads();
-    int *ctr = (PLACE ? p.bcur : p.bcnt) + (size_t)(b * p.G + g) * ntile;
+    const int key0 = (b * p.G + g) * ntile;
+    int *ctr = (PLACE ? p.bcur : p.bcnt) + (size_t)key0;
     for (int i = tid; i < ntile; i += 256) {
         const int c = tab[i];
         if (c) tab[i] = atomicAdd(ctr + i, c);  // first row of this workgroup's range
+        if constexpr (PLACE) tend[i] = p.bstart[key0 + i + 1];
     }
     if constexpr (PLACE) {
         __syncthreads();
@@ -291,9 +299,15 @@ __global__ __launch_bounds__(256) void dcn2_bucket_kernel(const BwdParams p, con
             if (n >= N) continue;
             int sx = -1;
             if (rank[k] >= 0) {
-                const BucketSample bs = bucket_sample(p, offset_v, esz_is_f32, is_bf16, b, plane, n);
-                const int key = (b * p.G + g) * ntile + bs.tkey;
-                sx = place_sample(p, bs, key, tab[bs.tkey] + rank[k]);
+                // Row of the sample; written only inside the bucket's range, so
+                // the storage is never written out of bounds, whatever the counts.
+                const BucketSample &bs = bsk[k];
+                const int row = tab[bs.tkey] + rank[k];
+                if (row >= 0 && row < tend[bs.tkey]) {
+                    p.rec[row] = make_int4(row, (bs.sp.y0 & 0xffff) | (int)((unsigned)bs.sp.x0 << 16),
+                                           __float_as_int(bs.sp.ly), __float_as_int(bs.sp.lx));
+                    sx = row;
+                }
             }
             p.sidx[((size_t)b * p.G * KK + plane) * N + n] = sx;
         }
@@ -2905,7 +2919,7 @@ static hipError_t backward_t(const Geo &g, const BwdParams &p0, void *grad_input
             if ((e = hipGetLastError()) != hipSuccess) return e;
             dcn2_bucket_scan_kernel<<<1, 1024, 0, s>>>(p.bcnt, p.bstart, p.bcur, nbuckets);
             if ((e = hipGetLastError()) != hipSuccess) return e;
-            if (tab) dcn2_bucket_kernel<true><<<bgrid, 256, tab_bytes, s>>>(p, p.offset, f32, isbf);
+            if (tab) dcn2_bucket_kernel<true><<<bgrid, 256, 2 * tab_bytes, s>>>(p, p.offset, f32, isbf);
             else dcn2_bucket_global_kernel<true><<<bgrid, 256, 0, s>>>(p, p.offset, f32, isbf);
             if ((e = hipGetLastError()) != hipSuccess) return e;
         }

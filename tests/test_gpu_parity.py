@@ -468,7 +468,7 @@ def test_clustered_offsets_one_bucket(dtype):
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16], ids=["float32", "float16"])
 def test_bucket_table_beyond_lds(dtype):
     """An image of 2063 x 2063 pixels has 129 x 129 = 16641 cell tiles, more
-    than the bucket pre-pass's LDS table holds (16384), so the count and place
+    than the bucket pre-pass's LDS tables hold (8192), so the count and place
     passes take their global-atomic variant.  1x1 kernel, 4 channels, offsets
     N(0, 2): all five gradients against the oracle."""
     w, t = _small(dtype, B=1, C=4, H=2063, W=2063, Cout=4, k=1, p=0, G=1, osc=2.0, seed=5)
