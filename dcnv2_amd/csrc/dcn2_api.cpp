@@ -267,8 +267,10 @@ static int backward_impl(const Geo &g, const void *input, const void *weight, co
     clr.n[0] = (size_t)g.Mp * g.Kp;
     clr.p[1] = (float *)(base + ws.gb_acc);
     clr.n[1] = grad_bias ? (size_t)g.Mp : 0;
+    // (bcnt, bstart and bcur are adjacent: the place pass that scans the
+    // counts itself claims rows from bcur = 0)
     clr.p[2] = (float *)(base + ws.bcnt);
-    clr.n[2] = g.B > 0 ? (size_t)gg.nbuckets : 0;
+    clr.n[2] = g.B > 0 ? (ws.bcur - ws.bcnt) / sizeof(int) + (size_t)gg.nbuckets : 0;
     prof_begin(DCN2_STAGE_BWD_PACK, s);
     if ((rc = check_launch(launch_pack(g, g.xt_direct ? nullptr : input, (void *)xt, weight, wt,
                                        tab, true, s, &clr), "pack")))

@@ -208,8 +208,16 @@ __device__ __forceinline__ float shfl_xor_f(float v, int mask) {
 // (workgroup, cell tile) adds its count (count pass) or claims a range of the
 // bucket's rows (place pass).  Claiming rows with one global atomic per wave
 // instead serialises thousands of atomics on each bucket counter.
-constexpr int kBucketTab = 8192;  // cell tiles of one image the LDS tables may hold (two in the place pass: 64 KB)
+//
+// With at most kBucketFold buckets in all the place pass also does the scan:
+// each workgroup sums the counts of the buckets before its image and group
+// and scans those of its own tiles (a few thousand L2-resident ints), claims
+// rows relative to the bucket start (bcur then starts at 0), and the first
+// workgroup of each (image, group) writes its bucket starts for the later
+// kernels.  That saves the one-workgroup scan launch between the passes.
+constexpr int kBucketTab = 8191;   // cell tiles of one image the LDS tables may hold (2 * 8191 + 1 ints: 64 KB)
 constexpr int kBucketSPT = 4;      // samples per thread
+constexpr int kBucketFold = 4096;  // buckets up to which the place pass scans the counts itself
 
 struct BucketSample {
     SamplePos sp;
@@ -262,17 +270,40 @@ __device__ __forceinline__ int place_sample(const BwdParams &p, const BucketSamp
 // PLACE = false: the count pass (bcnt); true: the place pass (bcur, rec, sidx).
 template <bool PLACE>
 __global__ __launch_bounds__(256) void dcn2_bucket_kernel(const BwdParams p, const void *offset_v,
-                                                          int esz_is_f32, int is_bf16) {
+                                                          int esz_is_f32, int is_bf16, int fold) {
     // [nty * ntx] per-tile counts, then (place pass) first rows; the place
-    // pass also keeps each tile's bucket end.  Sized at launch, so small
-    // images run many workgroups per CU.
+    // pass also keeps the tiles' bucket starts, [nty * ntx + 1].  Sized at
+    // launch, so small images run many workgroups per CU.
     extern __shared__ int tab[];
+    __shared__ int wsum[4];
     const int N = p.Ho * p.Wo, KK = p.kh * p.kw;
     const int tid = threadIdx.x, ntile = p.nty * p.ntx;
-    int *const tend = tab + ntile;  // (place pass only)
+    int *const tst = tab + ntile;  // (place pass only)
     const int plane = blockIdx.y, b = blockIdx.z, g = plane / KK;
+    const int key0 = (b * p.G + g) * ntile;
     const int n_base = blockIdx.x * 256 * kBucketSPT;
     for (int i = tid; i < ntile; i += 256) tab[i] = 0;
+    // Folded scan (place pass): tst[i] = bcnt[0] + ... + bcnt[key0 + i - 1],
+    // i = 0..ntile (every count is complete: the count pass has ended).
+    // Thread t holds counts 16t .. 16t + 15 from four independent 16-byte
+    // loads, issued before the samples' offset loads so that both are in
+    // flight together, through a buffer over the first key0 + ntile counts
+    // rounded up to whole 16-byte pieces (bcnt has room for them; pieces past
+    // it read 0); counts past key0 + ntile are set to 0.
+    static_assert(kBucketFold == 256 * 16, "16 counts per thread");
+    typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+    const int nb = key0 + ntile, lane = tid & 63;
+    int v[16];
+    if (PLACE && fold) {
+        const __amdgpu_buffer_rsrc_t crs =
+            __builtin_amdgcn_make_buffer_rsrc(p.bcnt, (short)0, ((nb + 3) & ~3) * (int)sizeof(int), 0x00020000);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const u32x4 r = __builtin_amdgcn_raw_buffer_load_b128(crs, (tid * 16 + 4 * q) * 4, 0, 0);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[4 * q + e] = (int)r[e];
+        }
+    }
     __syncthreads();
     int rank[kBucketSPT];
     BucketSample bsk[kBucketSPT];  // the place pass keeps the positions (no second computation)
@@ -283,13 +314,44 @@ __global__ __launch_bounds__(256) void dcn2_bucket_kernel(const BwdParams p, con
         rank[k] = bs.any ? atomicAdd(tab + bs.tkey, 1) : -1;
         if constexpr (PLACE) bsk[k] = bs;
     }
+    int sum = 0, incl = 0;
+    if (PLACE && fold) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            v[e] = tid * 16 + e < nb ? v[e] : 0;
+            sum += v[e];
+        }
+        incl = sum;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const int o = __shfl_up(incl, d, 64);
+            if (lane >= d) incl += o;
+        }
+        if (lane == 63) wsum[tid >> 6] = incl;
+    }
     __syncthreads();
-    const int key0 = (b * p.G + g) * ntile;
+    if (PLACE && fold) {
+        int run = incl - sum;
+        for (int w = 0; w < (tid >> 6); ++w) run += wsum[w];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int j = tid * 16 + e;
+            if (j >= key0 && j < nb) tst[j - key0] = run;
+            run += v[e];
+        }
+        if (tid == 255) tst[ntile] = run;  // (the counts past nb are 0): the total
+    } else if (PLACE) {
+        for (int i = tid; i <= ntile; i += 256) tst[i] = p.bstart[key0 + i];
+    }
+    if constexpr (PLACE) __syncthreads();
+    if (PLACE && fold && blockIdx.x == 0 && plane % KK == 0)
+        for (int i = tid; i <= ntile; i += 256) p.bstart[key0 + i] = tst[i];
     int *ctr = (PLACE ? p.bcur : p.bcnt) + (size_t)key0;
     for (int i = tid; i < ntile; i += 256) {
         const int c = tab[i];
-        if (c) tab[i] = atomicAdd(ctr + i, c);  // first row of this workgroup's range
-        if constexpr (PLACE) tend[i] = p.bstart[key0 + i + 1];
+        // first row of this workgroup's range (bcur counts from the bucket
+        // start when folded, holds absolute rows otherwise)
+        if (c) tab[i] = (PLACE && fold ? tst[i] : 0) + atomicAdd(ctr + i, c);
     }
     if constexpr (PLACE) {
         __syncthreads();
@@ -303,7 +365,7 @@ __global__ __launch_bounds__(256) void dcn2_bucket_kernel(const BwdParams p, con
                 // the storage is never written out of bounds, whatever the counts.
                 const BucketSample &bs = bsk[k];
                 const int row = tab[bs.tkey] + rank[k];
-                if (row >= 0 && row < tend[bs.tkey]) {
+                if (row >= 0 && row < tst[bs.tkey + 1]) {
                     p.rec[row] = make_int4(row, (bs.sp.y0 & 0xffff) | (int)((unsigned)bs.sp.x0 << 16),
                                            __float_as_int(bs.sp.ly), __float_as_int(bs.sp.lx));
                     sx = row;
@@ -2912,14 +2974,19 @@ static hipError_t backward_t(const Geo &g, const BwdParams &p0, void *grad_input
             const int f32 = sizeof(T) == 4, isbf = std::is_same<T, bf16>::value;
             const int nbuckets = g.B * g.G * p.nty * p.ntx;
             const bool tab = (long)p.nty * p.ntx <= kBucketTab;
+            const int fold = tab && nbuckets <= kBucketFold;  // bcnt, bstart, bcur cleared by the pack launch
             const dim3 bgrid(ceil_div(g.N, tab ? 256 * kBucketSPT : 256), g.G * g.KK, g.B);
             const size_t tab_bytes = (size_t)p.nty * p.ntx * sizeof(int);
-            if (tab) dcn2_bucket_kernel<false><<<bgrid, 256, tab_bytes, s>>>(p, p.offset, f32, isbf);
+            if (tab) dcn2_bucket_kernel<false><<<bgrid, 256, tab_bytes, s>>>(p, p.offset, f32, isbf, 0);
             else dcn2_bucket_global_kernel<false><<<bgrid, 256, 0, s>>>(p, p.offset, f32, isbf);
             if ((e = hipGetLastError()) != hipSuccess) return e;
-            dcn2_bucket_scan_kernel<<<1, 1024, 0, s>>>(p.bcnt, p.bstart, p.bcur, nbuckets);
-            if ((e = hipGetLastError()) != hipSuccess) return e;
-            if (tab) dcn2_bucket_kernel<true><<<bgrid, 256, 2 * tab_bytes, s>>>(p, p.offset, f32, isbf);
+            if (!fold) {
+                dcn2_bucket_scan_kernel<<<1, 1024, 0, s>>>(p.bcnt, p.bstart, p.bcur, nbuckets);
+                if ((e = hipGetLastError()) != hipSuccess) return e;
+            }
+            if (tab)
+                dcn2_bucket_kernel<true><<<bgrid, 256, 2 * tab_bytes + sizeof(int), s>>>(p, p.offset, f32, isbf,
+                                                                                        fold);
             else dcn2_bucket_global_kernel<true><<<bgrid, 256, 0, s>>>(p, p.offset, f32, isbf);
             if ((e = hipGetLastError()) != hipSuccess) return e;
         }

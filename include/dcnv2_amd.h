@@ -176,7 +176,7 @@ enum dcn2_stage {
                                     grad_weight / grad_bias finalised with it     */
     DCN2_STAGE_BWD_FINAL = 6,    /* conversion to the caller's dtype and layout
                                     (per-pixel grad_input only)                  */
-    DCN2_STAGE_BWD_BUCKET = 7,   /* grad_input bucket passes (count, scan, place) */
+    DCN2_STAGE_BWD_BUCKET = 7,   /* grad_input bucket passes (count, scan + place) */
     DCN2_STAGE_COUNT = 8
 };
 DCN2_API int dcn2_profile_enable(int on);

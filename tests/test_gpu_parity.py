@@ -482,6 +482,21 @@ def test_bucket_table_beyond_lds(dtype):
     torch.cuda.empty_cache()
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["float32", "bfloat16"])
+def test_bucket_scan_launch(dtype):
+    """8 images x 2 groups of 256 x 256 pixels: 17 x 17 cell tiles each, 4624
+    buckets in all, more than the place pass scans by itself (4096), so the
+    separate scan launch runs between the LDS-table count and place passes.
+    1x1 kernel, offsets N(0, 2): all five gradients against the oracle."""
+    w, t = _small(dtype, B=8, C=4, H=256, W=256, Cout=4, k=1, p=0, G=2, osc=2.0, seed=6)
+    out = gpu_forward(t, w.geometry())
+    grads = gpu_backward(t, w.geometry())
+    torch.cuda.synchronize()
+    check("output", out, oracle_forward(t, w.geometry()), TOL[dtype])
+    for name, g, r in zip(GRADS, grads, oracle_backward(t, w.geometry())):
+        check(name, g, r, TOL[dtype])
+
+
 # --------------------------------------------------------------------------- fused backward
 def _backward_path(t, geo, go, fused):
     """Backward with the fused kernel allowed or not (DCN2_BWD_FUSED), and
