@@ -184,7 +184,7 @@ BwdWorkspace bwd_workspace(const Geo &g) {
     w.cgm = o;
     o += align256((size_t)gg.rows * g.Cgp * gg.row_esz);
     w.rec = o;
-    o += align256((size_t)gg.rows * 16);
+    o += align256((size_t)gg.rows * 12);  // 12-byte sample records
     w.bcnt = o;
     o += align256((size_t)gg.nbuckets * sizeof(int) + 16);
     w.bstart = o;

@@ -36,6 +36,14 @@
 
 namespace dcn2 {
 
+// Record of a placed sample: its floor corner (y0 in the low, x0 in the high
+// 16 bits, both >= -2) and the bilinear fractions (12 bytes: the consumers
+// find the sample's hand-off row from the record's own position).
+struct BucketRec {
+    int yx;
+    float ly, lx;
+};
+
 struct BwdParams {
     const void *xt, *wt, *tab, *offset, *mask, *gout;
     void *goff, *gmask;
@@ -52,7 +60,7 @@ struct BwdParams {
     // [bstart[k], bstart[k+1]); there are at most B*G*KK*N of them (one per
     // sample), so the storage is sized exactly and no bucket can overflow.
     void *cgm;          // [rows][Cgp] masked column gradient rows, call dtype
-    int4 *rec;          // [rows] sample records, in bucket order
+    struct BucketRec *rec;  // [rows] sample records, in bucket order
     int *bcnt;          // [nbuckets] samples per bucket (count pass)
     int *bstart;        // [nbuckets + 1] first row of each bucket (exclusive scan of bcnt)
     int *bcur;          // [nbuckets] next free row of each bucket (place pass)
@@ -255,15 +263,13 @@ __device__ __forceinline__ BucketSample bucket_sample(const BwdParams &p, const 
     return r;
 }
 
-// Record of a placed sample: its floor corner (y0 in the low, x0 in the high
-// 16 bits, both >= -2) and the bilinear fractions.  Row `row` of the bucket
-// storage is written only if it lies inside the bucket's range, so the
-// storage is never written out of bounds, whatever the counts.
+// Places a sample's record (BucketRec).  Row `row` of the bucket storage is
+// written only if it lies inside the bucket's range, so the storage is never
+// written out of bounds, whatever the counts.
 __device__ __forceinline__ int place_sample(const BwdParams &p, const BucketSample &bs, int key,
                                             int row) {
     if (row < 0 || row >= p.bstart[key + 1]) return -1;
-    p.rec[row] = make_int4(row, (bs.sp.y0 & 0xffff) | (int)((unsigned)bs.sp.x0 << 16),
-                           __float_as_int(bs.sp.ly), __float_as_int(bs.sp.lx));
+    p.rec[row] = BucketRec{(bs.sp.y0 & 0xffff) | (int)((unsigned)bs.sp.x0 << 16), bs.sp.ly, bs.sp.lx};
     return row;
 }
 
@@ -366,8 +372,8 @@ __global__ __launch_bounds__(256) void dcn2_bucket_kernel(const BwdParams p, con
                 const BucketSample &bs = bsk[k];
                 const int row = tab[bs.tkey] + rank[k];
                 if (row >= 0 && row < tst[bs.tkey + 1]) {
-                    p.rec[row] = make_int4(row, (bs.sp.y0 & 0xffff) | (int)((unsigned)bs.sp.x0 << 16),
-                                           __float_as_int(bs.sp.ly), __float_as_int(bs.sp.lx));
+                    p.rec[row] = BucketRec{(bs.sp.y0 & 0xffff) | (int)((unsigned)bs.sp.x0 << 16), bs.sp.ly,
+                                           bs.sp.lx};
                     sx = row;
                 }
             }
@@ -2047,7 +2053,7 @@ __global__ __launch_bounds__(512) void dcn2_gi_gather_kernel(const BwdParams p) 
     // records) to write its ring
     for (int base = 0; base == 0 || base < count; base += kGatherBatch) {
         const int nrec = min(count - base, kGatherBatch);
-        const int4 *__restrict__ recs = p.rec + (size_t)row0 + base;
+        const BucketRec *__restrict__ recs = p.rec + (size_t)row0 + base;
         const bool first = base == 0;
         if (!first) __syncthreads();  // the previous batch is done with the LDS arrays
 
@@ -2062,10 +2068,10 @@ __global__ __launch_bounds__(512) void dcn2_gi_gather_kernel(const BwdParams p) 
             key[k] = -1;
             fr[k] = make_float2(0.f, 0.f);
             if (r < nrec) {
-                const int4 rc = recs[r];
-                const int cy = (int)(short)(rc.y & 0xffff) - oy, cx = (rc.y >> 16) - ox;  // [0, TS)
+                const BucketRec rc = recs[r];
+                const int cy = (int)(short)(rc.yx & 0xffff) - oy, cx = (rc.yx >> 16) - ox;  // [0, TS)
                 const int cell = cy * TS + cx;
-                fr[k] = make_float2(__int_as_float(rc.z), __int_as_float(rc.w));
+                fr[k] = make_float2(rc.ly, rc.lx);
                 key[k] = (cell << 16) | atomicAdd(&ccnt[cell], 1);
             }
         }
@@ -2320,7 +2326,7 @@ __global__ __launch_bounds__(512) void dcn2_gi_push_kernel(const BwdParams p) {
             __syncthreads();  // the window is clear / the previous batch is done with the LDS arrays
             if (cc == 0 || count > kGatherBatch) {
                 // 1. counting sort by cell (cell = local row * TS + local column)
-                const int4 *__restrict__ recs = p.rec + (size_t)row0 + base;
+                const BucketRec *__restrict__ recs = p.rec + (size_t)row0 + base;
                 for (int i = tid; i < NCELL; i += 512) ccnt[i] = 0;
                 __syncthreads();
                 int key[RPT];  // (cell << 16) | rank, or -1
@@ -2331,10 +2337,10 @@ __global__ __launch_bounds__(512) void dcn2_gi_push_kernel(const BwdParams p) {
                     key[k] = -1;
                     fr[k] = make_float2(0.f, 0.f);
                     if (r < nrec) {
-                        const int4 rc = recs[r];
-                        const int cy = (int)(short)(rc.y & 0xffff) - oy, cx = (rc.y >> 16) - ox;  // [0, TS)
+                        const BucketRec rc = recs[r];
+                        const int cy = (int)(short)(rc.yx & 0xffff) - oy, cx = (rc.yx >> 16) - ox;  // [0, TS)
                         const int cell = cy * TS + cx;
-                        fr[k] = make_float2(__int_as_float(rc.z), __int_as_float(rc.w));
+                        fr[k] = make_float2(rc.ly, rc.lx);
                         key[k] = (cell << 16) | atomicAdd(&ccnt[cell], 1);
                     }
                 }
@@ -3225,7 +3231,7 @@ hipError_t launch_backward(const Geo &g, const void *xt, const void *wt, const v
     p.go_vec = (g.out_nhwc ? g.Cout % 8 == 0 : g.N % 8 == 0) && (((uintptr_t)grad_out & 15) == 0);
     const GatherGeo gg = gather_geometry(g);
     p.cgm = cgm;
-    p.rec = (int4 *)rec;
+    p.rec = (BucketRec *)rec;
     p.bcnt = bcnt;
     p.bstart = bstart;
     p.bcur = bcur;
