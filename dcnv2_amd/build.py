@@ -23,11 +23,15 @@ ARCH = "gfx950"
 
 COMMON = ["-O3", "-std=c++17", "-fPIC", "-fvisibility=hidden", f"--offload-arch={ARCH}", "-I", os.path.join(ROOT, "include")]
 DEVICE = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+# Per-source extra flags.  The resident-weight forward keeps the weight in
+# AGPRs, so its MFMA accumulators must be VGPRs (the compiler would otherwise
+# put them in AGPRs and copy weight fragments out on every use).
+EXTRA = {"dcn2_forward_rw.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
 def _compile(src: str) -> str:
     obj = os.path.join(BUILD, os.path.basename(src) + ".o")
-    cmd = [HIPCC, *COMMON, *DEVICE, "-c", src, "-o", obj]
+    cmd = [HIPCC, *COMMON, *DEVICE, *EXTRA.get(os.path.basename(src), []), "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     noise = "packed-fp32-ops"  # the host pass warns that it does not know the feature
     msgs = [ln for ln in (r.stdout + r.stderr).splitlines() if noise not in ln and ln.strip()]

@@ -136,6 +136,7 @@ int make_geo(const dcn2_desc *d, Geo &g) {
     g.off_bs = 2LL * g.G * g.KK * g.N;
     g.msk_bs = (long long)g.G * g.KK * g.N;
     g.msk_logit = 0;
+    g.rw = rw_eligible(g) ? 1 : 0;
     return DCN2_OK;
 }
 
@@ -156,7 +157,10 @@ FwdWorkspace fwd_workspace(const Geo &g) {
     FwdWorkspace w;
     size_t o = 0;
     w.xt = o;
-    if (!g.xt_direct) o += align256((size_t)g.B * g.H * g.W * g.cs * g.esz);
+    if (g.rw)
+        o += align256(rw_input_bytes(g));
+    else if (!g.xt_direct)
+        o += align256((size_t)g.B * g.H * g.W * g.cs * g.esz);
     w.wp = o;
     o += align256((size_t)g.Mp * g.Kp * g.esz);
     w.tab = o;
@@ -218,20 +222,30 @@ int forward_impl(const Geo &g, const void *input, const void *weight, const void
                     "dcn2_forward: workspace needs %zu bytes at 256-byte alignment (got %zu)",
                     ws.total, workspace_bytes);
     if (g.B == 0) return DCN2_OK;
-    if (g.xt_direct && ((uintptr_t)input & 15))
+    // The resident-weight forward stores 16-byte pieces; for an output that is
+    // not 16-byte aligned the chunk-streaming kernel runs instead, in the same
+    // workspace (its channels-last copy is smaller than the pixel-pair one).
+    Geo gf = g;
+    if (gf.rw && ((uintptr_t)output & 15)) gf.rw = 0;
+    // a channels-last input whose channels need no padding is read in place
+    // (except by the resident-weight forward, which reads the pixel-pair copy)
+    const bool direct = gf.xt_direct && !gf.rw;
+    if (direct && ((uintptr_t)input & 15))
         return fail(DCN2_EINVAL, "dcn2_forward: a channels-last input must be 16-byte aligned");
     hipStream_t s = (hipStream_t)stream;
     char *base = (char *)workspace;
-    // a channels-last input whose channels need no padding is read in place
-    const void *xt = g.xt_direct ? input : base + ws.xt;
+    const void *xt = direct ? input : base + ws.xt;
     void *wp = base + ws.wp, *tab = base + ws.tab;
     prof_begin(DCN2_STAGE_FWD_PACK, s);
-    if ((rc = check_launch(launch_pack(g, g.xt_direct ? nullptr : input, (void *)xt, weight, wp,
-                                       tab, false, s), "pack")))
+    if ((rc = check_launch(launch_pack(gf, direct ? nullptr : input, (void *)xt, weight, wp, tab,
+                                       false, s), "pack")))
         return rc;
     prof_end(DCN2_STAGE_FWD_PACK, s);
     prof_begin(DCN2_STAGE_FWD_MAIN, s);
-    rc = check_launch(launch_forward(g, xt, wp, tab, offset, mask, bias, output, s), "forward");
+    if (gf.rw)
+        rc = check_launch(launch_forward_rw(gf, xt, wp, offset, mask, bias, output, s), "forward");
+    else
+        rc = check_launch(launch_forward(gf, xt, wp, tab, offset, mask, bias, output, s), "forward");
     prof_end(DCN2_STAGE_FWD_MAIN, s);
     return rc;
 }
