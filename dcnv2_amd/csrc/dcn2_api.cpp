@@ -157,10 +157,7 @@ FwdWorkspace fwd_workspace(const Geo &g) {
     FwdWorkspace w;
     size_t o = 0;
     w.xt = o;
-    if (g.rw)
-        o += align256(rw_input_bytes(g));
-    else if (!g.xt_direct)
-        o += align256((size_t)g.B * g.H * g.W * g.cs * g.esz);
+    if (!g.xt_direct) o += align256((size_t)g.B * g.H * g.W * g.cs * g.esz);
     w.wp = o;
     o += align256((size_t)g.Mp * g.Kp * g.esz);
     w.tab = o;
@@ -223,13 +220,12 @@ int forward_impl(const Geo &g, const void *input, const void *weight, const void
                     ws.total, workspace_bytes);
     if (g.B == 0) return DCN2_OK;
     // The resident-weight forward stores 16-byte pieces; for an output that is
-    // not 16-byte aligned the chunk-streaming kernel runs instead, in the same
-    // workspace (its channels-last copy is smaller than the pixel-pair one).
+    // not 16-byte aligned the chunk-streaming kernel runs instead (both read
+    // the same channels-last copy).
     Geo gf = g;
     if (gf.rw && ((uintptr_t)output & 15)) gf.rw = 0;
     // a channels-last input whose channels need no padding is read in place
-    // (except by the resident-weight forward, which reads the pixel-pair copy)
-    const bool direct = gf.xt_direct && !gf.rw;
+    const bool direct = gf.xt_direct;
     if (direct && ((uintptr_t)input & 15))
         return fail(DCN2_EINVAL, "dcn2_forward: a channels-last input must be 16-byte aligned");
     hipStream_t s = (hipStream_t)stream;

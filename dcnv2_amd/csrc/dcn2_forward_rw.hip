@@ -11,26 +11,25 @@
 // loop then moves no weight bytes at all; the only vector-memory traffic is
 // the corner gathers (32 KB per 64-pixel step), which is what bounds it.
 //
-// Input layout (pack_input_pairs in dcn2_pack.hip): xp[b][yy][j][c][2] with
-// yy = y + 1 in [0, H+2) and j in [0, W]: the channel-c value of pixels
-// (y, j-1) and (y, j) side by side (zero outside the image, and rows yy = 0
-// and H+1 all zero).  A bilinear sample at (y0 + ly, x0 + lx) then reads two
-// 256-byte runs, row yy = y0+1 and row yy+1 at pair j = x0+1, and each 32-bit
-// word is the (left, right) corner pair of one channel: the blend is two
-// v_dot2_f32_f16 per channel, (w00, w01).(x00, x01) + (w10, w11).(x10, x11),
-// with exact products and fp32 sums.  The corner weights are rounded to fp16
-// for the dot products (relative 2^-12); the blended column is rounded once to
-// fp16 for the MFMA, as the reference rounds its columns (com.cu:83, 87).
-// Corners outside the image read the stored zeros, and a sample with no
-// corner inside reads past the image (zeros from the buffer range check).
+// Input: the channels-last copy xt[b][y*W + x][64] of the pack kernel (or a
+// channels-last input of 64 channels itself), so one bilinear corner of one
+// pixel is one 128-byte run.  The blend multiplies the fp16 corner values by
+// fp32 corner weights and sums in fp32 with v_fma_mix_f32 (one rounding of
+// the blended column to fp16, as the reference samples in fp32 and rounds its
+// columns, com.cu:119-148, 83, 87).  v_fma_mix issues between the MFMAs of
+// the same wave almost for free; packed dot products do not (measured on
+// MI355X: four v_dot2_f32_f16 per 32x32x16 MFMA double its time, four
+// v_fma_mix_f32 add 15 %).  A corner outside the image has an offset past the
+// image and reads zero from the buffer range check.
 //
 // Work: 64-pixel tiles of one image, all 256 output rows, walked persistently
-// and XCD-aware.  One pipeline step per tap: the MFMAs of tap t (16 32x32x16
-// per wave over the LDS stage of t), the blend of tap t+1 (gathered one step
-// earlier) into the other stage, the gathers of tap t+2, one barrier.  Each
-// wave samples its own 16 pixels of every tap; their bilinear descriptors
-// (row offset, two weight pairs) are computed one tile ahead into an LDS ring
-// that only that wave reads.
+// and XCD-aware.  One pipeline step per tap: the MFMAs of step s (16
+// 32x32x16 per wave over LDS stage s % 3), the blend of step s+2 (gathered
+// one step earlier) into its stage, the gathers of step s+3, one barrier; the
+// first fragments of step s+1 are read before that barrier (their stage was
+// completed a step earlier).  Each wave samples its own 16 pixels of every
+// tap; their bilinear descriptors (four corner offsets and weights) are
+// computed one tile ahead into an LDS ring that only that wave reads.
 #include "dcn2_common.h"
 #include "dcn2_kernels.h"
 #include "../../include/dcnv2_amd.h"
@@ -43,14 +42,13 @@ typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
 struct RwParams {
-    const void *xp;      // pair-packed input, one image = img_bytes
+    const void *xt;      // channels-last input, 64 channels, one image = img_bytes
     const void *wp;      // fragment-ordered weight: 8 row blocks x 9 chunks x 4 k-steps
     const void *offset, *mask, *bias;
     void *out;
     int H, W, Wo, N, Cout, sh, sw, ph, pw, dh, dw;
     int ntiles, tiles;       // 64-pixel tiles per image, B * ntiles
-    unsigned img_bytes;      // bytes of one image of xp: (H+2)*(W+1)*256
-    unsigned row_bytes;      // (W+1)*256
+    unsigned img_bytes;      // bytes of one image of xt: H*W*128
     unsigned out_img_bytes;  // Cout*N*2
     long long off_bs, msk_bs;
     int msk_logit;
@@ -60,17 +58,17 @@ constexpr int kRwPx = 64;     // pixels per tile
 constexpr int kRwTaps = 9;    // K chunks (taps) per tile
 constexpr int kRwLdk = 72;    // stage pitch (halfs): 144 bytes, conflict-free fragment reads
 
-// Descriptor of one (tap, pixel) in the ring: x = byte offset of the sample's
-// first row pair inside the image of xp (img_bytes: no corner inside),
-// y = fp16 weights (w00, w01) of that row, z = (w10, w11) of the next row.
-typedef uint4 RwDesc;
 
 template <int MASK, bool ONHWC>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void dcn2_fwd_rw_kernel(const RwParams p) {
     __shared__ __attribute__((aligned(16))) f16 stage[3][kRwPx][kRwLdk];
-    // [tile parity][tap; 9 = sink for the idle lanes of the last round][pixel]
-    __shared__ __attribute__((aligned(16))) RwDesc ring[2][kRwTaps + 1][kRwPx];
+    // Descriptor ring, [tile parity][tap; 9 = sink for the idle lanes of the
+    // last round][pixel]: the byte offsets of the four corners (y0,x0)
+    // (y0,x0+1) (y0+1,x0) (y0+1,x0+1) inside the image (img_bytes outside it)
+    // and their fp32 weights with the mask folded in.
+    __shared__ __attribute__((aligned(16))) uint4 ringO[2][kRwTaps + 1][kRwPx];
+    __shared__ __attribute__((aligned(16))) float4 ringW[2][kRwTaps + 1][kRwPx];
     // tap-8 weight fragments of every wave: [wave][ks*2 + rb][lane]
     __shared__ __attribute__((aligned(16))) f16x8 sA8[4][8][64];
     __shared__ __attribute__((aligned(16))) float sBias[256];
@@ -122,7 +120,7 @@ void dcn2_fwd_rw_kernel(const RwParams p) {
         const int t = xcd_remap((int)blockIdx.x + min(k, my_tiles - 1) * G, p.tiles);
         T.b = uni(t / p.ntiles);
         T.n0 = uni((t - T.b * p.ntiles) * kRwPx);
-        const char *xb = (const char *)p.xp + (size_t)T.b * p.img_bytes;
+        const char *xb = (const char *)p.xt + (size_t)T.b * p.img_bytes;
         T.xrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(xb), (short)0, (int)p.img_bytes,
                                                   0x00020000);
         char *ob = (char *)p.out + (size_t)T.b * p.out_img_bytes;
@@ -155,9 +153,15 @@ void dcn2_fwd_rw_kernel(const RwParams p) {
             if constexpr (MASK) o.m[r] = T.mskb[(size_t)tap * p.N + nc];
         }
     };
-    auto put_desc = [&](int par, int r, const OmRaw &o) __attribute__((always_inline)) {
-        const int tap = 4 * r + dq;
-        const int tc = min(tap, kRwTaps - 1);
+    // One descriptor round in two halves, placed in different slices of a
+    // step: the sample position (desc_pos) and the corner offsets, weights
+    // and ring writes (desc_put).
+    struct DescPos {
+        int y0, x0;
+        float ly, lx, mv;
+    };
+    auto desc_pos = [&](int r, const OmRaw &o) __attribute__((always_inline)) {
+        const int tc = min(4 * r + dq, kRwTaps - 1);
         const int ki = (tc * 11) >> 5, kj = tc - 3 * ki;  // tc / 3, tc % 3 for tc < 9
         float y = (float)(o.by + ki * p.dh) + (float)o.dy[r];
         float x = (float)(o.bx + kj * p.dw) + (float)o.dx[r];
@@ -166,91 +170,119 @@ void dcn2_fwd_rw_kernel(const RwParams p) {
         y = fminf(fmaxf(y, -2.0f), (float)p.H + 1.0f);
         x = fminf(fmaxf(x, -2.0f), (float)p.W + 1.0f);
         const float fy = floorf(y), fx = floorf(x);
-        const int y0 = (int)fy, x0 = (int)fx;
-        const float ly = y - fy, lx = x - fx, hy = 1.0f - ly, hx = 1.0f - lx;
+        DescPos d;
+        d.y0 = (int)fy;
+        d.x0 = (int)fx;
+        d.ly = y - fy;
+        d.lx = x - fx;
         float mv = 1.0f;
         if constexpr (MASK == 1) mv = (float)o.m[r];
         if constexpr (MASK == 2) mv = 1.0f / (1.0f + __expf(-(float)o.m[r]));
-        mv = o.live ? mv : 0.0f;  // pixels past N sample 0
-        const float wy0 = hy * mv, wy1 = ly * mv;
-        const h2 w0 = __builtin_convertvector((float __attribute__((ext_vector_type(2)))){wy0 * hx, wy0 * lx}, h2);
-        const h2 w1 = __builtin_convertvector((float __attribute__((ext_vector_type(2)))){wy1 * hx, wy1 * lx}, h2);
-        // some corner inside: y0 in [-1, H-1] and x0 in [-1, W-1]
-        const bool in = (unsigned)(y0 + 1) <= (unsigned)p.H && (unsigned)(x0 + 1) <= (unsigned)p.W;
-        const unsigned off = (unsigned)((y0 + 1) * (p.W + 1) + (x0 + 1)) * 256u;
-        RwDesc d;
-        d.x = in ? off : p.img_bytes;
-        d.y = __builtin_bit_cast(unsigned, w0);
-        d.z = __builtin_bit_cast(unsigned, w1);
-        d.w = 0;
-        ring[par][tap < kRwTaps ? tap : kRwTaps][dP] = d;
+        d.mv = o.live ? mv : 0.0f;  // pixels past N sample 0
+        return d;
+    };
+    auto desc_put = [&](int par, int r, const DescPos &d) __attribute__((always_inline)) {
+        const int tap = 4 * r + dq;
+        const float hy = 1.0f - d.ly, hx = 1.0f - d.lx;
+        const float wy0 = hy * d.mv, wy1 = d.ly * d.mv;
+        const int y0 = d.y0, x0 = d.x0;
+        const bool vy0 = (unsigned)y0 < (unsigned)p.H, vy1 = (unsigned)(y0 + 1) < (unsigned)p.H;
+        const bool vx0 = (unsigned)x0 < (unsigned)p.W, vx1 = (unsigned)(x0 + 1) < (unsigned)p.W;
+        const unsigned base = (unsigned)(y0 * p.W + x0) * 128u, rowb = (unsigned)p.W * 128u;
+        // (selects as bit masks: a conditional expression can become a
+        // divergent branch that splits the step's scheduling region)
+        auto pick = [&](bool v, unsigned o) __attribute__((always_inline)) {
+            const unsigned m = 0u - (unsigned)v;
+            return (o & m) | (p.img_bytes & ~m);
+        };
+        const int slot = tap < kRwTaps ? tap : kRwTaps;
+        ringO[par][slot][dP] = make_uint4(pick(vy0 && vx0, base), pick(vy0 && vx1, base + 128u),
+                                          pick(vy1 && vx0, base + rowb), pick(vy1 && vx1, base + rowb + 128u));
+        ringW[par][slot][dP] = make_float4(wy0 * hx, wy0 * d.lx, wy1 * hx, wy1 * d.lx);
+    };
+    auto put_desc = [&](int par, int r, const OmRaw &o) __attribute__((always_inline)) {
+        desc_put(par, r, desc_pos(r, o));
     };
 
     // ---------------------------------------------------------------- sampling
-    // Lane l gathers 16-byte piece pc = l%16 (channels 4pc..4pc+3, both
-    // pixels of the pair) of pixels 16w + 4i + sq, i = 0..3, rows 0 and 1.
-    const int pc = lane & 15, sq = lane >> 4;
-    uint4 gx[2][8];      // [set][2i + row]
-    // ring entries a step needs, read at its start: the row offsets of the
-    // gathers it issues and the weight pairs of the pixels it blends
-    auto ring_off = [&](unsigned (&ro)[4], int par, int tap) __attribute__((always_inline)) {
+    // Lane l gathers 16-byte piece pc = l%8 (channels 8pc..8pc+7) of the four
+    // corners of pixels 16w + 8i + pg, pg = l/8, i = 0, 1: 8 loads per step,
+    // 8 lanes per 128-byte corner run.
+    const int pc = lane & 7, pg = lane >> 3;
+    uint4 gx[2][8];      // [set][4i + corner]
+    // ring entries a step needs, read at its start: the corner offsets of the
+    // gathers it issues and the corner weights of the pixels it blends
+    auto ring_off = [&](uint4 (&ro)[2], int par, int tap) __attribute__((always_inline)) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) ro[i] = ring[par][tap][16 * w + 4 * i + sq].x;
+        for (int i = 0; i < 2; ++i) ro[i] = ringO[par][tap][16 * w + 8 * i + pg];
     };
-    auto ring_wts = [&](uint2 (&wt)[4], int par, int tap) __attribute__((always_inline)) {
+    auto ring_wts = [&](float4 (&wt)[2], int par, int tap) __attribute__((always_inline)) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const RwDesc d = ring[par][tap][16 * w + 4 * i + sq];
-            wt[i] = make_uint2(d.y, d.z);
+        for (int i = 0; i < 2; ++i) wt[i] = ringW[par][tap][16 * w + 8 * i + pg];
+    };
+    // corners 2h, 2h+1 of pixel i
+    auto gather2 = [&](auto set_c, const uint4 (&ro)[2], const Tile &T, auto i_c, auto h_c)
+        __attribute__((always_inline)) {
+        constexpr int SET = decltype(set_c)::value, i = decltype(i_c)::value, h = decltype(h_c)::value;
+        const unsigned o[2] = {h ? ro[i].z : ro[i].x, h ? ro[i].w : ro[i].y};
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(T.xrs, (int)(o[q] + (unsigned)pc * 16u), 0, 0);
+            gx[SET][4 * i + 2 * h + q] = make_uint4(v.x, v.y, v.z, v.w);
         }
     };
-    auto gather = [&](auto set_c, const unsigned (&ro)[4], const Tile &T) __attribute__((always_inline)) {
-        constexpr int SET = decltype(set_c)::value;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int voff = (int)(ro[i] + (unsigned)pc * 16u);
-            const u32x4 v0 = __builtin_amdgcn_raw_buffer_load_b128(T.xrs, voff, 0, 0);
-            const u32x4 v1 = __builtin_amdgcn_raw_buffer_load_b128(T.xrs, voff, (int)p.row_bytes, 0);
-            gx[SET][2 * i] = make_uint4(v0.x, v0.y, v0.z, v0.w);
-            gx[SET][2 * i + 1] = make_uint4(v1.x, v1.y, v1.z, v1.w);
-        }
+    auto gather = [&](auto set_c, const uint4 (&ro)[2], const Tile &T) __attribute__((always_inline)) {
+        auto z = std::integral_constant<int, 0>{};
+        auto o = std::integral_constant<int, 1>{};
+        gather2(set_c, ro, T, z, z);
+        gather2(set_c, ro, T, z, o);
+        gather2(set_c, ro, T, o, z);
+        gather2(set_c, ro, T, o, o);
     };
-    // blend of the data gathered into set SET for ring entry (par, tap):
-    // the weight pairs are read back from the ring (still intact: a tile's
-    // entries are only replaced in the middle of the next tile)
-    auto blend_px = [&](auto set_c, int st, const uint2 (&wt)[4], auto i_c) __attribute__((always_inline)) {
-        constexpr int SET = decltype(set_c)::value;
-        {
-            constexpr int i = decltype(i_c)::value;
-            const uint4 r0 = gx[SET][2 * i], r1 = gx[SET][2 * i + 1];
-            const uint2 d = make_uint2(wt[i].x, wt[i].y);
-            const h2 w1 = __builtin_bit_cast(h2, d.y);
-            const unsigned a0[4] = {r0.x, r0.y, r0.z, r0.w}, a1[4] = {r1.x, r1.y, r1.z, r1.w};
-            float v[4];
+    // blend of channels 4h..4h+3 of pixel i from gather set SET: fp32
+    // weights times fp16 corners, fp32 sums (v_fma_mix_f32)
+    auto blend_half = [&](auto set_c, const float4 (&wt)[2], auto i_c, auto h_c, float (&v)[4])
+        __attribute__((always_inline)) {
+        constexpr int SET = decltype(set_c)::value, i = decltype(i_c)::value, h = decltype(h_c)::value;
+        const float wq[4] = {wt[i].x, wt[i].y, wt[i].z, wt[i].w};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) v[c] = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint4 r = gx[SET][4 * i + q];
+            const unsigned u[2] = {h ? r.z : r.x, h ? r.w : r.y};
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
-                // first product pair with the VOP3P form and a zero addend (the
-                // accumulating VOP2 form would need a zeroing move first)
-                asm("v_dot2_f32_f16 %0, %1, %2, 0" : "=v"(v[c]) : "v"(a0[c]), "v"(d.x));
-                v[c] = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, a1[c]), w1, v[c], false);
+                const h2 x2 = __builtin_bit_cast(h2, u[c >> 1]);
+                v[c] = fmaf(wq[q], (float)x2[c & 1], v[c]);
             }
-            typedef float f2 __attribute__((ext_vector_type(2)));
-            const h2 lo = __builtin_convertvector((f2){v[0], v[1]}, h2);
-            const h2 hi = __builtin_convertvector((f2){v[2], v[3]}, h2);
-            *reinterpret_cast<u32x2 *>(&stage[st][16 * w + 4 * i + sq][4 * pc]) =
-                u32x2{__builtin_bit_cast(unsigned, lo), __builtin_bit_cast(unsigned, hi)};
         }
     };
+    auto store_px = [&](int st, auto i_c, const float (&v0)[4], const float (&v1)[4])
+        __attribute__((always_inline)) {
+        constexpr int i = decltype(i_c)::value;
+        typedef float f2 __attribute__((ext_vector_type(2)));
+        const h2 a = __builtin_convertvector((f2){v0[0], v0[1]}, h2);
+        const h2 b = __builtin_convertvector((f2){v0[2], v0[3]}, h2);
+        const h2 c = __builtin_convertvector((f2){v1[0], v1[1]}, h2);
+        const h2 d = __builtin_convertvector((f2){v1[2], v1[3]}, h2);
+        *reinterpret_cast<u32x4 *>(&stage[st][16 * w + 8 * i + pg][8 * pc]) =
+            u32x4{__builtin_bit_cast(unsigned, a), __builtin_bit_cast(unsigned, b),
+                  __builtin_bit_cast(unsigned, c), __builtin_bit_cast(unsigned, d)};
+    };
     auto blend = [&](auto set_c, int st, int par, int tap) __attribute__((always_inline)) {
-        uint2 wt[4];
+        float4 wt[2];
         ring_wts(wt, par, tap);
-        blend_px(set_c, st, wt, std::integral_constant<int, 0>{});
-        blend_px(set_c, st, wt, std::integral_constant<int, 1>{});
-        blend_px(set_c, st, wt, std::integral_constant<int, 2>{});
-        blend_px(set_c, st, wt, std::integral_constant<int, 3>{});
+        float v0[4], v1[4];
+        blend_half(set_c, wt, std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{}, v0);
+        blend_half(set_c, wt, std::integral_constant<int, 0>{}, std::integral_constant<int, 1>{}, v1);
+        store_px(st, std::integral_constant<int, 0>{}, v0, v1);
+        blend_half(set_c, wt, std::integral_constant<int, 1>{}, std::integral_constant<int, 0>{}, v0);
+        blend_half(set_c, wt, std::integral_constant<int, 1>{}, std::integral_constant<int, 1>{}, v1);
+        store_px(st, std::integral_constant<int, 1>{}, v0, v1);
     };
     auto gather_at = [&](auto set_c, int par, int tap, const Tile &T) __attribute__((always_inline)) {
-        unsigned ro[4];
+        uint4 ro[2];
         ring_off(ro, par, tap);
         gather(set_c, ro, T);
     };
@@ -306,14 +338,17 @@ void dcn2_fwd_rw_kernel(const RwParams p) {
             }
         }
     };
-    // Output of the tile: the accumulators are rounded to fp16 and staged in
-    // this wave's LDS block (4 consecutive pixels of one row, NCHW, or 4
-    // consecutive channels of one pixel, channels-last, per 8-byte write),
-    // then written as 16-byte pieces, 8 lanes per 128-byte run of a row (or a
-    // pixel), so every store instruction covers 8 whole 128-byte lines.
-    // Pieces outside the output get an offset past the buffer and are dropped
-    // (N % 8 == 0, resp. Cout % 8 == 0: a piece is all in or all out).
-    auto store_tile = [&](const Tile &T) __attribute__((always_inline)) {
+    // Output of a tile: the accumulators are rounded to fp16 and staged in
+    // this wave's LDS block at the tile's last step (stage_out: 4 consecutive
+    // pixels of one row, NCHW, or 4 consecutive channels of one pixel,
+    // channels-last, per 8-byte write); during the next tile's first step the
+    // block is read back and written as 16-byte pieces, 8 lanes per 128-byte
+    // run of a row (or a pixel), two store instructions per slice (flush_out),
+    // so every store covers 8 whole 128-byte lines and no step waits for the
+    // LDS round trip.  Pieces outside the output get an offset past the buffer
+    // and are dropped (N % 8 == 0, resp. Cout % 8 == 0: a piece is all in or
+    // all out).
+    auto stage_out = [&]() __attribute__((always_inline)) {
         f16(&so)[64][kRwLdk] = sOut[w];
 #pragma unroll
         for (int rb = 0; rb < 2; ++rb)
@@ -332,11 +367,16 @@ void dcn2_fwd_rw_kernel(const RwParams p) {
                     *reinterpret_cast<u32x2 *>(dst) =
                         u32x2{__builtin_bit_cast(unsigned, lo), __builtin_bit_cast(unsigned, hi)};
                 }
+    };
+    auto flush_out = [&](const Tile &T, int it0) __attribute__((always_inline)) {
+        f16(&so)[64][kRwLdk] = sOut[w];
         const int seg = lane & 7;
+        uint4 v[2];
 #pragma unroll
-        for (int it = 0; it < 8; ++it) {
-            const int row = it * 8 + (lane >> 3);
-            const uint4 v = *reinterpret_cast<const uint4 *>(&so[row][seg * 8]);
+        for (int k = 0; k < 2; ++k) v[k] = *reinterpret_cast<const uint4 *>(&so[(it0 + k) * 8 + (lane >> 3)][seg * 8]);
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int row = (it0 + k) * 8 + (lane >> 3);
             unsigned off;
             if constexpr (ONHWC) {
                 const int n = T.n0 + row, m = w * 64 + seg * 8;
@@ -349,12 +389,16 @@ void dcn2_fwd_rw_kernel(const RwParams p) {
             }
             // non-temporal: the output is not read again by this kernel, so
             // its lines should not push the gathered input out of the L2
-            __builtin_amdgcn_raw_buffer_store_b128(u32x4{v.x, v.y, v.z, v.w}, T.ors, (int)off, 0, 2);
+            __builtin_amdgcn_raw_buffer_store_b128(u32x4{v[k].x, v[k].y, v[k].z, v[k].w}, T.ors, (int)off, 0, 2);
         }
     };
 
     // ---------------------------------------------------------------- prologue
     Tile cur = tile_at(0), nxt = tile_at(1);
+    // the "previous tile" of the first one: an output buffer of no records,
+    // so its flush stores are dropped
+    Tile prv = cur;
+    prv.ors = __builtin_amdgcn_make_buffer_rsrc(p.out, (short)0, 0, 0x00020000);
     OmRaw om;
     load_om(cur, om);
     __syncthreads();  // sA8 and sBias written
@@ -410,31 +454,55 @@ void dcn2_fwd_rw_kernel(const RwParams p) {
             // issue while its MFMAs run.  Slice 0 issues the gathers of step
             // s+3; slices 1-3 blend the four pixel groups of step s+2.
             auto set_b = std::integral_constant<int, GB>{};
-            unsigned ro[4];
-            uint2 wt[4];
+            auto i0_c = std::integral_constant<int, 0>{};
+            auto i1_c = std::integral_constant<int, 1>{};
+            uint4 ro[2];
+            float4 wt[2];
+            float v0[4], v1[4];
+            // gathers of step s+3 go out two per slice (pixel 0 in slices 0-1,
+            // pixel 1 in slices 2-3), so the wave never blocks on a full
+            // vector-memory queue for a whole batch; each pixel's loads still
+            // have a full step before its blend (pixel 0 in slice 1, pixel 1
+            // in slices 2-3 of the next step)
+            const Tile &TI = J + 3 < kRwTaps ? cur : nxt;
+            auto set_i = std::integral_constant<int, GI>{};
+            // descriptor round J-2 of the next tile (steps 2-4): position in
+            // slice 1, offsets / weights / ring writes in slice 3
+            constexpr bool DESC = J >= 2 && J <= 4;
+            DescPos dpos;
             ring_off(ro, IP, IT);
             ring_wts(wt, BP, BT);
             __builtin_amdgcn_sched_barrier(0);
             mfma_ks(std::integral_constant<int, J>{}, std::integral_constant<int, 0>{}, bfA);
-            gather(std::integral_constant<int, GI>{}, ro, J + 3 < kRwTaps ? cur : nxt);
+            gather2(set_i, ro, TI, i0_c, i0_c);
             read_bf(bfA, SM, 2);
+            if constexpr (J == 0) flush_out(prv, 0);
             __builtin_amdgcn_sched_barrier(0);
             mfma_ks(std::integral_constant<int, J>{}, std::integral_constant<int, 1>{}, bfB);
-            blend_px(set_b, SB, wt, std::integral_constant<int, 0>{});
-            blend_px(set_b, SB, wt, std::integral_constant<int, 1>{});
+            gather2(set_i, ro, TI, i0_c, i1_c);
+            blend_half(set_b, wt, i0_c, i0_c, v0);
+            blend_half(set_b, wt, i0_c, i1_c, v1);
+            store_px(SB, i0_c, v0, v1);
             read_bf(bfB, SM, 3);
+            if constexpr (J == 0) flush_out(prv, 2);
+            if constexpr (DESC) dpos = desc_pos(J - 2, om);
             __builtin_amdgcn_sched_barrier(0);
             mfma_ks(std::integral_constant<int, J>{}, std::integral_constant<int, 2>{}, bfA);
-            blend_px(set_b, SB, wt, std::integral_constant<int, 2>{});
+            gather2(set_i, ro, TI, i1_c, i0_c);
+            blend_half(set_b, wt, i1_c, i0_c, v0);
             read_bf(bfA, SN, 0);
+            if constexpr (J == 0) flush_out(prv, 4);
             __builtin_amdgcn_sched_barrier(0);
             mfma_ks(std::integral_constant<int, J>{}, std::integral_constant<int, 3>{}, bfB);
-            blend_px(set_b, SB, wt, std::integral_constant<int, 3>{});
+            gather2(set_i, ro, TI, i1_c, i1_c);
+            blend_half(set_b, wt, i1_c, i1_c, v1);
+            store_px(SB, i1_c, v0, v1);
             read_bf(bfB, SN, 1);
-            if constexpr (J >= 2 && J <= 4) put_desc(P ^ 1, J - 2, om);
+            if constexpr (J == 0) flush_out(prv, 6);
+            if constexpr (DESC) desc_put(P ^ 1, J - 2, dpos);
             __builtin_amdgcn_sched_barrier(0);
             if constexpr (J == kRwTaps - 1) {
-                store_tile(cur);
+                stage_out();
                 init_acc();
             }
             __syncthreads();
@@ -452,31 +520,36 @@ void dcn2_fwd_rw_kernel(const RwParams p) {
     int k = 0;
     for (; k + 2 <= my_tiles; k += 2) {
         tile(std::integral_constant<int, 0>{});
+        prv = cur;
         cur = nxt;
         nxt = tile_at(k + 2);
         load_om(nxt, om);
         tile(std::integral_constant<int, 1>{});
+        prv = cur;
         cur = nxt;
         nxt = tile_at(k + 3);
         load_om(nxt, om);
     }
-    if (k < my_tiles) tile(std::integral_constant<int, 0>{});
+    if (k < my_tiles) {
+        tile(std::integral_constant<int, 0>{});
+        prv = cur;
+    }
+    // the last tile's output (staged at its last step)
+#pragma unroll
+    for (int it = 0; it < 8; it += 2) flush_out(prv, it);
 }
 
 bool rw_eligible(const Geo &g) {
     return g.dtype == DCN2_F16 && g.G == 1 && g.Cgp == 64 && g.KK == kRwTaps && g.Mp == 256 &&
            g.WG == 1 && (g.out_nhwc ? g.Cout % 8 == 0 : g.N % 8 == 0) &&
-           (long long)(g.H + 2) * (g.W + 1) * 256 < 0x7fffffffLL &&
            (long long)g.Cout * g.N * 2 < 0x7fffffffLL;
 }
 
-size_t rw_input_bytes(const Geo &g) { return (size_t)g.B * (g.H + 2) * (g.W + 1) * 256; }
-
-hipError_t launch_forward_rw(const Geo &g, const void *xp, const void *wp, const void *offset,
+hipError_t launch_forward_rw(const Geo &g, const void *xt, const void *wp, const void *offset,
                              const void *mask, const void *bias, void *out, hipStream_t s) {
     if (g.B == 0) return hipSuccess;
     RwParams p;
-    p.xp = xp;
+    p.xt = xt;
     p.wp = wp;
     p.offset = offset;
     p.mask = mask;
@@ -495,8 +568,7 @@ hipError_t launch_forward_rw(const Geo &g, const void *xp, const void *wp, const
     p.dw = g.dw;
     p.ntiles = ceil_div(g.N, kRwPx);
     p.tiles = g.B * p.ntiles;
-    p.img_bytes = (unsigned)((size_t)(g.H + 2) * (g.W + 1) * 256);
-    p.row_bytes = (unsigned)((g.W + 1) * 256);
+    p.img_bytes = (unsigned)((size_t)g.H * g.W * 128);
     p.out_img_bytes = (unsigned)((size_t)g.Cout * g.N * 2);
     p.off_bs = g.off_bs;
     p.msk_bs = g.msk_bs;

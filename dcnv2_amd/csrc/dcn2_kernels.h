@@ -38,8 +38,8 @@ struct Geo {
     // sigmoid (the offset-and-mask predictor's raw output, dcn2_*_om).
     long long off_bs, msk_bs;
     int msk_logit;
-    // The forward runs dcn2_fwd_rw_kernel (weight resident in registers, input
-    // in the pixel-pair layout) instead of the chunk-streaming kernels.
+    // The forward runs dcn2_fwd_rw_kernel (weight resident in registers)
+    // instead of the chunk-streaming kernels.
     int rw;
 };
 
@@ -97,12 +97,11 @@ hipError_t launch_forward(const Geo &g, const void *xt, const void *wp, const vo
                           const void *offset, const void *mask, const void *bias, void *out,
                           hipStream_t s);
 
-// dcn2_forward_rw.hip: the resident-weight forward, its eligibility (f16,
+// dcn2_forward_rw.hip: the resident-weight forward and its eligibility (f16,
 // one deformable group of <= 64 channels, 3x3, 128 < Cout <= 256, no weight
-// groups) and the bytes of its pixel-pair input.
+// groups).
 bool rw_eligible(const Geo &g);
-size_t rw_input_bytes(const Geo &g);
-hipError_t launch_forward_rw(const Geo &g, const void *xp, const void *wp, const void *offset,
+hipError_t launch_forward_rw(const Geo &g, const void *xt, const void *wp, const void *offset,
                              const void *mask, const void *bias, void *out, hipStream_t s);
 
 // dcn2_backward.hip

@@ -33,9 +33,6 @@ struct PackParams {
     int kc, kstep, kpl, Mp, Kp;    // MFMA packing
     int transpose;                 // 0: forward A fragments, 1: backward W'^T fragments
     int nhwc;                      // input is channels-last [B][HW][C]
-    int pairs;                     // input -> pixel-pair layout (see pack_input_pairs)
-    int H, W, pjt;                 // pairs: image size and 64-pair blocks per row
-    int pair_vec;                  // pairs: 16-byte loads of 8 columns (NCHW) / channels (NHWC)
     int nw;                        // weight blocks
     float4 *clr[3];                // buffers to zero, 16-byte pieces each
     long clr_n4[3];
@@ -121,84 +118,6 @@ __device__ __forceinline__ void pack_input_block(const PackParams &p, int blk) {
         for (int e = 0; e < E; ++e) v[e] = tile[cg + e][((pl / E) ^ (((cg + e) / E) & 7)) * E + pl % E];
         *reinterpret_cast<uint4 *>(xt + ((size_t)b * p.HW + px0 + pl) * p.cs + cp0 + cg) =
             __builtin_bit_cast(uint4, v);
-    }
-}
-
-// Pixel-pair layout of the resident-weight forward (dcn2_forward_rw.hip):
-// xp[b][yy][j][c][2], yy in [0, H+2), j in [0, W], c in [0, 64): the channel-c
-// values of pixels (yy-1, j-1) and (yy-1, j), zero outside the image (so rows
-// 0 and H+1 and the pair halves at x = -1 and x = W are zero).  Every byte of
-// every image is written.  A row of W+1 pairs is cut into pjt = max(1,
-// (W+1)/64) blocks of 64 pairs, the last one taking the remainder (< 128).
-// A block stages its input columns x = j0-1 .. j1-1 of all 64 channels in LDS
-// as [column][channel] and writes each pair as a 16-byte piece of 4 channels x
-// 2 pixels.  NCHW rows are read with 16-byte loads of 8 columns (lane =
-// channel), channels-last pixels with 16-byte loads of 8 channels.
-constexpr int kPairCols = 129;  // most input columns a block stages (127 pairs + 1)
-template <typename T>
-__device__ __forceinline__ void pack_input_pairs(const PackParams &p, int blk) {
-    constexpr int LDC = 72;  // LDS pitch (elements) of one column: 144 bytes
-    __shared__ __attribute__((aligned(16))) T tl[kPairCols][LDC];
-    const T *__restrict__ in = (const T *)p.in;
-    const int jc = blk % p.pjt, r = blk / p.pjt;
-    const int yy = r % (p.H + 2), b = r / (p.H + 2);
-    const int y = yy - 1;
-    const int j0 = jc * 64, j1 = jc + 1 == p.pjt ? p.W + 1 : j0 + 64;  // pairs [j0, j1)
-    const int ncol = j1 - j0 + 1;                                       // columns j0-1 .. j1-1
-    const bool yin = (unsigned)y < (unsigned)p.H;
-    const int tid = threadIdx.x;
-    if (p.nhwc) {
-        // column xi (x = j0-1+xi), channel group cg of 8
-        for (int idx = tid; idx < ncol * 8; idx += 256) {
-            const int xi = idx >> 3, cg = idx & 7, x = j0 - 1 + xi;
-            uint4 v = make_uint4(0, 0, 0, 0);
-            if (yin && (unsigned)x < (unsigned)p.W) {
-                const T *src = in + (((size_t)b * p.H + y) * p.W + x) * p.C + cg * 8;
-                if (p.pair_vec && cg * 8 + 8 <= p.C) {
-                    v = *reinterpret_cast<const uint4 *>(src);
-                } else {
-                    T e8[8];
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) e8[e] = cg * 8 + e < p.C ? src[e] : (T)0.0f;
-                    v = __builtin_bit_cast(uint4, e8);
-                }
-            }
-            *reinterpret_cast<uint4 *>(&tl[xi][cg * 8]) = v;
-        }
-    } else {
-        // channel c = lane, 8 columns per load; the column j0-1 separately
-        const int c = tid & 63;
-        const bool cin = yin && c < p.C;
-        const T *row = in + (((size_t)b * p.C + (c < p.C ? c : 0)) * p.H + (yin ? y : 0)) * p.W;
-        for (int g = tid >> 6; g * 8 < ncol - 1; g += 4) {
-            const int x = j0 + g * 8;  // columns x .. x+7 -> xi = 1 + g*8 ..
-            T e8[8];
-            if (cin && p.pair_vec && x + 8 <= p.W) {
-                *reinterpret_cast<uint4 *>(e8) = *reinterpret_cast<const uint4 *>(row + x);
-            } else {
-#pragma unroll
-                for (int e = 0; e < 8; ++e) e8[e] = (cin && x + e < p.W) ? row[x + e] : (T)0.0f;
-            }
-#pragma unroll
-            for (int e = 0; e < 8; ++e)
-                if (1 + g * 8 + e < ncol) tl[1 + g * 8 + e][c] = e8[e];
-        }
-        if (tid < 64) tl[0][c] = (cin && j0 >= 1) ? row[j0 - 1] : (T)0.0f;
-    }
-    __syncthreads();
-    T *__restrict__ xp = (T *)p.xt + ((size_t)b * (p.H + 2) + yy) * (size_t)(p.W + 1) * 128;
-    const int npc = (j1 - j0) * 16;  // 16-byte pieces of the block
-    for (int idx = tid; idx < npc; idx += 256) {
-        const int jj = idx >> 4, pc = idx & 15;
-        const uint2 a = *reinterpret_cast<const uint2 *>(&tl[jj][4 * pc]);      // x = j-1
-        const uint2 c2 = *reinterpret_cast<const uint2 *>(&tl[jj + 1][4 * pc]); // x = j
-        // interleave: (a.c0, c2.c0), (a.c1, c2.c1), ...
-        uint4 v;
-        v.x = __builtin_amdgcn_perm(c2.x, a.x, 0x05040100u);
-        v.y = __builtin_amdgcn_perm(c2.x, a.x, 0x07060302u);
-        v.z = __builtin_amdgcn_perm(c2.y, a.y, 0x05040100u);
-        v.w = __builtin_amdgcn_perm(c2.y, a.y, 0x07060302u);
-        *reinterpret_cast<uint4 *>(xp + (size_t)(j0 + jj) * 128 + pc * 8) = v;
     }
 }
 
@@ -292,12 +211,6 @@ __global__ __launch_bounds__(256) void pack_kernel(const PackParams p) {
     if (blk < p.nw) {
         pack_weight_block<T>(p, blk);
     } else if (blk < p.nw + p.nin) {
-        if constexpr (sizeof(T) == 2) {
-            if (p.pairs) {
-                pack_input_pairs<T>(p, blk - p.nw);
-                return;
-            }
-        }
         if (p.nhwc)
             pack_input_block_nhwc<T>(p, blk - p.nw);
         else
@@ -347,13 +260,6 @@ static hipError_t pack_t(const Geo &g, const void *input, void *xt, const void *
     p.Kp = g.Kp;
     p.transpose = transpose ? 1 : 0;
     p.nhwc = g.nhwc;
-    // the resident-weight forward reads the pixel-pair layout
-    p.pairs = (g.rw && !transpose) ? 1 : 0;
-    p.H = g.H;
-    p.W = g.W;
-    p.pjt = (g.W + 1) / 64 > 1 ? (g.W + 1) / 64 : 1;
-    p.pair_vec = (g.nhwc ? g.C % 8 == 0 : g.W % 8 == 0) && (((uintptr_t)input & 15) == 0);
-    if (p.pairs && input) p.nin = g.B * (g.H + 2) * p.pjt;
     // one thread per 16-byte piece of the packed weight (Mp*Kp is a multiple of 16/esz)
     const long nw = ((long)g.Mp * g.Kp / E + 255) / 256;
     p.nw = (int)nw;
