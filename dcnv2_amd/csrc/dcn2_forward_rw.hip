@@ -248,7 +248,7 @@ void dcn2_fwd_rw_kernel(const RwParams p) {
 #pragma unroll
         for (int c = 0; c < 4; ++c) v[c] = 0.0f;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
+        for (int q = 3; q >= 0; --q) {  // the last-issued corner first: one wait covers all four
             const uint4 r = gx[SET][4 * i + q];
             const unsigned u[2] = {h ? r.z : r.x, h ? r.w : r.y};
 #pragma unroll
@@ -308,7 +308,11 @@ void dcn2_fwd_rw_kernel(const RwParams p) {
             typedef unsigned long long u64x8 __attribute__((ext_vector_type(8)));
 #pragma unroll
             for (int rb = 0; rb < 2; ++rb) {
-                const uint32_t bb = __float_as_uint(bias_r[rb]);
+                // (the empty asm keeps the compiler from hoisting the 32-register
+                // bias image out of the loop and holding it for the whole kernel)
+                float br = bias_r[rb];
+                asm volatile("" : "+v"(br));
+                const uint32_t bb = __float_as_uint(br);
                 const unsigned long long b2 = ((unsigned long long)bb << 32) | bb;
 #pragma unroll
                 for (int pb = 0; pb < 2; ++pb) acc[rb][pb] = __builtin_bit_cast(f32x16, u64x8(b2));
