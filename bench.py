@@ -220,6 +220,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--mode", choices=("full", "fwd", "c2", "c3", "c4"), default="full")
     ap.add_argument("--copy-mib", type=int, default=0)
+    ap.add_argument("--bwd-slice-mib", type=int, default=0,
+                    help="backward workspace budget per slice of images (0: library default)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU; the batch-sharded multi-GPU path is "
@@ -248,6 +250,9 @@ def main():
             _C.dcn_v2_forward(*args5, *_geo(w))
             return _C.dcn_v2_backward(*args5, t["grad_output"], *_geo(w))
         return f
+
+    if args.bwd_slice_mib:
+        _C.set_option("bwd_slice_bytes", args.bwd_slice_mib << 20)
 
     if args.copy_mib:
         n = args.copy_mib << 20

@@ -88,6 +88,10 @@ def lib() -> ctypes.CDLL:
             L.dcn2_profile_read.argtypes = [ctypes.c_int, ctypes.POINTER(ctypes.c_double),
                                             ctypes.POINTER(ctypes.c_int)]
             L.dcn2_profile_read.restype = ctypes.c_int
+            L.dcn2_set_option.argtypes = [ctypes.c_int, ctypes.c_int64]
+            L.dcn2_set_option.restype = ctypes.c_int
+            L.dcn2_get_option.argtypes = [ctypes.c_int]
+            L.dcn2_get_option.restype = ctypes.c_int64
             _lib = L
     return _lib
 
@@ -335,6 +339,39 @@ def dcn_v2_backward_om(input, weight, om, bias, grad_output, stride_h, stride_w,
 
 def version() -> str:
     return lib().dcn2_version().decode()
+
+
+# process-wide options of the library (enum dcn2_option)
+OPTIONS = ("bwd_slice_bytes", "bwd_fused", "gi_push")
+
+
+def set_option(name: str, value: int) -> None:
+    """bwd_slice_bytes: backward workspace budget per slice of images;
+    bwd_fused: -1 automatic, 0 never the fused backward kernel; gi_push: -1
+    automatic, 0 per-pixel grad_input, 1 by cells."""
+    if lib().dcn2_set_option(OPTIONS.index(name), int(value)) != 0:
+        raise _err("set_option")
+
+
+def get_option(name: str) -> int:
+    return int(lib().dcn2_get_option(OPTIONS.index(name)))
+
+
+class option:
+    """Context manager: `with option("gi_push", 0): ...` sets an option and
+    restores its previous value on exit."""
+
+    def __init__(self, name: str, value: int):
+        self.name, self.value = name, value
+
+    def __enter__(self):
+        self.prev = get_option(self.name)
+        set_option(self.name, self.value)
+        return self
+
+    def __exit__(self, *exc):
+        set_option(self.name, self.prev)
+        return False
 
 
 STAGES = ("fwd_pack", "fwd_main", "bwd_pack", "bwd_colgrad", "bwd_gradw", "bwd_gather",

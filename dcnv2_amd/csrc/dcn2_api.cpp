@@ -8,6 +8,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
 #include <string>
@@ -20,6 +21,10 @@
 namespace dcn2 {
 
 static thread_local std::string g_last_error;
+
+// process-wide options (dcn2_set_option)
+static std::atomic<long long> g_opt_slice_bytes{DCN2_BWD_SLICE_BYTES_DEFAULT};
+static std::atomic<int> g_opt_fused{-1}, g_opt_push{-1};
 
 int fail(int code, const char *fmt, ...) {
     char buf[512];
@@ -81,6 +86,10 @@ int make_geo(const dcn2_desc *d, Geo &g) {
     if (g.H + 2 * g.ph < g.dh * (g.kh - 1) + 1 || g.W + 2 * g.pw < g.dw * (g.kw - 1) + 1 ||
         g.Ho <= 0 || g.Wo <= 0)
         return fail(DCN2_EINVAL, "dcn2: empty output (%d x %d)", g.Ho, g.Wo);
+    g.slice_bytes = g_opt_slice_bytes.load(std::memory_order_relaxed);
+    g.opt_fused = g_opt_fused.load(std::memory_order_relaxed);
+    g.opt_push = g_opt_push.load(std::memory_order_relaxed);
+    g.Bs = g.B;
     g.esz = g.dtype == DCN2_F32 ? 4 : 2;
     g.KC = g.dtype == DCN2_F32 ? 32 : 64;
     g.Cg = g.C / g.G;
@@ -166,11 +175,14 @@ FwdWorkspace fwd_workspace(const Geo &g) {
     return w;
 }
 
-BwdWorkspace bwd_workspace(const Geo &g) {
+BwdWorkspace bwd_workspace(const Geo &g0) {
+    Geo g = g0;
+    g.B = g0.Bs;
     BwdWorkspace w;
     size_t o = 0;
     w.xt = o;
-    if (!g.xt_direct) o += align256((size_t)g.B * g.H * g.W * g.cs * g.esz);
+    const size_t xt_bytes = g.xt_direct ? 0 : align256((size_t)g.B * g.H * g.W * g.cs * g.esz);
+    o += xt_bytes;
     w.wt = o;
     o += align256((size_t)g.Mp * g.Kp * g.esz);
     w.tab = o;
@@ -184,6 +196,8 @@ BwdWorkspace bwd_workspace(const Geo &g) {
     o += align256((size_t)g.Mp * sizeof(float));
     w.cgm = o;
     o += align256((size_t)gg.rows * g.Cgp * gg.row_esz);
+    w.rsc = o;
+    if (gg.row_scaled) o += align256((size_t)gg.rows * (g.Cgp / 32));
     w.rec = o;
     o += align256((size_t)gg.rows * 12);  // 12-byte sample records
     w.bcnt = o;
@@ -194,10 +208,39 @@ BwdWorkspace bwd_workspace(const Geo &g) {
     o += align256((size_t)gg.nbuckets * sizeof(int));
     w.sidx = o;
     o += align256((size_t)g.B * g.G * g.KK * g.N * sizeof(int));
-    w.ring = o;
-    o += align256((size_t)gg.nbuckets * kGatherRing * g.Cgp * sizeof(float));
+    // The border rings are written after the last read of xt (the
+    // grad_weight kernels and the column-gradient kernels run before the
+    // grad_input kernels), so they share xt's bytes when they fit there.
+    const size_t ring_bytes = align256((size_t)gg.nbuckets * kGatherRing * g.Cgp * sizeof(float));
+    if (ring_bytes <= xt_bytes) {
+        w.ring = w.xt;
+    } else {
+        w.ring = o;
+        o += ring_bytes;
+    }
     w.total = o;
     return w;
+}
+
+// Images per backward slice: the largest count whose workspace fits the
+// slice budget (at least one), then evened out over the slices that count
+// implies (B = 16 with room for 6 runs as 6 + 5 + 5, not 6 + 6 + 4).
+static int bwd_slice_images(const Geo &g) {
+    auto bytes = [&](int b) {
+        Geo t = g;
+        t.Bs = b;
+        return bwd_workspace(t).total;
+    };
+    const size_t budget = (size_t)std::max(1LL, g.slice_bytes);
+    if (g.B <= 1 || bytes(g.B) <= budget) return g.B;
+    int lo = 1, hi = g.B;  // bytes(lo) fits or lo == 1; bytes(hi) does not
+    while (hi - lo > 1) {
+        const int mid = lo + (hi - lo) / 2;
+        if (bytes(mid) <= budget) lo = mid;
+        else hi = mid;
+    }
+    const int nslices = (g.B + lo - 1) / lo;
+    return (g.B + nslices - 1) / nslices;
 }
 
 static int check_launch(hipError_t e, const char *what) {
@@ -246,7 +289,7 @@ int forward_impl(const Geo &g, const void *input, const void *weight, const void
     return rc;
 }
 
-static int backward_impl(const Geo &g, const void *input, const void *weight, const void *mask,
+static int backward_impl(const Geo &g0, const void *input, const void *weight, const void *mask,
                          const void *offset, const void *grad_output, void *grad_input,
                          void *grad_offset, void *grad_mask, void *grad_weight, void *grad_bias,
                          void *workspace, size_t workspace_bytes, void *stream) {
@@ -254,10 +297,12 @@ static int backward_impl(const Geo &g, const void *input, const void *weight, co
 
     if (!weight || !grad_weight)
         return fail(DCN2_EINVAL, "dcn2_backward: null weight/grad_weight pointer");
-    if (g.B > 0 && (!input || !offset || !grad_output || !grad_input || !grad_offset))
+    if (g0.B > 0 && (!input || !offset || !grad_output || !grad_input || !grad_offset))
         return fail(DCN2_EINVAL, "dcn2_backward: null input/offset/grad pointer");
     if ((mask == nullptr) != (grad_mask == nullptr))
         return fail(DCN2_EINVAL, "dcn2_backward: grad_mask must be given exactly when mask is");
+    Geo g = g0;
+    g.Bs = bwd_slice_images(g0);
     const BwdWorkspace ws = bwd_workspace(g);
     if (!workspace || workspace_bytes < ws.total || ((uintptr_t)workspace & 255))
         return fail(DCN2_EWORKSPACE,
@@ -267,33 +312,57 @@ static int backward_impl(const Geo &g, const void *input, const void *weight, co
         return fail(DCN2_EINVAL, "dcn2_backward: a channels-last input must be 16-byte aligned");
     hipStream_t s = (hipStream_t)stream;
     char *base = (char *)workspace;
-    const void *xt = g.xt_direct ? input : base + ws.xt;
     void *wt = base + ws.wt, *tab = base + ws.tab;
-    // the pack launch also zeroes the grad_weight / grad_bias accumulators and
-    // the bucket counts
-    const GatherGeo gg = gather_geometry(g);
-    ClearList clr;
-    clr.p[0] = (float *)(base + ws.gw_acc);
-    clr.n[0] = (size_t)g.Mp * g.Kp;
-    clr.p[1] = (float *)(base + ws.gb_acc);
-    clr.n[1] = grad_bias ? (size_t)g.Mp : 0;
-    // (bcnt, bstart and bcur are adjacent: the place pass that scans the
-    // counts itself claims rows from bcur = 0)
-    clr.p[2] = (float *)(base + ws.bcnt);
-    clr.n[2] = g.B > 0 ? (ws.bcur - ws.bcnt) / sizeof(int) + (size_t)gg.nbuckets : 0;
-    prof_begin(DCN2_STAGE_BWD_PACK, s);
-    if ((rc = check_launch(launch_pack(g, g.xt_direct ? nullptr : input, (void *)xt, weight, wt,
-                                       tab, true, s, &clr), "pack")))
-        return rc;
-    prof_end(DCN2_STAGE_BWD_PACK, s);
-    return check_launch(launch_backward(g, xt, wt, tab, offset, mask, grad_output,
-                                        grad_input, grad_offset, grad_mask, grad_weight,
-                                        grad_bias, (float *)(base + ws.gi_acc),
-                                        (float *)(base + ws.gw_acc), (float *)(base + ws.gb_acc),
-                                        base + ws.cgm, base + ws.rec, (int *)(base + ws.bcnt),
-                                        (int *)(base + ws.bstart), (int *)(base + ws.bcur),
-                                        (int *)(base + ws.sidx), (float *)(base + ws.ring), s),
-                        "backward");
+    // Slices of g.Bs images (the last may hold fewer), each on the same
+    // workspace in stream order: its pack launch transposes the slice's input
+    // and zeroes the bucket counts (the first one also packs the weight and
+    // zeroes the grad_weight / grad_bias accumulators, which every slice adds
+    // to); the last slice writes grad_weight / grad_bias.  An empty batch is
+    // one slice of no images.
+    const size_t esz = g.esz;
+    const size_t in_img = (size_t)g.C * g.H * g.W * esz, go_img = (size_t)g.Cout * g.N * esz;
+    const size_t off_img = (size_t)g.off_bs * esz, msk_img = (size_t)g.msk_bs * esz;
+    int b0 = 0;
+    do {
+        Geo gs = g;
+        gs.B = std::min(g.Bs, g.B - b0);
+        gs.Bs = gs.B;
+        const bool first = b0 == 0, last = b0 + gs.B >= g.B;
+        auto at = [&](const void *ptr, size_t img) -> const char * {
+            return ptr ? (const char *)ptr + (size_t)b0 * img : nullptr;
+        };
+        const void *in_s = at(input, in_img);
+        const void *xt = g.xt_direct ? in_s : base + ws.xt;
+        const GatherGeo gg = gather_geometry(gs);
+        ClearList clr;
+        clr.p[0] = (float *)(base + ws.gw_acc);
+        clr.n[0] = first ? (size_t)g.Mp * g.Kp : 0;
+        clr.p[1] = (float *)(base + ws.gb_acc);
+        clr.n[1] = first && grad_bias ? (size_t)g.Mp : 0;
+        // (bcnt, bstart and bcur are adjacent: the place pass that scans the
+        // counts itself claims rows from bcur = 0)
+        clr.p[2] = (float *)(base + ws.bcnt);
+        clr.n[2] = gs.B > 0 ? (ws.bcur - ws.bcnt) / sizeof(int) + (size_t)gg.nbuckets : 0;
+        prof_begin(DCN2_STAGE_BWD_PACK, s);
+        if ((rc = check_launch(launch_pack(gs, g.xt_direct ? nullptr : in_s, (void *)xt,
+                                           first ? weight : nullptr, wt, tab, true, s, &clr),
+                               "pack")))
+            return rc;
+        prof_end(DCN2_STAGE_BWD_PACK, s);
+        if ((rc = check_launch(
+                 launch_backward(gs, xt, wt, tab, at(offset, off_img), at(mask, msk_img),
+                                 at(grad_output, go_img), (void *)at(grad_input, in_img),
+                                 (void *)at(grad_offset, off_img), (void *)at(grad_mask, msk_img),
+                                 grad_weight, grad_bias, (float *)(base + ws.gi_acc),
+                                 (float *)(base + ws.gw_acc), (float *)(base + ws.gb_acc),
+                                 base + ws.cgm, base + ws.rsc, base + ws.rec, (int *)(base + ws.bcnt),
+                                 (int *)(base + ws.bstart), (int *)(base + ws.bcur),
+                                 (int *)(base + ws.sidx), (float *)(base + ws.ring), last, s),
+                 "backward")))
+            return rc;
+        b0 += gs.B;
+    } while (b0 < g.B);
+    return DCN2_OK;
 }
 
 
@@ -321,7 +390,40 @@ size_t dcn2_forward_workspace_bytes(const dcn2_desc *d) {
 size_t dcn2_backward_workspace_bytes(const dcn2_desc *d) {
     Geo g;
     if (make_geo(d, g)) return 0;
+    g.Bs = bwd_slice_images(g);
     return bwd_workspace(g).total;
+}
+
+int dcn2_set_option(int option, int64_t value) {
+    switch (option) {
+    case DCN2_OPT_BWD_SLICE_BYTES:
+        if (value < 1) return fail(DCN2_EINVAL, "dcn2_set_option: slice budget %lld < 1", (long long)value);
+        g_opt_slice_bytes.store(value, std::memory_order_relaxed);
+        return DCN2_OK;
+    case DCN2_OPT_BWD_FUSED:
+        if (value != -1 && value != 0)
+            return fail(DCN2_EINVAL, "dcn2_set_option: DCN2_OPT_BWD_FUSED takes -1 or 0, not %lld",
+                        (long long)value);
+        g_opt_fused.store((int)value, std::memory_order_relaxed);
+        return DCN2_OK;
+    case DCN2_OPT_GI_PUSH:
+        if (value < -1 || value > 1)
+            return fail(DCN2_EINVAL, "dcn2_set_option: DCN2_OPT_GI_PUSH takes -1, 0 or 1, not %lld",
+                        (long long)value);
+        g_opt_push.store((int)value, std::memory_order_relaxed);
+        return DCN2_OK;
+    default:
+        return fail(DCN2_EINVAL, "dcn2_set_option: unknown option %d", option);
+    }
+}
+
+int64_t dcn2_get_option(int option) {
+    switch (option) {
+    case DCN2_OPT_BWD_SLICE_BYTES: return g_opt_slice_bytes.load(std::memory_order_relaxed);
+    case DCN2_OPT_BWD_FUSED: return g_opt_fused.load(std::memory_order_relaxed);
+    case DCN2_OPT_GI_PUSH: return g_opt_push.load(std::memory_order_relaxed);
+    default: return -2;
+    }
 }
 
 

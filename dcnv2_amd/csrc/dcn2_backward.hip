@@ -59,7 +59,8 @@ struct BwdParams {
     // rows of all buckets are packed back to back, bucket k owning rows
     // [bstart[k], bstart[k+1]); there are at most B*G*KK*N of them (one per
     // sample), so the storage is sized exactly and no bucket can overflow.
-    void *cgm;          // [rows][Cgp] masked column gradient rows, call dtype
+    void *cgm;          // [rows][Cgp] masked column gradient rows (RowOf)
+    unsigned char *rsc; // [rows][Cgp/32] scale codes of bf16 rows (row_block_scale)
     struct BucketRec *rec;  // [rows] sample records, in bucket order
     int *bcnt;          // [nbuckets] samples per bucket (count pass)
     int *bstart;        // [nbuckets + 1] first row of each bucket (exclusive scan of bcnt)
@@ -106,12 +107,46 @@ __device__ __forceinline__ int gw_chunk(const BwdParams &p, int j, int m0) {
 }
 
 // Element type of the masked column-gradient rows the column-gradient kernel
-// hands to the grad_input gather: fp32 for bf16, whose 8-bit mantissa would
-// add a rounding that the reference's fp32 col2im (com.cu:553-609) does not
-// have, and the call type otherwise.
+// hands to the grad_input gather: the call type, except bf16, whose 8-bit
+// significand would add a rounding that the reference's fp32 col2im
+// (com.cu:553-609) does not have.  bf16 rows are fp16 with one power-of-two
+// scale per 32 channels (block floating point, kRowScaled): the largest
+// magnitude of the 32 is brought to [2^14, 2^15) before the rounding to fp16,
+// so every value keeps an 11-bit significand down to 2^-14 of its block's
+// largest (subnormal below), and the block's exponent spans bf16's range.
+// The scale codes live in BwdParams::rsc, one byte per 32 channels of a row.
 template <typename T> struct RowOf { typedef T type; };
-template <> struct RowOf<bf16> { typedef float type; };
-constexpr int row_elem_bytes(int dtype) { return dtype == DCN2_F32 || dtype == DCN2_BF16 ? 4 : 2; }
+template <> struct RowOf<bf16> { typedef f16 type; };
+template <typename T> constexpr bool kRowScaled = std::is_same<T, bf16>::value;
+constexpr int row_elem_bytes(int dtype) { return dtype == DCN2_F32 ? 4 : 2; }
+constexpr bool row_scaled(int dtype) { return dtype == DCN2_BF16; }
+
+// Value of lane l ^ 1 / l ^ 2 (within each group of 4 lanes), by DPP quad permutes.
+__device__ __forceinline__ float quad_xor1(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, true));
+}
+__device__ __forceinline__ float quad_xor2(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, true));
+}
+
+// Scale of one 32-channel block of a bf16 hand-off row, held by a quad of
+// lanes with 8 values each (every lane of the quad calls this).  Returns the
+// factor 2^s the values are multiplied by before the rounding to fp16, s =
+// min(141 - e, 127) for the biased exponent e of the block's largest
+// magnitude, and sets `code` = 127 - s, from which the consumers rebuild
+// 2^-s (row_unscale; a block below 2^-113 gets code 0, read back as 0).
+// NaN values stay NaN (fmaxf skips them) and infinities stay infinite.
+__device__ __forceinline__ float row_block_scale(const float (&v)[8], unsigned &code) {
+    float mx = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf(v[e]));
+    mx = fmaxf(mx, quad_xor1(mx));
+    mx = fmaxf(mx, quad_xor2(mx));
+    const int sc = min(141 - (int)(__float_as_uint(mx) >> 23), 127);
+    code = (unsigned)(127 - sc);
+    return __int_as_float((sc + 127) << 23);
+}
+__device__ __forceinline__ float row_unscale(unsigned code) { return __int_as_float(code << 23); }
 
 // Buffer offset at or past one image's gO bytes (a load there reads 0); the
 // kernels that read gO through it require Cout*N*sizeof(T) <= kGoOutOfRange.
@@ -844,6 +879,17 @@ __global__ __launch_bounds__(512) void dcn2_colgrad_kernel(const BwdParams p) {
             uint4 *row = reinterpret_cast<uint4 *>((R *)p.cgm + (size_t)d.sidx * p.Cgp + id.cc * KC +
                                                    co * EPL);
             uint4 *dst = in && d.mode == 1 ? row : trash_v;
+            if constexpr (kRowScaled<T>) {
+                // lanes co 0-3 / 4-7 (quads) hold the chunk row's two 32-channel blocks
+                unsigned code;
+                const float f = row_block_scale(mv8, code);
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) mv8[e] *= f;
+                unsigned char *sc = in && d.mode == 1 && (co & 3) == 0
+                                        ? p.rsc + (size_t)d.sidx * (p.Cgp / 32) + id.cc * 2 + (co >> 2)
+                                        : reinterpret_cast<unsigned char *>(trash_v) + 8;
+                *sc = (unsigned char)code;
+            }
 #pragma unroll
             for (int i = 0; i < NST; ++i) dst[i] = pack16<R>(mv8 + i * (16 / sizeof(R)));
         }
@@ -1448,13 +1494,6 @@ __device__ __forceinline__ int fused_swz_c(int n) { return ((n & 3) << 1) | ((n 
 // Trash bytes each lane of the fused kernel may write (its widest hand-off row).
 constexpr int kFusedTrashLane = 32;
 
-// Value of lane l ^ 1 / l ^ 2 (within each group of 4 lanes), by DPP quad permutes.
-__device__ __forceinline__ float quad_xor1(float v) {
-    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, true));
-}
-__device__ __forceinline__ float quad_xor2(float v) {
-    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, true));
-}
 
 template <typename T, bool GN>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
@@ -1789,6 +1828,16 @@ void dcn2_bwd_fused_kernel(const BwdParams p) {
             uint4 *row = srow >= 0
                              ? reinterpret_cast<uint4 *>((R *)p.cgm + (size_t)srow * KC + kb * 32 + cq * E)
                              : trash_v;
+            if constexpr (kRowScaled<T>) {
+                // the pixel's quad of lanes holds 32-channel block kb of the row
+                unsigned code;
+                const float f = row_block_scale(mrow, code);
+#pragma unroll
+                for (int e = 0; e < E; ++e) mrow[e] *= f;
+                unsigned char *sc = srow >= 0 && cq == 0 ? p.rsc + (size_t)srow * (KC / 32) + kb
+                                                         : reinterpret_cast<unsigned char *>(trash_v) + 8;
+                *sc = (unsigned char)code;
+            }
 #pragma unroll
             for (int u = 0; u < NST; ++u) row[u] = pack16<R>(mrow + u * (16 / sizeof(R)));
         }
@@ -2024,8 +2073,10 @@ constexpr int kGatherBatch = 4096;  // records of one batch the LDS sort holds
 // below it), so a load there reads 0.
 constexpr int kGatherOutOfRange = 0x7ffffff0;
 // static LDS of dcn2_gi_gather_kernel: cell counts and starts, sorted slots and fractions
+// (plus the sorted scale codes of bf16 rows)
 constexpr int kGatherStaticLds = kCellTile * kCellTile * 4 + (kCellTile * kCellTile + 1) * 4 +
                                  kGatherBatch * 2 + kGatherBatch * 8;
+constexpr int gather_static_lds(bool scaled) { return kGatherStaticLds + (scaled ? kGatherBatch * 2 : 4); }
 
 template <typename T>
 __global__ __launch_bounds__(512) void dcn2_gi_gather_kernel(const BwdParams p) {
@@ -2036,7 +2087,9 @@ __global__ __launch_bounds__(512) void dcn2_gi_gather_kernel(const BwdParams p) 
     __shared__ int cstart[NCELL + 1];
     __shared__ unsigned short sslot[kGatherBatch];    // row in the batch, sorted by cell
     __shared__ float2 sfrac[kGatherBatch];            // (ly, lx), sorted by cell
-    static_assert(sizeof(ccnt) + sizeof(cstart) + sizeof(sslot) + sizeof(sfrac) == kGatherStaticLds,
+    __shared__ unsigned short ssc[kRowScaled<T> ? kGatherBatch : 2];  // bf16 rows: the chunk's scale codes
+    static_assert(sizeof(ccnt) + sizeof(cstart) + sizeof(sslot) + sizeof(sfrac) + sizeof(ssc) ==
+                      gather_static_lds(kRowScaled<T>),
                   "the launch's occupancy cap assumes this static LDS");
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -2126,7 +2179,17 @@ __global__ __launch_bounds__(512) void dcn2_gi_gather_kernel(const BwdParams p) 
         typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
         const int co = lane % LPR, ps = lane / LPR;
         const int row_bytes = p.Cgp * (int)sizeof(R);
+        // bf16 rows: this lane's 8 channels lie in 32-channel block co / 4 of the chunk
+        const int sc_shift = 8 * (co >> 2);
         for (int cc = 0; cc < cpg; ++cc) {
+            if constexpr (kRowScaled<T>) {
+                // the chunk's scale codes of the batch's rows, in sorted order
+                if (cc > 0) __syncthreads();  // the previous chunk is done with ssc
+                const unsigned short *rsc16 =
+                    reinterpret_cast<const unsigned short *>(p.rsc) + ((size_t)row0 + base) * cpg + cc;
+                for (int i = tid; i < nrec; i += 512) ssc[i] = rsc16[(size_t)sslot[i] * cpg];
+                __syncthreads();
+            }
             // buffer over the batch's rows from this chunk's first channel (uniform);
             // the lane's slice goes into the offset
             const R *rows = (const R *)p.cgm + ((size_t)row0 + base) * p.Cgp + cc * KC;
@@ -2159,7 +2222,7 @@ __global__ __launch_bounds__(512) void dcn2_gi_gather_kernel(const BwdParams p) 
                 // take each row's offset and weight from its lane (ds_swizzle in
                 // bit mode: lane (l & 0x18) | u of every 32-lane half), so the
                 // index arithmetic is done once per row instead of once per lane.
-                auto row_info = [&](int jb, int &off, float &w) __attribute__((always_inline)) {
+                auto row_info = [&](int jb, int &off, float &w, int &sc) __attribute__((always_inline)) {
                     const int j = jb + co;
                     const bool ok = j < tot, q1 = j >= e1, q2 = j >= e2, q3 = j >= e3;
                     int pos = beg[0] + j;
@@ -2172,12 +2235,17 @@ __global__ __launch_bounds__(512) void dcn2_gi_gather_kernel(const BwdParams p) 
                     const float wx = (q1 != q2) || q3 ? f.y : 1.0f - f.y;  // corners 01, 11
                     w = ok ? wy * wx : 0.0f;
                     off = ok ? (int)sslot[pos] * row_bytes : kGatherOutOfRange;
+                    sc = kRowScaled<T> ? (int)ssc[kRowScaled<T> ? pos : 0] : 0;
                 };
-                auto fetch = [&](int off, float w, u32x4 (&raw)[LPR][NLD], float (&wgt)[LPR]) __attribute__((always_inline)) {
+                auto fetch = [&](int off, float w, int sc, u32x4 (&raw)[LPR][NLD], float (&wgt)[LPR]) __attribute__((always_inline)) {
                     static_for<0, LPR>([&](auto uc) __attribute__((always_inline)) {
                         constexpr int u = decltype(uc)::value;
                         const int ou = __builtin_amdgcn_ds_swizzle(off, (u << 5) | 0x18);
                         wgt[u] = __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(w), (u << 5) | 0x18));
+                        if constexpr (kRowScaled<T>) {
+                            const int scu = __builtin_amdgcn_ds_swizzle(sc, (u << 5) | 0x18);
+                            wgt[u] *= row_unscale(((unsigned)scu >> sc_shift) & 0xffu);
+                        }
                         // row_bytes is a multiple of 128 * NLD (the slice's range)
                         // and the marker has the low bits set, so OR-ing the slice
                         // in keeps either in range
@@ -2201,20 +2269,20 @@ __global__ __launch_bounds__(512) void dcn2_gi_gather_kernel(const BwdParams p) 
                 };
                 u32x4 ra[LPR][NLD], rb[LPR][NLD];
                 float wa[LPR], wb[LPR];
-                int oa, ob;
+                int oa, ob, sa, sb;
                 float xa, xb;
                 // (scheduling barriers keep each batch's loads ahead of the sums of
                 // the previous one; left alone the scheduler groups the fetches)
-                row_info(0, oa, xa);
-                fetch(oa, xa, ra, wa);
+                row_info(0, oa, xa, sa);
+                fetch(oa, xa, sa, ra, wa);
                 for (int j0 = 0; j0 < tot; j0 += 2 * LPR) {
-                    row_info(j0 + LPR, ob, xb);
-                    fetch(ob, xb, rb, wb);
+                    row_info(j0 + LPR, ob, xb, sb);
+                    fetch(ob, xb, sb, rb, wb);
                     __builtin_amdgcn_sched_barrier(0);
                     accumulate(ra, wa);
                     __builtin_amdgcn_sched_barrier(0);
-                    row_info(j0 + 2 * LPR, oa, xa);
-                    fetch(oa, xa, ra, wa);
+                    row_info(j0 + 2 * LPR, oa, xa, sa);
+                    fetch(oa, xa, sa, ra, wa);
                     __builtin_amdgcn_sched_barrier(0);
                     accumulate(rb, wb);
                     __builtin_amdgcn_sched_barrier(0);
@@ -2296,6 +2364,7 @@ __global__ __launch_bounds__(512) void dcn2_gi_push_kernel(const BwdParams p) {
     __shared__ int cstart[NCELL + 1];
     __shared__ unsigned short sslot[kGatherBatch];  // row in the batch, sorted by cell
     __shared__ float2 sfrac[kGatherBatch];          // (ly, lx), sorted by cell
+    __shared__ unsigned short ssc[kRowScaled<T> ? kGatherBatch : 1];  // bf16 rows: the chunk's scale codes
     // window [pixel][KC channels]: the lane's piece h (channels co*EPL + 4h ..)
     // at 16-byte slot h*LPR + co of its pixel, so the 8 lanes of a group
     // touch 8 consecutive slots per access
@@ -2312,6 +2381,8 @@ __global__ __launch_bounds__(512) void dcn2_gi_push_kernel(const BwdParams p) {
     const int co = lane % LPR, gq = lane / LPR;
     const int row_bytes = p.Cgp * (int)sizeof(R);
     const int slice = co * 16 * NLD;
+    // bf16 rows: this lane's 8 channels lie in 32-channel block co / 4 of the chunk
+    const int sc_shift = 8 * (co >> 2);
     auto piece = [&](int pix, int h) __attribute__((always_inline)) {
         return reinterpret_cast<f32x4 *>(win + pix * KC) + h * LPR + co;
     };
@@ -2376,6 +2447,14 @@ __global__ __launch_bounds__(512) void dcn2_gi_push_kernel(const BwdParams p) {
                 }
                 __syncthreads();
             }
+            if constexpr (kRowScaled<T>) {
+                // the chunk's scale codes of the batch's rows, in sorted order
+                // (the barrier at the batch's start ordered the last reads of ssc)
+                const unsigned short *rsc16 =
+                    reinterpret_cast<const unsigned short *>(p.rsc) + ((size_t)row0 + base) * cpg + cc;
+                for (int i = tid; i < nrec; i += 512) ssc[i] = rsc16[(size_t)sslot[i] * cpg];
+                __syncthreads();
+            }
 
             // 2. the cells.  Rows come in batches of RPB per lane group from
             //    buffer loads over the batch's rows: a row index past the cell's
@@ -2412,7 +2491,7 @@ __global__ __launch_bounds__(512) void dcn2_gi_push_kernel(const BwdParams p) {
                 return r == 0 ? a[0] : (r == 1 ? a[1] : (r == 2 ? a[2] : a[3]));
             };
             // batch jb of round r: the row offset, fractions of row jb*RPB + co
-            auto row_info = [&](int r, int jb, int &off, float &ly, float &lx) __attribute__((always_inline)) {
+            auto row_info = [&](int r, int jb, int &off, float &ly, float &lx, int &sc) __attribute__((always_inline)) {
                 const int j = jb * RPB + co;
                 const bool ok = co < RPB && j < pick(rtot, r);
                 const int pos = ok ? pick(rbeg, r) + j : 0;
@@ -2420,6 +2499,7 @@ __global__ __launch_bounds__(512) void dcn2_gi_push_kernel(const BwdParams p) {
                 ly = ok ? f.x : 0.0f;
                 lx = ok ? f.y : 0.0f;
                 off = ok ? (int)sslot[pos] * row_bytes : kGatherOutOfRange;
+                sc = kRowScaled<T> ? (int)ssc[kRowScaled<T> ? pos : 0] : 0;
             };
             // A batch in flight: the RPB rows' loads (each lane's slice of
             // row u comes from lane u of its group) and this lane's own row's
@@ -2427,10 +2507,12 @@ __global__ __launch_bounds__(512) void dcn2_gi_push_kernel(const BwdParams p) {
             struct Batch {
                 u32x4 raw[RPB][NLD];
                 float ly, lx;
+                int sc;
             };
-            auto fetch = [&](int off, float ly, float lx, Batch &bt) __attribute__((always_inline)) {
+            auto fetch = [&](int off, float ly, float lx, int sc, Batch &bt) __attribute__((always_inline)) {
                 bt.ly = ly;
                 bt.lx = lx;
+                bt.sc = sc;
                 static_for<0, RPB>([&](auto uc) __attribute__((always_inline)) {
                     constexpr int u = decltype(uc)::value;
                     const int ou = __builtin_amdgcn_ds_swizzle(off, (u << 5) | 0x18);
@@ -2450,9 +2532,17 @@ __global__ __launch_bounds__(512) void dcn2_gi_push_kernel(const BwdParams p) {
             auto accumulate = [&](const Batch &bt) __attribute__((always_inline)) {
                 static_for<0, RPB>([&](auto uc) __attribute__((always_inline)) {
                     constexpr int u = decltype(uc)::value;
-                    const float fy = __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(bt.ly), (u << 5) | 0x18));
+                    float fy = __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(bt.ly), (u << 5) | 0x18));
                     const float fx = __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(bt.lx), (u << 5) | 0x18));
-                    const float hy = 1.0f - fy, hx = 1.0f - fx;
+                    float hy = 1.0f - fy;
+                    const float hx = 1.0f - fx;
+                    if constexpr (kRowScaled<T>) {
+                        // the inverse scale of the lane's 32-channel block of row u
+                        const int scu = __builtin_amdgcn_ds_swizzle(bt.sc, (u << 5) | 0x18);
+                        const float f = row_unscale(((unsigned)scu >> sc_shift) & 0xffu);
+                        hy *= f;
+                        fy *= f;
+                    }
                     const float w[4] = {hy * hx, hy * fx, fy * hx, fy * fx};
 #pragma unroll
                     for (int h = 0; h < NLD; ++h) {
@@ -2493,10 +2583,10 @@ __global__ __launch_bounds__(512) void dcn2_gi_push_kernel(const BwdParams p) {
             int fr = 0, fj = 0, cr = 0, cj = 0;
             auto fetch_next = [&](Batch &bt) __attribute__((always_inline)) {
                 if (fr < 4) {
-                    int off;
+                    int off, sc;
                     float ly, lx;
-                    row_info(fr, fj, off, ly, lx);
-                    fetch(off, ly, lx, bt);
+                    row_info(fr, fj, off, ly, lx, sc);
+                    fetch(off, ly, lx, sc, bt);
                     if (++fj == pick(nbat, fr)) {
                         ++fr;
                         fj = 0;
@@ -2933,7 +3023,7 @@ __global__ __launch_bounds__(256) void finalize_gi_nhwc_kernel(const float *__re
 // ---------------------------------------------------------------------------
 template <typename T>
 static hipError_t backward_t(const Geo &g, const BwdParams &p0, void *grad_input,
-                             void *grad_weight, void *grad_bias, hipStream_t s) {
+                             void *grad_weight, void *grad_bias, bool last, hipStream_t s) {
     BwdParams p = p0;
     hipError_t e;
     // (the fp32 grad_weight / grad_bias accumulators and the bucket counts
@@ -2947,10 +3037,11 @@ static hipError_t backward_t(const Geo &g, const BwdParams &p0, void *grad_input
     // The fused kernel (column gradient and grad_weight in one pass) serves
     // 2-byte types with Mp == 256, one K chunk per deformable group, gO rows
     // that take 16-byte loads, and images of gO and xt below 2 GiB each.
-    // DCN2_BWD_FUSED=0 in the environment selects the two-kernel path for
-    // every shape (the tests compare both paths).
+    // Option DCN2_OPT_BWD_FUSED = 0 selects the two-kernel path for every
+    // shape (the tests compare both paths).
     // grad_weight / grad_bias finalisation (run by the grad_input finalisation
-    // launch, or alone for an empty batch)
+    // launch of the last slice, or alone for an empty batch; the earlier
+    // slices only accumulate, nblk = 0)
     GwFinal<T> gwf;
     gwf.gwa = p.gw_acc;
     gwf.gba = p.gb_acc;
@@ -2964,11 +3055,10 @@ static hipError_t backward_t(const Geo &g, const BwdParams &p0, void *grad_input
     gwf.Cgp = g.Cgp;
     gwf.G = g.G;
     gwf.Kp = g.Kp;
-    gwf.nblk = (std::max<long>((long)g.Cout * g.Cw * g.KK, g.Cout) + 255) / 256;
+    gwf.nblk = last ? (std::max<long>((long)g.Cout * g.Cw * g.KK, g.Cout) + 255) / 256 : 0;
     bool fused = false;
-    const char *fenv = std::getenv("DCN2_BWD_FUSED");
     if constexpr (sizeof(T) == 2)
-        fused = !(fenv && fenv[0] == '0') && g.Mp == 256 && g.Cgp == g.KC && p.go_vec &&
+        fused = g.opt_fused != 0 && g.Mp == 256 && g.Cgp == g.KC && p.go_vec &&
                 (long long)g.Cout * g.N * (long long)sizeof(T) <= kGoOutOfRange &&
                 (long long)g.H * g.W * g.cs * (long long)sizeof(T) <= kGoOutOfRange;
     if (g.B > 0) {
@@ -3086,7 +3176,8 @@ static hipError_t backward_t(const Geo &g, const BwdParams &p0, void *grad_input
         const long ring_items = ((long)nrow * g.W + (long)(g.H - nrow) * ncol) * (g.cs / 4);
         if (gg.by_cells) {
             // grad_weight first (when not fused), so that its finalisation can
-            // ride in the last launch, ring_final_kernel
+            // ride in the last launch, ring_final_kernel, and before the border
+            // rings overwrite xt (they may share its bytes, see bwd_workspace)
             if (!fused && (e = run_gradw()) != hipSuccess) return e;
             prof_begin(DCN2_STAGE_BWD_GATHER, s);
             p.gi_out = grad_input;
@@ -3106,11 +3197,16 @@ static hipError_t backward_t(const Geo &g, const BwdParams &p0, void *grad_input
             rf.items = (long)g.B * ((g.nhwc ? (long)nrow * g.W : 0) + (long)(g.H - nrow) * ncol) *
                        (g.cs / 4);
             rf.nb_items = (rf.items + 255) / 256;
+            // (none in a slice before the last when the images have no
+            // tile-boundary pixels)
             const long rblocks = rf.nb_rows + rf.nb_items + gwf.nblk;
-            ring_final_kernel<T><<<(unsigned)rblocks, 256, 0, s>>>(p, rf, gwf);
+            if (rblocks > 0) ring_final_kernel<T><<<(unsigned)rblocks, 256, 0, s>>>(p, rf, gwf);
             if ((e = hipGetLastError()) != hipSuccess) return e;
             prof_end(DCN2_STAGE_BWD_GATHER, s);
         } else {
+            // grad_weight first (when not fused): it reads xt, whose bytes the
+            // border rings may share (see bwd_workspace)
+            if (!fused && (e = run_gradw()) != hipSuccess) return e;
             prof_begin(DCN2_STAGE_BWD_GATHER, s);
             // At most two workgroups per CU (extra LDS reserved at launch): each
             // bucket's rows are read once per corner, and with three buckets per
@@ -3120,7 +3216,7 @@ static hipError_t backward_t(const Geo &g, const BwdParams &p0, void *grad_input
             if (hipDeviceGetAttribute(&lds_cu, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor,
                                       dev) != hipSuccess)
                 lds_cu = 0;
-            const int pad = std::max(0, lds_cu / 3 + 256 - kGatherStaticLds);
+            const int pad = std::max(0, lds_cu / 3 + 256 - gather_static_lds(kRowScaled<T>));
             dcn2_gi_gather_kernel<T><<<nbk, 512, pad, s>>>(p);
             if ((e = hipGetLastError()) != hipSuccess) return e;
             // the windows' border rings into gi_acc (tile-boundary pixels only)
@@ -3131,7 +3227,6 @@ static hipError_t backward_t(const Geo &g, const BwdParams &p0, void *grad_input
             }
             if ((e = hipGetLastError()) != hipSuccess) return e;
             prof_end(DCN2_STAGE_BWD_GATHER, s);
-            if (!fused && (e = run_gradw()) != hipSuccess) return e;
             // 4. grad_input to the caller's layout (and grad_weight / grad_bias)
             prof_begin(DCN2_STAGE_BWD_FINAL, s);
             const int HW = g.H * g.W;
@@ -3172,15 +3267,16 @@ GatherGeo gather_geometry(const Geo &g) {
     // every sample is placed in at most one bucket
     gg.rows = (long)g.B * g.G * g.KK * g.N;
     gg.row_esz = row_elem_bytes(g.dtype);
+    gg.row_scaled = row_scaled(g.dtype) ? 1 : 0;
     gg.batch_bytes = (long)kGatherBatch * g.Cgp * gg.row_esz;
     gg.max_batch_bytes = kGatherOutOfRange;
     // By cells (each row read once, one block per CU) when the buckets are
     // full enough to amortise a block's fixed work; per pixel otherwise.
-    // DCN2_GI_PUSH=1 / 0 in the environment forces either.  Measured: c2 68
+    // Option DCN2_OPT_GI_PUSH = 1 / 0 forces either.  Measured: c2 68
     // against 72 us, c3 ~190 against 282 us (2304 samples per bucket); c4
     // (576 per bucket) ~118 against 73 us.
-    const char *genv = std::getenv("DCN2_GI_PUSH");
-    gg.by_cells = genv ? genv[0] != '0' : gg.rows >= (long)kPushMinPerBucket * gg.nbuckets;
+    gg.by_cells = g.opt_push >= 0 ? g.opt_push != 0
+                                  : gg.rows >= (long)kPushMinPerBucket * gg.nbuckets;
     return gg;
 }
 
@@ -3188,9 +3284,9 @@ hipError_t launch_backward(const Geo &g, const void *xt, const void *wt, const v
                            const void *offset,
                            const void *mask, const void *grad_out, void *grad_input,
                            void *grad_offset, void *grad_mask, void *grad_weight, void *grad_bias,
-                           float *gi_acc, float *gw_acc, float *gb_acc, void *cgm, void *rec,
-                           int *bcnt, int *bstart, int *bcur, int *sidx, float *ring,
-                           hipStream_t s) {
+                           float *gi_acc, float *gw_acc, float *gb_acc, void *cgm, void *rsc,
+                           void *rec, int *bcnt, int *bstart, int *bcur, int *sidx, float *ring,
+                           bool last, hipStream_t s) {
     BwdParams p;
     p.xt = xt;
     p.wt = wt;
@@ -3231,6 +3327,7 @@ hipError_t launch_backward(const Geo &g, const void *xt, const void *wt, const v
     p.go_vec = (g.out_nhwc ? g.Cout % 8 == 0 : g.N % 8 == 0) && (((uintptr_t)grad_out & 15) == 0);
     const GatherGeo gg = gather_geometry(g);
     p.cgm = cgm;
+    p.rsc = (unsigned char *)rsc;
     p.rec = (BucketRec *)rec;
     p.bcnt = bcnt;
     p.bstart = bstart;
@@ -3242,9 +3339,9 @@ hipError_t launch_backward(const Geo &g, const void *xt, const void *wt, const v
     p.gi_out = nullptr;  // (set by the by-cells grad_input)
     p.gi_nhwc = p.gi_vec = 0;
     switch (g.dtype) {
-    case DCN2_F16: return backward_t<f16>(g, p, grad_input, grad_weight, grad_bias, s);
-    case DCN2_BF16: return backward_t<bf16>(g, p, grad_input, grad_weight, grad_bias, s);
-    default: return backward_t<float>(g, p, grad_input, grad_weight, grad_bias, s);
+    case DCN2_F16: return backward_t<f16>(g, p, grad_input, grad_weight, grad_bias, last, s);
+    case DCN2_BF16: return backward_t<bf16>(g, p, grad_input, grad_weight, grad_bias, last, s);
+    default: return backward_t<float>(g, p, grad_input, grad_weight, grad_bias, last, s);
     }
 }
 

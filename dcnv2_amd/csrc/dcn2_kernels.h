@@ -41,6 +41,13 @@ struct Geo {
     // The forward runs dcn2_fwd_rw_kernel (weight resident in registers)
     // instead of the chunk-streaming kernels.
     int rw;
+    // Process-wide options read once per call (dcn2_set_option): backward
+    // slice budget in bytes, fused backward allowed (-1 auto, 0 never),
+    // grad_input by cells (-1 auto, 0 per pixel, 1 by cells).
+    long long slice_bytes;
+    int opt_fused, opt_push;
+    // The images of one backward slice (B when the batch runs in one piece).
+    int Bs;
 };
 
 // dcn2_api.cpp: the descriptor check shared by every entry point, the forward
@@ -59,8 +66,9 @@ struct FwdWorkspace {
 FwdWorkspace fwd_workspace(const Geo &g);
 
 struct BwdWorkspace {
-    size_t xt, wt, tab, gi_acc, gw_acc, gb_acc, cgm, rec, bcnt, bstart, bcur, sidx, ring, total;
+    size_t xt, wt, tab, gi_acc, gw_acc, gb_acc, cgm, rsc, rec, bcnt, bstart, bcur, sidx, ring, total;
 };
+// Carves the backward workspace of one slice of g.Bs images.
 // Border-ring pixels of one grad_input gather window (4 x the cell tile side).
 constexpr int kGatherRing = 64;
 BwdWorkspace bwd_workspace(const Geo &g);
@@ -71,6 +79,7 @@ BwdWorkspace bwd_workspace(const Geo &g);
 // limit they must stay below.
 struct GatherGeo {
     int ntx, nty, row_esz;
+    int row_scaled;  // bf16 rows carry one scale byte per 32 channels
     long nbuckets, rows;
     long batch_bytes, max_batch_bytes;
     // grad_input by cells (dcn2_gi_push_kernel, written straight into the
@@ -81,7 +90,7 @@ struct GatherGeo {
 GatherGeo gather_geometry(const Geo &g);
 
 // dcn2_pack.hip: input -> xt (skipped when input is null) and weight -> wp +
-// chunk table in one launch; transpose selects the backward's W'^T fragment
+// chunk table (skipped when weight is null) in one launch; transpose selects the backward's W'^T fragment
 // order.  The input is NCHW, or channels-last when g.nhwc.
 // Up to three fp32 buffers the pack launch also zeroes (extra workgroups), so
 // the backward's accumulators need no launch of their own; n = 0 skips one.
@@ -104,13 +113,15 @@ bool rw_eligible(const Geo &g);
 hipError_t launch_forward_rw(const Geo &g, const void *xt, const void *wp, const void *offset,
                              const void *mask, const void *bias, void *out, hipStream_t s);
 
-// dcn2_backward.hip
+// dcn2_backward.hip: the backward of g.B images (one slice of the batch; the
+// pointers point at its first image).  grad_weight / grad_bias accumulate in
+// gw_acc / gb_acc over the slices and are written out when `last` is set.
 hipError_t launch_backward(const Geo &g, const void *xt, const void *wt, const void *tab,
                            const void *offset,
                            const void *mask, const void *grad_out, void *grad_input,
                            void *grad_offset, void *grad_mask, void *grad_weight, void *grad_bias,
-                           float *gi_acc, float *gw_acc, float *gb_acc, void *cgm, void *rec,
-                           int *bcnt, int *bstart, int *bcur, int *sidx, float *ring,
-                           hipStream_t s);
+                           float *gi_acc, float *gw_acc, float *gb_acc, void *cgm, void *rsc,
+                           void *rec, int *bcnt, int *bstart, int *bcur, int *sidx, float *ring,
+                           bool last, hipStream_t s);
 
 }  // namespace dcn2

@@ -260,8 +260,10 @@ static hipError_t pack_t(const Geo &g, const void *input, void *xt, const void *
     p.Kp = g.Kp;
     p.transpose = transpose ? 1 : 0;
     p.nhwc = g.nhwc;
-    // one thread per 16-byte piece of the packed weight (Mp*Kp is a multiple of 16/esz)
-    const long nw = ((long)g.Mp * g.Kp / E + 255) / 256;
+    // one thread per 16-byte piece of the packed weight (Mp*Kp is a multiple of
+    // 16/esz); none when weight is null (a later slice of the backward, whose
+    // packed weight and table the first slice wrote)
+    const long nw = weight ? ((long)g.Mp * g.Kp / E + 255) / 256 : 0;
     p.nw = (int)nw;
     p.clr_blk[0] = 0;
     for (int i = 0; i < 3; ++i) {

@@ -6,8 +6,8 @@
  * plain pointers, sizes and a HIP stream handle; there are no framework types.
  * All work is enqueued asynchronously on `stream` (a hipStream_t; NULL = the
  * null stream) and nothing synchronises the host.  The library keeps no state
- * between calls apart from the per-thread error message, so calls are
- * re-entrant.
+ * between calls apart from the per-thread error message and the process-wide
+ * options of dcn2_set_option, so calls are re-entrant.
  *
  * Semantics are those of torchvision.ops.deform_conv2d(input, offset, weight,
  * bias, stride, padding, dilation, mask), the comparator the reference names:
@@ -48,7 +48,7 @@
 extern "C" {
 #endif
 
-#define DCN2_ABI_VERSION 3
+#define DCN2_ABI_VERSION 4
 #define DCN2_API __attribute__((visibility("default")))
 
 enum dcn2_dtype { DCN2_F32 = 0, DCN2_F16 = 1, DCN2_BF16 = 2 };
@@ -64,6 +64,13 @@ enum dcn2_dtype { DCN2_F32 = 0, DCN2_F16 = 1, DCN2_BF16 = 2 };
  * counterpart in the reference, which takes and returns contiguous NCHW only. */
 enum dcn2_layout { DCN2_NCHW = 0, DCN2_NHWC = 1 };
 
+/* Status codes.  DCN2_ERANGE: the kernels index within one image with 32-bit
+ * offsets (the image's base is 64-bit), so per image every tensor must hold
+ * fewer than 2^31 elements, the batch at most 65535 images, H and W at most
+ * 32767, and the input's channels-last copy must stay below 4 GiB in bytes:
+ * (H*W + 1) * G * Cgp * sizeof(dtype) + 256 < 2^32, where Cgp is
+ * C/deformable_groups rounded up to 64 (fp16/bf16) or 32 (fp32) channels
+ * (e.g. fp32, C = 256, 2048 x 2048 is rejected). */
 enum dcn2_status {
     DCN2_OK = 0,
     DCN2_EINVAL = 1,     /* bad geometry, dtype, null pointer or group split     */
@@ -99,6 +106,27 @@ DCN2_API int dcn2_output_shape(const dcn2_desc *d, int32_t *out_h, int32_t *out_
  * start required).  0 is returned for an invalid description. */
 DCN2_API size_t dcn2_forward_workspace_bytes(const dcn2_desc *d);
 DCN2_API size_t dcn2_backward_workspace_bytes(const dcn2_desc *d);
+
+/* Process-wide options (no counterpart in the reference, whose backward holds
+ * one image's columns, com.cu:766, and has one code path).  A call reads them
+ * once when it starts; set them between calls (a call on another thread that
+ * is already running keeps what it read).  The workspace size a call needs
+ * depends on them: query dcn2_backward_workspace_bytes after changing one.
+ *   DCN2_OPT_BWD_SLICE_BYTES  The backward runs the batch in slices of whole
+ *       images, as many per slice as keep its workspace within this many
+ *       bytes (at least one image; the slices are made equal in size up to
+ *       one image).  Default DCN2_BWD_SLICE_BYTES_DEFAULT; minimum 1.
+ *   DCN2_OPT_BWD_FUSED  -1 (default): the backward uses its fused
+ *       column-gradient + grad_weight kernel where the shape allows it;
+ *       0: never (two kernels).
+ *   DCN2_OPT_GI_PUSH  -1 (default): grad_input by cells where the buckets
+ *       are dense enough, per pixel otherwise; 1: by cells; 0: per pixel.
+ * dcn2_set_option returns DCN2_EINVAL for an unknown option or value;
+ * dcn2_get_option returns the current value (-2 for an unknown option). */
+enum dcn2_option { DCN2_OPT_BWD_SLICE_BYTES = 0, DCN2_OPT_BWD_FUSED = 1, DCN2_OPT_GI_PUSH = 2 };
+#define DCN2_BWD_SLICE_BYTES_DEFAULT ((int64_t)192 << 20)
+DCN2_API int dcn2_set_option(int option, int64_t value);
+DCN2_API int64_t dcn2_get_option(int option);
 
 /* Forward.  Replaces MyDCN_forward / _C.dcn_v2_forward (com.cu:198-272,
  * ext.cpp:16; bound in dcn_v2_mm.py:20-30).  `mask` may be NULL (all ones,

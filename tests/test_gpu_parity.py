@@ -339,8 +339,8 @@ def test_channels_last_input(case):
 ], ids=["f16_c64", "bf16_c24_dg2", "f32_c64_dg2", "bf16_c18_dg2"])
 def test_grad_input_channels_last_by_cells(case):
     """A channels_last grad_input written directly by the per-cell kernel and
-    ring_final_kernel (DCN2_GI_PUSH=1), and by the per-pixel kernel with its
-    finalisation (DCN2_GI_PUSH=0): all five gradients against the oracle, for
+    ring_final_kernel (option gi_push = 1), and by the per-pixel kernel with its
+    finalisation (gi_push = 0): all five gradients against the oracle, for
     either grad_output layout."""
     dtype, C, G, Cout, H, W = case
     w, t = _small(dtype, B=2, C=C, H=H, W=W, Cout=Cout, G=G, osc=3.0, seed=29)
@@ -350,10 +350,10 @@ def test_grad_input_channels_last_by_cells(case):
     args = [None if t[k] is None else t[k].to(DEV) for k in IN5]
     go = t["grad_output"].to(DEV)
     rgrads = oracle_backward(t, geo)
-    for push in ("1", "0"):
+    for push in (1, 0):
         for go_t, tag in ((go.to(memory_format=cl), "grad_output channels_last"), (go, "grad_output NCHW")):
-            grads = _with_env("DCN2_GI_PUSH", push,
-                              lambda: _C.dcn_v2_backward(x_cl, *args[1:], go_t, *_args(geo)))
+            grads = _with_option("gi_push", push,
+                                 lambda: _C.dcn_v2_backward(x_cl, *args[1:], go_t, *_args(geo)))
             torch.cuda.synchronize()
             assert grads[0].is_contiguous(memory_format=cl)
             for name, g, r in zip(GRADS, grads, rgrads):
@@ -499,24 +499,19 @@ def test_bucket_scan_launch(dtype):
 
 # --------------------------------------------------------------------------- fused backward
 def _backward_path(t, geo, go, fused):
-    """Backward with the fused kernel allowed or not (DCN2_BWD_FUSED), and
+    """Backward with the fused kernel allowed or not (option bwd_fused), and
     whether the separate grad_weight stage ran (it does not when fused)."""
-    prev = os.environ.get("DCN2_BWD_FUSED")
-    os.environ["DCN2_BWD_FUSED"] = "1" if fused else "0"
-    try:
-        _C.profile_enable(True)
-        for s in _C.STAGES:
-            _C.profile_read(s)
-        args = [None if t[k] is None else t[k].to(DEV) for k in IN5]
-        grads = _C.dcn_v2_backward(*args, go, *_args(geo))
-        torch.cuda.synchronize()
-        gradw_launches = _C.profile_read("bwd_gradw")[1]
-    finally:
-        _C.profile_enable(False)
-        if prev is None:
-            del os.environ["DCN2_BWD_FUSED"]
-        else:
-            os.environ["DCN2_BWD_FUSED"] = prev
+    with _C.option("bwd_fused", -1 if fused else 0):
+        try:
+            _C.profile_enable(True)
+            for s in _C.STAGES:
+                _C.profile_read(s)
+            args = [None if t[k] is None else t[k].to(DEV) for k in IN5]
+            grads = _C.dcn_v2_backward(*args, go, *_args(geo))
+            torch.cuda.synchronize()
+            gradw_launches = _C.profile_read("bwd_gradw")[1]
+        finally:
+            _C.profile_enable(False)
     return grads, gradw_launches
 
 
@@ -554,17 +549,36 @@ def test_fused_backward(dtype, case):
                 check(f"{name} ({'fused' if fused else 'two kernels'})", g, r, TOL[dtype])
 
 
+@pytest.mark.parametrize("scale_exp", [100, -100, 0], ids=["x2^100", "x2^-100", "x1"])
+@pytest.mark.parametrize("path", [(-1, 1), (0, 1), (-1, 0)], ids=["fused_by_cells", "two_kernels_by_cells",
+                                                                 "fused_per_pixel"])
+def test_bf16_handoff_rows_keep_range(scale_exp, path):
+    """bf16 hands the column gradient to grad_input as fp16 rows with a
+    power-of-two scale per 32 channels: a grad_output scaled far outside fp16's
+    range (2^100, 2^-100; bf16 holds both) gives the same relative errors as
+    an unscaled one, on either column-gradient kernel and either grad_input
+    kernel; one row block of all zeros (a zero grad_output image) reads back
+    as zeros.  Against the fp64 oracle on the same scaled values."""
+    fused, push = path
+    w, t = _small(torch.bfloat16, B=2, C=64, H=19, W=17, Cout=256, G=1, osc=2.5, seed=53)
+    go = t["grad_output"].double() * 2.0 ** scale_exp
+    go[1] = 0.0
+    t["grad_output"] = go.bfloat16()
+    geo = w.geometry()
+    rg = oracle_backward(t, geo)
+    with _C.option("bwd_fused", fused), _C.option("gi_push", push):
+        grads = gpu_backward(t, geo)
+        torch.cuda.synchronize()
+    assert torch.isfinite(grads[0].float()).all()
+    assert (grads[0][1] == 0).all()
+    for name, g, r in zip(GRADS, grads, rg):
+        check(f"{name} (grad_output x 2^{scale_exp})", g, r, TOL[torch.bfloat16])
+
+
 # --------------------------------------------------------------------------- grad_input kernels
-def _with_env(name, value, fn):
-    prev = os.environ.get(name)
-    os.environ[name] = value
-    try:
+def _with_option(name, value, fn):
+    with _C.option(name, value):
         return fn()
-    finally:
-        if prev is None:
-            del os.environ[name]
-        else:
-            os.environ[name] = prev
 
 
 @pytest.mark.parametrize("case", [
@@ -577,7 +591,7 @@ def _with_env(name, value, fn):
 @pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
 def test_grad_input_by_cells_and_by_pixels(dtype, case):
     """grad_input from the per-cell kernel (rows read once, window summed in
-    LDS) and from the per-pixel kernel (DCN2_GI_PUSH=1 / 0; the host picks by
+    LDS) and from the per-pixel kernel (option gi_push = 1 / 0; the host picks by
     samples per bucket): all five gradients against the oracle for both."""
     C, G, Cout, H, W, k, st, osc, clustered = case
     if clustered:
@@ -587,8 +601,8 @@ def test_grad_input_by_cells_and_by_pixels(dtype, case):
         w, t = _small(dtype, B=2, C=C, H=H, W=W, Cout=Cout, k=k, p=k // 2, s=st, G=G, osc=osc, seed=23)
     geo = w.geometry()
     rg = oracle_backward(t, geo)
-    for push in ("1", "0"):
-        grads = _with_env("DCN2_GI_PUSH", push, lambda: gpu_backward(t, geo))
+    for push in (1, 0):
+        grads = _with_option("gi_push", push, lambda: gpu_backward(t, geo))
         torch.cuda.synchronize()
         for name, g, r in zip(GRADS, grads, rg):
             check(f"{name} (push={push})", g, r, TOL[dtype])

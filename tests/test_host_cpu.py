@@ -132,25 +132,86 @@ def test_workspace_sizes(L):
     assert L.dcn2_forward_workspace_bytes(ctypes.byref(desc(B=0))) > 0
 
 
-def test_backward_workspace_is_exact_size(L, monkeypatch):
+def test_backward_workspace_is_exact_size(L):
     """The grad_input buckets hold one row per sample (B*G*kh*kw*Ho*Wo rows of
     Cg rounded to 64 channels), however the samples cluster, so the c2 shape
-    (B8 C64 128x128 Cout256 fp16) needs about 198 MB: channels-last input
-    copy 16.8 MB, rows 151 MB, 12-byte records 14.2 MB, sample rows 4.7 MB, border
-    rings 10.6 MB, packed weights and grad_weight accumulator 0.9 MB.  Its
+    (B8 C64 128x128 Cout256 fp16) needs about 188 MB: channels-last input
+    copy 16.8 MB (whose bytes the 10.6 MB of border rings reuse once the
+    column-gradient kernel is done with it), rows 151 MB, 12-byte records
+    14.2 MB, sample rows 4.7 MB, packed weights and grad_weight accumulator
+    0.9 MB.  Its
     buckets are full enough for the by-cells grad_input, which writes the
-    caller's grad_input directly; the per-pixel form (forced with
-    DCN2_GI_PUSH=0) adds the fp32 grad_input accumulator, 33.6 MB."""
-    d = desc(B=8, C=64, H=128, W=128, Co=256, dtype=1)
-    nbytes = L.dcn2_backward_workspace_bytes(ctypes.byref(d))
-    rows = 8 * 9 * 128 * 128
-    assert rows * (64 * 2 + 12) < nbytes < 200e6
-    # bf16 hands fp32 rows to the gather: twice the row bytes
-    d16 = desc(B=8, C=64, H=128, W=128, Co=256, dtype=2)
-    assert L.dcn2_backward_workspace_bytes(ctypes.byref(d16)) - nbytes == rows * 64 * 2
-    monkeypatch.setenv("DCN2_GI_PUSH", "0")
-    acc = 8 * 128 * 128 * 64 * 4
-    assert L.dcn2_backward_workspace_bytes(ctypes.byref(d)) - nbytes == acc
+    caller's grad_input directly; the per-pixel form (option gi_push = 0)
+    adds the fp32 grad_input accumulator, 33.6 MB.  (Unsliced: the slice
+    budget is raised for the comparison.)"""
+    with _C.option("bwd_slice_bytes", 1 << 40):
+        d = desc(B=8, C=64, H=128, W=128, Co=256, dtype=1)
+        nbytes = L.dcn2_backward_workspace_bytes(ctypes.byref(d))
+        rows = 8 * 9 * 128 * 128
+        assert rows * (64 * 2 + 12) < nbytes < 200e6
+        # bf16 hands fp16 rows with one scale byte per 32 channels to the gather
+        d16 = desc(B=8, C=64, H=128, W=128, Co=256, dtype=2)
+        assert L.dcn2_backward_workspace_bytes(ctypes.byref(d16)) - nbytes == rows * 2
+        with _C.option("gi_push", 0):
+            acc = 8 * 128 * 128 * 64 * 4
+            assert L.dcn2_backward_workspace_bytes(ctypes.byref(d)) - nbytes == acc
+
+
+def _ws(L, **kw):
+    return L.dcn2_backward_workspace_bytes(ctypes.byref(desc(**kw)))
+
+
+def test_backward_workspace_slices_the_batch(L):
+    """The backward runs the batch in slices of whole images whose workspace
+    fits the slice budget (default 192 MiB): c2 (188 MB) and c4 (182 MB) fit in
+    one slice; c3 (B16 C256 64x64 dg4 bf16, 23.6 MB per image, 382 MB in one
+    piece) runs as two slices of eight images, within 200 MB.  A smaller budget gives equal
+    slices (B = 7 with room for 3 images: 3 + 2 + 2, workspace of 3), and a
+    budget below one image still runs one image per slice."""
+    assert _C.get_option("bwd_slice_bytes") == 192 << 20
+    c2 = dict(B=8, C=64, H=128, W=128, Co=256, dtype=1)
+    c3 = dict(B=16, C=256, H=64, W=64, Co=256, G=4, dtype=2)
+    c4 = dict(B=2, C=128, H=256, W=256, Co=128, sh=2, sw=2, ph=2, pw=2, dh=2, dw=2, dtype=1)
+    with _C.option("bwd_slice_bytes", 1 << 40):
+        full = {k: _ws(L, **v) for k, v in (("c2", c2), ("c3", c3), ("c4", c4))}
+        c3_one, c3_eight = _ws(L, **dict(c3, B=1)), _ws(L, **dict(c3, B=8))
+        # eight images fit the budget, nine do not: 16 = 8 + 8
+        assert c3_eight <= 192 << 20 < _ws(L, **dict(c3, B=9))
+    assert _ws(L, **c2) == full["c2"] < 190e6
+    assert _ws(L, **c4) == full["c4"] < 190e6
+    assert full["c3"] > 380e6
+    assert _ws(L, **c3) == c3_eight < 200e6
+    one, two, three = (_ws(L, **dict(c2, B=b)) for b in (1, 2, 3))
+    with _C.option("bwd_slice_bytes", three):
+        assert _ws(L, **dict(c2, B=7)) == three
+        assert _ws(L, **dict(c2, B=6)) == three
+        assert _ws(L, **dict(c2, B=4)) == two
+    with _C.option("bwd_slice_bytes", one - 1):
+        assert _ws(L, **dict(c2, B=5)) == one
+    assert c3_one < c3_eight
+
+
+def test_options_reject_bad_values(L):
+    for name, bad in (("bwd_slice_bytes", 0), ("bwd_fused", 1), ("gi_push", 2), ("gi_push", -2)):
+        prev = _C.get_option(name)
+        with pytest.raises(RuntimeError, match="dcn2_set_option"):
+            _C.set_option(name, bad)
+        assert _C.get_option(name) == prev
+    assert L.dcn2_set_option(7, 0) == 1 and "unknown option" in L.dcn2_last_error().decode()
+    assert L.dcn2_get_option(7) == -2
+
+
+def test_per_image_byte_range(L):
+    """A channels-last input copy of 4 GiB or more per image is rejected with
+    DCN2_ERANGE before anything runs (fp32, C 256, 2048 x 2048: 4 GiB), while
+    one just below fits (2047 x 2048)."""
+    d = desc(B=1, C=256, H=2048, W=2048, Co=32, dtype=0)
+    rc, _, _ = out_hw(L, d)
+    assert rc == 4 and "byte range" in L.dcn2_last_error().decode()
+    assert L.dcn2_forward_workspace_bytes(ctypes.byref(d)) == 0
+    assert L.dcn2_backward_workspace_bytes(ctypes.byref(d)) == 0
+    rc, _, _ = out_hw(L, desc(B=1, C=256, H=2047, W=2048, Co=32, dtype=0))
+    assert rc == 0
 
 
 def test_entry_points_reject_before_any_launch(L):
@@ -367,13 +428,19 @@ def test_dcnv2_module_weight_groups(oracle_C):
 
 def test_channels_last_workspace(L):
     """A channels-last input whose channels need no padding is read in place:
-    the workspace drops exactly the repacked copy; with padding it keeps it."""
+    the workspace drops exactly the repacked copy; with padding it keeps it.
+    (The backward's border rings, 64 pixels x Cgp fp32 per cell-tile bucket,
+    reuse the copy's bytes when they fit there, so without a copy they take
+    their own.)"""
+    al = lambda n: (n + 255) // 256 * 256
     for dtype, esz, C in ((1, 2, 64), (2, 2, 128), (0, 4, 32)):
         nchw, nhwc = desc(C=C, dtype=dtype), desc(C=C, dtype=dtype, layout=1)
-        copy = 2 * 9 * 10 * C * esz
-        for fn in (L.dcn2_forward_workspace_bytes, L.dcn2_backward_workspace_bytes):
-            a, b = fn(ctypes.byref(nchw)), fn(ctypes.byref(nhwc))
-            assert 0 < b < a and a - b == (copy + 255) // 256 * 256
+        copy = al(2 * 9 * 10 * C * esz)
+        rings = al(2 * 64 * C * 4)  # B = 2 images of one bucket each; Cgp == C here
+        a, b = (L.dcn2_forward_workspace_bytes(ctypes.byref(x)) for x in (nchw, nhwc))
+        assert 0 < b < a and a - b == copy
+        a, b = (L.dcn2_backward_workspace_bytes(ctypes.byref(x)) for x in (nchw, nhwc))
+        assert 0 < b < a and a - b == copy - (rings if rings <= copy else 0)
     padded_cl, padded = desc(C=24, dtype=1, layout=1), desc(C=24, dtype=1)
     assert L.dcn2_forward_workspace_bytes(ctypes.byref(padded_cl)) == \
         L.dcn2_forward_workspace_bytes(ctypes.byref(padded))
