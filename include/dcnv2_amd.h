@@ -29,9 +29,11 @@
  * takes its operands in that dtype and accumulates in fp32 (the sampled
  * columns are rounded to it once, as com.cu:83, 87 rounds them to half); the
  * bilinear sampling arithmetic is fp32.  Intermediate roundings of the
- * backward, for fp16 only: the column gradient handed to the grad_input pass
- * and the one multiplied into the corner sums of grad_offset / grad_mask are
- * rounded to fp16 (products and sums stay fp32).
+ * backward: the column gradient handed to the grad_input pass is rounded to
+ * fp16 (fp16 calls) or to fp16 with one power-of-two scale per 32 channels
+ * (bf16 calls: an 11-bit significand over bf16's exponent range); for fp16
+ * the one multiplied into the corner sums of grad_offset / grad_mask is
+ * rounded to fp16 too (products and sums stay fp32); fp32 has none.
  *
  * Return value of every int function: 0 = success, otherwise a DCN2_E* code;
  * dcn2_last_error() then describes the failure.  This replaces the reference's
