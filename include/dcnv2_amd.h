@@ -179,7 +179,9 @@ DCN2_API int dcn2_backward_om(const dcn2_desc *d, const void *input, const void 
  * launched.  Every call on one GPU uses the same array: calls that overlap on
  * one GPU (concurrent streams or threads) race and must be serialised by the
  * caller; consecutive calls on one stream are safe.  Nothing is allocated and
- * nothing synchronises. */
+ * nothing synchronises.  Under HIP graph capture: make the first call on a
+ * device before capturing (it looks the array up with hipGetSymbolAddress);
+ * later calls capture as kernel nodes only (no memset, no allocation). */
 #define DCN2_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
 DCN2_API int dcn2_forward_noalloc(const dcn2_desc *d, const void *input, const void *weight,
                                   const void *mask, const void *offset, const void *bias,

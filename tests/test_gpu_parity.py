@@ -283,6 +283,58 @@ def test_weight_groups_split_per_group(dtype, case):
         check(name, g, r, TOL[dtype])
 
 
+@pytest.mark.parametrize("case", [
+    # C, Cout, deformable groups, weight groups (per-group launches, as above)
+    (128, 256, 1, 2),
+    (256, 512, 4, 4),
+], ids=["c128_wg2", "c256_dg4_wg4"])
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+def test_weight_groups_split_per_group_channels_last(dtype, case):
+    """The per-group launches with a channels_last input, output and
+    grad_output (the input read in place, the output and grad_output
+    channels-last): forward and all five gradients against the oracle."""
+    C, Cout, G, WG = case
+    w, t = _small(dtype, B=2, C=C, H=11, W=13, Cout=Cout, G=G, osc=2.0, seed=17)
+    t["weight"] = t["weight"][:, : C // WG].contiguous()
+    geo = w.geometry()
+    cl = torch.channels_last
+    args = [None if t[k] is None else t[k].to(DEV) for k in IN5]
+    args[0] = args[0].to(memory_format=cl)
+    out = _C.dcn_v2_forward(*args, *_args(geo))
+    go = t["grad_output"].to(DEV).to(memory_format=cl)
+    grads = _C.dcn_v2_backward(*args, go, *_args(geo))
+    torch.cuda.synchronize()
+    assert out.is_contiguous(memory_format=cl) and grads[0].is_contiguous(memory_format=cl)
+    check("output", out, oracle_forward(t, geo), TOL[dtype])
+    for name, g, r in zip(GRADS, grads, oracle_backward(t, geo)):
+        check(name, g, r, TOL[dtype])
+
+
+# --------------------------------------------------------------------------- NCHW vs channels_last
+@pytest.mark.parametrize("case", [
+    # B, C, H, W, Cout: fp16 3x3, <= 64 channels, 128 < Cout <= 256 (the
+    # resident-weight forward)
+    (8, 64, 16, 20, 256),    # 320 pixels per image: a partial last 64-pixel tile
+    (16, 48, 12, 10, 200),   # 48 channels padded to 64
+], ids=["b8_c64", "b16_c48"])
+def test_forward_nchw_matches_channels_last(case):
+    """The resident-weight forward on an NCHW input (transposed by the pack
+    launch) is bitwise equal to the same call on a channels_last copy
+    (repacked with padding channels, or read in place), twice in a row, and
+    matches the oracle."""
+    B, C, H, W, Cout = case
+    w, t = _small(torch.float16, B=B, C=C, H=H, W=W, Cout=Cout, G=1, osc=2.0, seed=61)
+    geo = w.geometry()
+    args = [None if t[k] is None else t[k].to(DEV) for k in IN5]
+    outs = [_C.dcn_v2_forward(*args, *_args(geo)) for _ in range(2)]
+    x_cl = args[0].to(memory_format=torch.channels_last)
+    ref = _C.dcn_v2_forward(x_cl, *args[1:], *_args(geo))
+    torch.cuda.synchronize()
+    for out in outs:
+        assert torch.equal(out, ref)
+    check("output (NCHW input)", outs[0], oracle_forward(t, geo), TOL[torch.float16])
+
+
 # --------------------------------------------------------------------------- channels_last
 @pytest.mark.parametrize("case", [
     # dtype, C, deformable groups, Cout: the input is read in place when C/G is a
