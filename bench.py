@@ -144,6 +144,13 @@ def _geo(w):
     return (w.stride, w.stride, w.pad, w.pad, w.dil, w.dil, w.groups)
 
 
+def _bwd_workspace_bytes(_C, w, t):
+    """dcn2_backward_workspace_bytes of workload w (NCHW tensors t)."""
+    import ctypes
+    d = _C.make_desc(t["input"], t["weight"], *_geo(w))
+    return _C.lib().dcn2_backward_workspace_bytes(ctypes.byref(d))
+
+
 def cpu_baseline(seconds, threads):
     """The float32 oracle (C, OpenMP) on bounded samples: c1 forward on image
     0 (the metric), c0 forward, and c2 forward + backward on image 0."""
@@ -225,7 +232,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU; the batch-sharded multi-GPU path is "
-              "described in DESIGN.md but not benchmarked (run with --gpus 1)", file=sys.stderr)
+              "a design only and is not benchmarked (run with --gpus 1)", file=sys.stderr)
         sys.exit(2)
 
     import torch
@@ -323,12 +330,15 @@ def main():
         "fwd_cold_note": "median per call after a 512 MiB write that evicts L2 and MALL",
         "roofline": {
             "bound": "mfma",
-            "kernel": "dcn2_fwd_ws_kernel (fused bilinear sampling + 32x32x16 f16 MFMA)",
+            "kernel": "dcn2_fwd_rw_kernel (weight resident in registers; fused bilinear sampling "
+                      "+ 32x32x16 f16 MFMA)",
             "achieved": round(achieved, 2),
             "peak": PEAK_FP16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_FP16_TFLOPS, 4),
             "traffic": _traffic(),
+            "traffic_source": "profiles/fwd_kernel_traffic_c1.md: rocprofv3 FETCH_SIZE + WRITE_SIZE "
+                              "passes of this kernel, calibrated against a copy of known size",
             "algorithmic_flops_per_launch": c1.gemm_flops(),
             "kernel_ms": round(kern_ms, 5),
         },
@@ -371,6 +381,7 @@ def main():
         st = _stage_avgs(_C, _C.STAGES)
         _C.profile_enable(False)
         e["fwd_bwd_ms"] = round(fbms, 5)
+        e["bwd_workspace_mb"] = round(_bwd_workspace_bytes(_C, w, t) / 1e6, 1)
         e["fwd_bwd_real_tflops"] = round(3 * w.gemm_flops() / (fbms * 1e-3) / 1e12, 1)
         e["fwd_bwd_stages"] = _stage_report(w, st)
         others[w.name] = e
