@@ -525,7 +525,11 @@ __global__ __launch_bounds__(512) void dcn2_colgrad_kernel(const BwdParams p) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int blk = wave % NB, wr = wave / NB;
     const int kb = blk / (BN / 32), nb = blk - kb * (BN / 32);
-    const int b = blockIdx.y, n0 = blockIdx.x * BN;
+    // tiles handed to the XCDs in contiguous ranges (xcd_remap): an XCD's
+    // blocks work on neighbouring pixel rows, so the corner lines their
+    // samples share are fetched into its L2 once
+    const int tile = xcd_remap((int)(blockIdx.y * gridDim.x + blockIdx.x), (int)(gridDim.x * gridDim.y));
+    const int b = tile / (int)gridDim.x, n0 = (tile - b * (int)gridDim.x) * BN;
     const int N = p.Ho * p.Wo, KK = p.kh * p.kw, cs = p.G * p.Cgp;
     const int cpg = p.Cgp / KC, nch = KK * p.G * cpg, nmc = p.Mp / MCH;
 
