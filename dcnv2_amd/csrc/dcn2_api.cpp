@@ -198,6 +198,8 @@ BwdWorkspace bwd_workspace(const Geo &g0) {
     o += align256((size_t)gg.rows * g.Cgp * gg.row_esz);
     w.rsc = o;
     if (gg.row_scaled) o += align256((size_t)gg.rows * (g.Cgp / 32));
+    w.csum = o;  // fp32 corner sums [B][G*KK][N][4] of the fused kernel
+    if (fused_bwd_shape(g) && g.Cgp > g.KC) o += align256((size_t)g.B * g.G * g.KK * g.N * 16);
     w.rec = o;
     o += align256((size_t)gg.rows * 12);  // 12-byte sample records
     w.bcnt = o;
@@ -343,6 +345,8 @@ static int backward_impl(const Geo &g0, const void *input, const void *weight, c
         // counts itself claims rows from bcur = 0)
         clr.p[2] = (float *)(base + ws.bcnt);
         clr.n[2] = gs.B > 0 ? (ws.bcur - ws.bcnt) / sizeof(int) + (size_t)gg.nbuckets : 0;
+        clr.p[3] = (float *)(base + ws.csum);
+        clr.n[3] = ws.rec > ws.csum && gs.B > 0 ? (size_t)gs.B * g.G * g.KK * g.N * 4 : 0;
         prof_begin(DCN2_STAGE_BWD_PACK, s);
         if ((rc = check_launch(launch_pack(gs, g.xt_direct ? nullptr : in_s, (void *)xt,
                                            first ? weight : nullptr, wt, tab, true, s, &clr),
@@ -355,7 +359,8 @@ static int backward_impl(const Geo &g0, const void *input, const void *weight, c
                                  (void *)at(grad_offset, off_img), (void *)at(grad_mask, msk_img),
                                  grad_weight, grad_bias, (float *)(base + ws.gi_acc),
                                  (float *)(base + ws.gw_acc), (float *)(base + ws.gb_acc),
-                                 base + ws.cgm, base + ws.rsc, base + ws.rec, (int *)(base + ws.bcnt),
+                                 base + ws.cgm, base + ws.rsc, (float *)(base + ws.csum), base + ws.rec,
+                                 (int *)(base + ws.bcnt),
                                  (int *)(base + ws.bstart), (int *)(base + ws.bcur),
                                  (int *)(base + ws.sidx), (float *)(base + ws.ring), last, s),
                  "backward")))

@@ -61,6 +61,7 @@ struct BwdParams {
     // sample), so the storage is sized exactly and no bucket can overflow.
     void *cgm;          // [rows][Cgp] masked column gradient rows (RowOf)
     unsigned char *rsc; // [rows][Cgp/32] scale codes of bf16 rows (row_block_scale)
+    float *csum;        // [B][G*KK][N][4] corner sums of groups of several chunks (fused kernel)
     struct BucketRec *rec;  // [rows] sample records, in bucket order
     int *bcnt;          // [nbuckets] samples per bucket (count pass)
     int *bstart;        // [nbuckets + 1] first row of each bucket (exclusive scan of bcnt)
@@ -1499,18 +1500,22 @@ __device__ __forceinline__ int fused_swz_c(int n) { return ((n & 3) << 1) | ((n 
 constexpr int kFusedTrashLane = 32;
 
 
-template <typename T, bool GN>
+template <typename T, bool GN, int MP>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void dcn2_bwd_fused_kernel(const BwdParams p) {
     static_assert(sizeof(T) == 2, "2-byte types");
+    static_assert(MP == 256 || MP == 128, "128 or 256 padded output channels");
     using M = Mma<T>;
     using frag = typename M::frag;
     typedef typename RowOf<T>::type R;
     typedef short s16x4 __attribute__((ext_vector_type(4)));
     constexpr int KC = M::KC, KSTEP = M::KSTEP;
-    constexpr int BN = 64, MP = 256;
+    constexpr int BN = 64;
     constexpr int NMS = MP / KSTEP / 2;  // column-gradient MFMA steps of one M half
     constexpr int NKS = BN / KSTEP;      // grad_weight MFMA steps (over pixels)
+    constexpr int RPW = MP / 8;          // gO rows each wave stages (32 or 16)
+    constexpr int NGL = RPW / 8;         // its 1 KiB stage loads per tile (4 or 2)
+    constexpr int NI = MP / 128;         // 32-column K blocks of a wave's grad_weight rows
     constexpr int LDX = 32 + 4;          // pitch (floats) of the cg areas
     constexpr int E = 8;                 // channels of one 16-byte piece
     constexpr int NST = E * (int)sizeof(R) / 16;  // 16-byte hand-off stores per lane
@@ -1529,8 +1534,14 @@ void dcn2_bwd_fused_kernel(const BwdParams p) {
     // wave; its gathered / consumed pixels are 32P + 16mh .. +15
     const int kb = wave & 1, P = (wave >> 1) & 1, mh = wave >> 2;
     const int blk = wave & 3, px0 = 32 * P + 16 * mh;
+    // grad_weight block of this wave: rows gw_row0 .. +31 and the NI K blocks
+    // from gw_i0 (MP 256: rows 32 wave, both K blocks; MP 128: rows
+    // 32 (wave % 4), K block wave / 4)
+    const int gw_row0 = MP == 256 ? 32 * wave : 32 * (wave & 3);
+    const int gw_i0 = MP == 256 ? 0 : wave >> 2;
     const int N = p.Ho * p.Wo, KK = p.kh * p.kw, cs = p.G * p.Cgp;
-    const int nch = KK * p.G;
+    const int cpg = p.Cgp / KC;
+    const int nch = KK * p.G * cpg;
     const int tpi = p.tiles_per_img;  // tiles of BN pixels per image
     // work item = (tile range sp, chunk c) with the chunk fastest, handed to
     // XCDs in contiguous ranges: the workgroups of one XCD share tile ranges,
@@ -1544,6 +1555,8 @@ void dcn2_bwd_fused_kernel(const BwdParams p) {
     const int t_last = t_end - 1;
     const ChunkEnt ce = ((const ChunkEnt *)p.tab)[c];
     const int plane = ce.x;  // offset / mask plane g*KK + tap
+    // the chunk's first channel within its group's Cgp-wide hand-off row
+    const int cbase = ce.w - (plane / KK) * p.Cgp;
 
     // W'^T fragments of K block kb, M half mh of chunk c (pack_weight_kernel
     // layout 1: fragment (row block 2c + kb, step s) is one contiguous run of
@@ -1557,10 +1570,11 @@ void dcn2_bwd_fused_kernel(const BwdParams p) {
     }
 
     // ---- gO stage --------------------------------------------------------
-    // The wave's 32 gO rows of tile t (4 KiB): load q (of 4) lands at LDS
-    // byte go_lds(buf) + 1024 q.  Rows past Cout and pixels past N read zeros.
+    // The wave's RPW gO rows of tile t (RPW * 128 bytes): load q (of NGL)
+    // lands at LDS byte go_lds(buf) + 1024 q.  Rows past Cout and pixels past
+    // N read zeros.
     auto go_lds = [&](int buf) __attribute__((always_inline)) {
-        return lds_addr(&sG[buf][0]) + wave * 4096;
+        return lds_addr(&sG[buf][0]) + wave * (RPW * BN * (int)sizeof(T));
     };
     // Tile t = image b, pixels n0 .. n0 + BN - 1.
     struct TileId {
@@ -1576,22 +1590,23 @@ void dcn2_bwd_fused_kernel(const BwdParams p) {
             const_cast<T *>((const T *)p.gout + (size_t)id.b * p.Cout * N), (short)0, (int)go_bytes,
             0x00020000);
     };
-    // Load q of the wave's rows: NCHW rows 32 wave + 8q + l/8, 8 pieces of 8
-    // pixels; channels-last block `wave`, pixel lines 16q + l/4, 4 pieces of 8
-    // rows.  The per-lane part of the byte offset (go_lo), the pixel of the
-    // piece within the tile (go_px) and whether its row exists (go_ok).
-    int go_lo[4], go_px[4];
-    bool go_ok[4];
+    // Load q of the wave's rows: NCHW rows RPW wave + 8q + l/8, 8 pieces of 8
+    // pixels; channels-last 32-row block RPW wave / 32, pixel lines
+    // (RPW wave % 32) * 2 + 16q + l/4, 4 pieces of 8 rows.  The per-lane part
+    // of the byte offset (go_lo), the pixel of the piece within the tile
+    // (go_px) and whether its row exists (go_ok).
+    int go_lo[NGL], go_px[NGL];
+    bool go_ok[NGL];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int q = 0; q < NGL; ++q) {
         if constexpr (GN) {
-            const int n = 16 * q + (lane >> 2);
-            const int m = 32 * wave + 8 * ((lane & 3) ^ fused_swz_cl(n));
+            const int n = (RPW * wave % 32) * 2 + 16 * q + (lane >> 2);
+            const int m = (RPW * wave / 32) * 32 + 8 * ((lane & 3) ^ fused_swz_cl(n));
             go_lo[q] = (n * p.Cout + m) * (int)sizeof(T);
             go_px[q] = n;
             go_ok[q] = m < p.Cout;
         } else {
-            const int r = 32 * wave + 8 * q + (lane >> 3);
+            const int r = RPW * wave + 8 * q + (lane >> 3);
             const int n = 8 * ((lane & 7) ^ fused_swz(r));
             go_lo[q] = (r * N + n) * (int)sizeof(T);
             go_px[q] = n;
@@ -1644,10 +1659,10 @@ void dcn2_bwd_fused_kernel(const BwdParams p) {
     };
     auto go_afrag = [&](int buf, int ks) __attribute__((always_inline)) {
         if constexpr (GN) {
-            return tr_frag([&](int n, int m) { return at_nm(buf, n, m); }, ks * KSTEP, wave * 32);
+            return tr_frag([&](int n, int m) { return at_nm(buf, n, m); }, ks * KSTEP, gw_row0);
         } else {
             return *reinterpret_cast<const frag *>(
-                at_rm(buf, wave * 32 + (lane & 31), ks * KSTEP + 8 * (lane >> 5)));
+                at_rm(buf, gw_row0 + (lane & 31), ks * KSTEP + 8 * (lane >> 5)));
         }
     };
 
@@ -1830,7 +1845,8 @@ void dcn2_bwd_fused_kernel(const BwdParams p) {
 #pragma unroll
             for (int e = 0; e < E; ++e) mrow[e] = cgv[e] * d1[0];
             uint4 *row = srow >= 0
-                             ? reinterpret_cast<uint4 *>((R *)p.cgm + (size_t)srow * KC + kb * 32 + cq * E)
+                             ? reinterpret_cast<uint4 *>((R *)p.cgm + (size_t)srow * p.Cgp + cbase + kb * 32 +
+                                                         cq * E)
                              : trash_v;
             if constexpr (kRowScaled<T>) {
                 // the pixel's quad of lanes holds 32-channel block kb of the row
@@ -1838,8 +1854,9 @@ void dcn2_bwd_fused_kernel(const BwdParams p) {
                 const float f = row_block_scale(mrow, code);
 #pragma unroll
                 for (int e = 0; e < E; ++e) mrow[e] *= f;
-                unsigned char *sc = srow >= 0 && cq == 0 ? p.rsc + (size_t)srow * (KC / 32) + kb
-                                                         : reinterpret_cast<unsigned char *>(trash_v) + 8;
+                unsigned char *sc = srow >= 0 && cq == 0
+                                        ? p.rsc + (size_t)srow * (p.Cgp / 32) + cbase / 32 + kb
+                                        : reinterpret_cast<unsigned char *>(trash_v) + 8;
                 *sc = (unsigned char)code;
             }
 #pragma unroll
@@ -1870,6 +1887,18 @@ void dcn2_bwd_fused_kernel(const BwdParams p) {
         const int b = id.b;
         const int nr = id.n0 + lane;
         const f32x4 S = sS[0][lane] + sS[1][lane];
+        if (cpg > 1) {
+            // a group of several chunks: this chunk's part of the corner sums
+            // goes to p.csum, summed over the group's chunks there, and
+            // dcn2_corner_finish_kernel turns the totals into grad_offset /
+            // grad_mask
+            float *cs4 = p.csum + (((size_t)b * p.G * KK + plane) * N + (nr < N ? nr : 0)) * 4;
+            if (nr < N) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) unsafeAtomicAdd(cs4 + q, S[q]);
+            }
+            return;
+        }
         const f32x4 d1 = sD[buf][lane][1];
         const int valid = sV[buf][lane];
         const float mv = d1[0], fly = d1[2], flx = d1[3];
@@ -1888,13 +1917,14 @@ void dcn2_bwd_fused_kernel(const BwdParams p) {
         T *gmp = p.gmask ? (T *)p.gmask + (size_t)b * p.msk_bs + (size_t)plane * N + nr : trash_t + 2;
         *(live ? gmp : trash_t + 2) = from_f32<T>(gm);
     };
-    f32x16 gacc[2];  // gW rows 32 wave .., K blocks 0 and 1
+    f32x16 gacc[NI];  // gW rows gw_row0 .., K blocks gw_i0 ..
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < NI; ++i)
 #pragma unroll
         for (int r = 0; r < 16; ++r) gacc[i][r] = 0.0f;
     float bsum = 0.0f;
-    const bool do_bias = p.gb_acc != nullptr && c == 0;
+    // (grad_bias once per row: from chunk 0, by the waves of K block 0)
+    const bool do_bias = p.gb_acc != nullptr && c == 0 && gw_i0 == 0;
     // acc + the sum of a fragment's 8 values (four 2-element dot products
     // with (1, 1), accumulated in fp32)
     auto sum8 = [](frag a, float acc) __attribute__((always_inline)) {
@@ -1919,22 +1949,25 @@ void dcn2_bwd_fused_kernel(const BwdParams p) {
     // grad_weight B fragments (columns of the tile in sC[cb]) and MFMA j =
     // 2 ks + i of gW += gO cols^T (grad_bias: compile-time switch, so no
     // branch sits between the MFMAs)
-    auto read_bfrags = [&](int cb, frag (&b)[NKS][2]) __attribute__((always_inline)) {
+    auto read_bfrags = [&](int cb, frag (&b)[NKS][NI]) __attribute__((always_inline)) {
         const auto atc = [&](int n, int k) __attribute__((always_inline)) { return at_c(cb, n, k); };
 #pragma unroll
         for (int ks = 0; ks < NKS; ++ks)
 #pragma unroll
-            for (int i = 0; i < 2; ++i) b[ks][i] = tr_frag(atc, ks * KSTEP, i * 32);
+            for (int i = 0; i < NI; ++i) b[ks][i] = tr_frag(atc, ks * KSTEP, (gw_i0 + i) * 32);
     };
-    auto gradw_mma = [&](const frag (&a)[NKS], const frag (&b)[NKS][2], int j, auto bias_c)
+    // MFMA point j (0 .. 2 NKS - 1) of a tile's grad_weight: MP 256 runs one
+    // MFMA at every point (j = 2 ks + i), MP 128 one at every even point
+    auto gradw_mma = [&](const frag (&a)[NKS], const frag (&b)[NKS][NI], int j, auto bias_c)
         __attribute__((always_inline)) {
-        const int ks = j >> 1, i = j & 1;
+        if (NI == 1 && (j & 1)) return;
+        const int ks = j >> 1, i = NI == 2 ? (j & 1) : 0;
         gacc[i] = M::mma(a[ks], b[ks][i], gacc[i]);
         if constexpr (decltype(bias_c)::value)
-            if (i == 1) bsum = sum8(a[ks], bsum);
+            if (i == NI - 1) bsum = sum8(a[ks], bsum);
     };
     auto gradw = [&](const frag (&a)[NKS], int cb, auto bias_c) __attribute__((always_inline)) {
-        frag b[NKS][2];
+        frag b[NKS][NI];
         read_bfrags(cb, b);
 #pragma unroll
         for (int j = 0; j < 2 * NKS; ++j) gradw_mma(a, b, j, bias_c);
@@ -1975,7 +2008,7 @@ void dcn2_bwd_fused_kernel(const BwdParams p) {
             const f32x4 goff = gather_offsets(0);
             const __amdgpu_buffer_rsrc_t grs = go_rsrc(id0), xrs = xt_rsrc(id0);
 #pragma unroll
-            for (int q = 0; q < 4; ++q) dma16(grs, go_off(id0, q), go_lds(0) + q * 1024);
+            for (int q = 0; q < NGL; ++q) dma16(grs, go_off(id0, q), go_lds(0) + q * 1024);
             gather(xrs, goff, rawset[0]);
         }
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the stage loads
@@ -2007,7 +2040,7 @@ void dcn2_bwd_fused_kernel(const BwdParams p) {
             // tile t+1's corner gathers into the other register set: nothing
             // waits for them before tile t+1's phase B
             gather(xt_rsrc(itn), gather_offsets(d3n), rawset[buf ^ 1]);
-            frag gb[NKS][2];
+            frag gb[NKS][NI];
             if constexpr (!first) read_bfrags(buf ^ 1, gb);
             consume(buf, d3, rawset[buf], [&](int j) __attribute__((always_inline)) {
                 if constexpr (!first) gradw_mma(ga, gb, j, bias_c);
@@ -2038,21 +2071,59 @@ void dcn2_bwd_fused_kernel(const BwdParams p) {
     if (do_bias) tiles(std::true_type{});
     else tiles(std::false_type{});
 
-    // grad_weight block of this workgroup: rows 32 wave .., columns c*KC ..
+    // grad_weight block of this wave: rows gw_row0 .., columns c*KC + 32 (gw_i0 + i) ..
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int k = c * KC + i * 32 + (lane & 31);
+    for (int i = 0; i < NI; ++i) {
+        const int k = c * KC + (gw_i0 + i) * 32 + (lane & 31);
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            const int m = wave * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            const int m = gw_row0 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
             if (m < p.Cout) unsafeAtomicAdd(p.gw_acc + (size_t)m * p.Kp + k, gacc[i][r]);
         }
     }
     if (do_bias) {
         const float v = bsum + shfl_xor_f(bsum, 32);
-        const int m = wave * 32 + (lane & 31);
+        const int m = gw_row0 + (lane & 31);
         if (lane < 32 && m < p.Cout) unsafeAtomicAdd(p.gb_acc + m, v);
     }
+}
+
+// ---------------------------------------------------------------------------
+// grad_offset / grad_mask of the fused kernel for groups of several channel
+// chunks: the corner sums S_q of a sample, summed over the group's chunks in
+// csum by the fused kernel's workgroups, become the coordinate and mask
+// gradients (com.cu:431-501), with the sample position, corner validity and
+// mask value recomputed from the offsets exactly as the fused kernel's
+// sampler does.  One thread per sample (pixel n, plane g*KK + tap, image b).
+template <typename T>
+__global__ __launch_bounds__(256) void dcn2_corner_finish_kernel(const BwdParams p) {
+    const int n = blockIdx.x * 256 + threadIdx.x;
+    const int plane = blockIdx.y, b = blockIdx.z;
+    const int N = p.Ho * p.Wo, KK = p.kh * p.kw;
+    if (n >= N) return;
+    const int tap = plane % KK, ki = tap / p.kw, kj = tap - ki * p.kw;
+    const int oy = n / p.Wo, ox = n - oy * p.Wo;
+    const T *offs = (const T *)p.offset + (size_t)b * p.off_bs + (size_t)plane * 2 * N;
+    const float y = (float)(oy * p.sh - p.ph + ki * p.dh) + to_f32(offs[n]);
+    const float x = (float)(ox * p.sw - p.pw + kj * p.dw) + to_f32(offs[N + n]);
+    float mv = 1.0f;
+    if (p.mask) {
+        mv = to_f32(((const T *)p.mask)[(size_t)b * p.msk_bs + (size_t)plane * N + n]);
+        if (p.msk_logit) mv = mask_value(mv, 1);
+    }
+    const SamplePos sp = sample_pos(y, x, p.H, p.W);
+    const f32x4 S = *reinterpret_cast<const f32x4 *>(p.csum + (((size_t)b * p.G * KK + plane) * N + n) * 4);
+    const float S0 = sp.vy0 && sp.vx0 ? S[0] : 0.0f, S1 = sp.vy0 && sp.vx1 ? S[1] : 0.0f;
+    const float S2 = sp.vy1 && sp.vx0 ? S[2] : 0.0f, S3 = sp.vy1 && sp.vx1 ? S[3] : 0.0f;
+    const float fly = sp.ly, flx = sp.lx, hy = 1.0f - fly, hx = 1.0f - flx;
+    const float goy = mv * (hx * (S2 - S0) + flx * (S3 - S1));
+    const float gox = mv * (hy * (S1 - S0) + fly * (S3 - S2));
+    const float gmr = hy * hx * S0 + hy * flx * S1 + fly * hx * S2 + fly * flx * S3;
+    const float gm = p.msk_logit ? gmr * mv * (1.0f - mv) : gmr;
+    T *go = (T *)p.goff + (size_t)b * p.off_bs + (size_t)plane * 2 * N + n;
+    go[0] = from_f32<T>(goy);
+    go[N] = from_f32<T>(gox);
+    if (p.gmask) ((T *)p.gmask)[(size_t)b * p.msk_bs + (size_t)plane * N + n] = from_f32<T>(gm);
 }
 
 // ---------------------------------------------------------------------------
@@ -3025,6 +3096,18 @@ __global__ __launch_bounds__(256) void finalize_gi_nhwc_kernel(const float *__re
 }
 
 // ---------------------------------------------------------------------------
+// The fused kernel (column gradient and grad_weight in one pass) serves
+// 2-byte types with Mp of 128 or 256 (one M chunk), and images of gO and xt
+// below 2 GiB each; the launch also needs gO rows that take 16-byte loads.
+// Groups of several K chunks (Cgp > KC) add their corner sums up in csum.
+// Option DCN2_OPT_BWD_FUSED = 0 selects the two-kernel path for every shape
+// (the tests compare both paths).
+bool fused_bwd_shape(const Geo &g) {
+    return g.esz == 2 && g.opt_fused != 0 && (g.Mp == 256 || g.Mp == 128) &&
+           (long long)g.Cout * g.N * g.esz <= kGoOutOfRange &&
+           (long long)g.H * g.W * g.cs * g.esz <= kGoOutOfRange;
+}
+
 template <typename T>
 static hipError_t backward_t(const Geo &g, const BwdParams &p0, void *grad_input,
                              void *grad_weight, void *grad_bias, bool last, hipStream_t s) {
@@ -3038,11 +3121,6 @@ static hipError_t backward_t(const Geo &g, const BwdParams &p0, void *grad_input
         hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         ncu <= 0)
         ncu = 256;
-    // The fused kernel (column gradient and grad_weight in one pass) serves
-    // 2-byte types with Mp == 256, one K chunk per deformable group, gO rows
-    // that take 16-byte loads, and images of gO and xt below 2 GiB each.
-    // Option DCN2_OPT_BWD_FUSED = 0 selects the two-kernel path for every
-    // shape (the tests compare both paths).
     // grad_weight / grad_bias finalisation (run by the grad_input finalisation
     // launch of the last slice, or alone for an empty batch; the earlier
     // slices only accumulate, nblk = 0)
@@ -3060,11 +3138,7 @@ static hipError_t backward_t(const Geo &g, const BwdParams &p0, void *grad_input
     gwf.G = g.G;
     gwf.Kp = g.Kp;
     gwf.nblk = last ? (std::max<long>((long)g.Cout * g.Cw * g.KK, g.Cout) + 255) / 256 : 0;
-    bool fused = false;
-    if constexpr (sizeof(T) == 2)
-        fused = g.opt_fused != 0 && g.Mp == 256 && g.Cgp == g.KC && p.go_vec &&
-                (long long)g.Cout * g.N * (long long)sizeof(T) <= kGoOutOfRange &&
-                (long long)g.H * g.W * g.cs * (long long)sizeof(T) <= kGoOutOfRange;
+    const bool fused = fused_bwd_shape(g) && p.go_vec;
     if (g.B > 0) {
         // 2. column gradient: grad_offset, grad_mask, grad_input accumulation
         //    (and grad_weight / grad_bias when fused)
@@ -3098,13 +3172,26 @@ static hipError_t backward_t(const Geo &g, const BwdParams &p0, void *grad_input
                     // one workgroup per CU: each K chunk gets CUs/nch ranges of
                     // 64-pixel tiles
                     BwdParams pf = p;
-                    const int nch = g.KK * g.G;
+                    const int cpg = g.Cgp / g.KC, nch = g.KK * g.G * cpg;
                     pf.tiles_per_img = ceil_div(g.N, 64);
                     pf.splits = std::max(1, std::min(ncu / nch, g.B * pf.tiles_per_img));
                     const int grid = pf.splits * nch;
-                    if (p.go_nhwc) dcn2_bwd_fused_kernel<T, true><<<grid, 512, 0, s>>>(pf);
-                    else dcn2_bwd_fused_kernel<T, false><<<grid, 512, 0, s>>>(pf);
+#define DCN2_FUSED(MPV)                                                                     \
+    do {                                                                                    \
+        if (p.go_nhwc) dcn2_bwd_fused_kernel<T, true, MPV><<<grid, 512, 0, s>>>(pf);       \
+        else dcn2_bwd_fused_kernel<T, false, MPV><<<grid, 512, 0, s>>>(pf);                \
+    } while (0)
+                    if (g.Mp == 256) DCN2_FUSED(256);
+                    else DCN2_FUSED(128);
+#undef DCN2_FUSED
                     if ((e = hipGetLastError()) != hipSuccess) return e;
+                    // groups of several chunks: grad_offset / grad_mask from
+                    // the corner sums the chunks added up in csum
+                    if (cpg > 1) {
+                        dcn2_corner_finish_kernel<T>
+                            <<<dim3(ceil_div(g.N, 256), g.G * g.KK, g.B), 256, 0, s>>>(pf);
+                        if ((e = hipGetLastError()) != hipSuccess) return e;
+                    }
                 }
             }
         }
@@ -3289,8 +3376,8 @@ hipError_t launch_backward(const Geo &g, const void *xt, const void *wt, const v
                            const void *mask, const void *grad_out, void *grad_input,
                            void *grad_offset, void *grad_mask, void *grad_weight, void *grad_bias,
                            float *gi_acc, float *gw_acc, float *gb_acc, void *cgm, void *rsc,
-                           void *rec, int *bcnt, int *bstart, int *bcur, int *sidx, float *ring,
-                           bool last, hipStream_t s) {
+                           float *csum, void *rec, int *bcnt, int *bstart, int *bcur, int *sidx,
+                           float *ring, bool last, hipStream_t s) {
     BwdParams p;
     p.xt = xt;
     p.wt = wt;
@@ -3332,6 +3419,7 @@ hipError_t launch_backward(const Geo &g, const void *xt, const void *wt, const v
     const GatherGeo gg = gather_geometry(g);
     p.cgm = cgm;
     p.rsc = (unsigned char *)rsc;
+    p.csum = csum;
     p.rec = (BucketRec *)rec;
     p.bcnt = bcnt;
     p.bstart = bstart;

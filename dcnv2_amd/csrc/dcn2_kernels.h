@@ -66,7 +66,7 @@ struct FwdWorkspace {
 FwdWorkspace fwd_workspace(const Geo &g);
 
 struct BwdWorkspace {
-    size_t xt, wt, tab, gi_acc, gw_acc, gb_acc, cgm, rsc, rec, bcnt, bstart, bcur, sidx, ring, total;
+    size_t xt, wt, tab, gi_acc, gw_acc, gb_acc, cgm, rsc, csum, rec, bcnt, bstart, bcur, sidx, ring, total;
 };
 // Carves the backward workspace of one slice of g.Bs images.
 // Border-ring pixels of one grad_input gather window (4 x the cell tile side).
@@ -92,11 +92,12 @@ GatherGeo gather_geometry(const Geo &g);
 // dcn2_pack.hip: input -> xt (skipped when input is null) and weight -> wp +
 // chunk table (skipped when weight is null) in one launch; transpose selects the backward's W'^T fragment
 // order.  The input is NCHW, or channels-last when g.nhwc.
-// Up to three fp32 buffers the pack launch also zeroes (extra workgroups), so
+// Up to kClearBufs fp32 buffers the pack launch also zeroes (extra workgroups), so
 // the backward's accumulators need no launch of their own; n = 0 skips one.
+constexpr int kClearBufs = 4;
 struct ClearList {
-    float *p[3];
-    size_t n[3];
+    float *p[kClearBufs];
+    size_t n[kClearBufs];
 };
 hipError_t launch_pack(const Geo &g, const void *input, void *xt, const void *weight, void *wp,
                        void *tab, bool transpose, hipStream_t s, const ClearList *clear = nullptr);
@@ -121,7 +122,10 @@ hipError_t launch_backward(const Geo &g, const void *xt, const void *wt, const v
                            const void *mask, const void *grad_out, void *grad_input,
                            void *grad_offset, void *grad_mask, void *grad_weight, void *grad_bias,
                            float *gi_acc, float *gw_acc, float *gb_acc, void *cgm, void *rsc,
-                           void *rec, int *bcnt, int *bstart, int *bcur, int *sidx, float *ring,
-                           bool last, hipStream_t s);
+                           float *csum, void *rec, int *bcnt, int *bstart, int *bcur, int *sidx,
+                           float *ring, bool last, hipStream_t s);
+// Whether the fused backward kernel may serve g (2-byte type, Cout <= 256),
+// and whether it then needs the corner-sum buffer (several chunks per group).
+bool fused_bwd_shape(const Geo &g);
 
 }  // namespace dcn2

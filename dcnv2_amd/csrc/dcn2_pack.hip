@@ -34,9 +34,9 @@ struct PackParams {
     int transpose;                 // 0: forward A fragments, 1: backward W'^T fragments
     int nhwc;                      // input is channels-last [B][HW][C]
     int nw;                        // weight blocks
-    float4 *clr[3];                // buffers to zero, 16-byte pieces each
-    long clr_n4[3];
-    int clr_blk[4];                // first clearing block of each buffer (prefix sums)
+    float4 *clr[kClearBufs];       // buffers to zero, 16-byte pieces each
+    long clr_n4[kClearBufs];
+    int clr_blk[kClearBufs + 1];   // first clearing block of each buffer (prefix sums)
 };
 constexpr int kClearPieces = 1024;  // 16-byte pieces zeroed per clearing block
 
@@ -218,7 +218,9 @@ __global__ __launch_bounds__(256) void pack_kernel(const PackParams p) {
     } else {
         // zero kClearPieces 16-byte pieces of one of the clear-list buffers
         const int cb = blk - p.nin - p.nw;
-        const int i = cb < p.clr_blk[1] ? 0 : (cb < p.clr_blk[2] ? 1 : 2);
+        int i = 0;
+#pragma unroll
+        for (int k = 1; k < kClearBufs; ++k) i = cb >= p.clr_blk[k] ? k : i;
         const long base = (long)(cb - p.clr_blk[i]) * kClearPieces;
         for (int k = threadIdx.x; k < kClearPieces; k += 256)
             if (base + k < p.clr_n4[i]) p.clr[i][base + k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
@@ -266,13 +268,13 @@ static hipError_t pack_t(const Geo &g, const void *input, void *xt, const void *
     const long nw = weight ? ((long)g.Mp * g.Kp / E + 255) / 256 : 0;
     p.nw = (int)nw;
     p.clr_blk[0] = 0;
-    for (int i = 0; i < 3; ++i) {
+    for (int i = 0; i < kClearBufs; ++i) {
         const size_t n = clear ? clear->n[i] : 0;
         p.clr[i] = n ? (float4 *)clear->p[i] : nullptr;
         p.clr_n4[i] = (long)((n + 3) / 4);
         p.clr_blk[i + 1] = p.clr_blk[i] + (int)((p.clr_n4[i] + kClearPieces - 1) / kClearPieces);
     }
-    const long blocks = p.nin + nw + p.clr_blk[3];
+    const long blocks = p.nin + nw + p.clr_blk[kClearBufs];
     pack_kernel<T><<<(unsigned)blocks, 256, 0, s>>>(p);
     return hipGetLastError();
 }

@@ -601,6 +601,50 @@ def test_fused_backward(dtype, case):
                 check(f"{name} ({'fused' if fused else 'two kernels'})", g, r, TOL[dtype])
 
 
+@pytest.mark.parametrize("case", [
+    # C, deformable groups, Cout, H, W, stride, pad, dilation, mask and bias, grad_output channels_last
+    (128, 1, 128, 23, 32, 2, 2, 2, True, False),   # the c4 shape class: two chunks, stride 2, dilation 2
+    (256, 1, 100, 14, 12, 1, 1, 1, True, False),   # four chunks per group, Cout not a multiple of 32
+    (96, 1, 64, 15, 16, 1, 1, 1, False, False),    # 96 channels padded to two chunks; no mask, no bias
+    (256, 2, 256, 11, 16, 1, 1, 1, True, False),   # 256 padded rows, two groups of two chunks
+    (128, 1, 120, 13, 11, 2, 1, 1, True, True),    # channels-last grad_output, N % 8 != 0
+    (64, 1, 128, 12, 14, 1, 1, 1, True, False),    # 128 rows, one chunk per group
+], ids=["c4_class", "chunks4_cout100", "c96_nomask", "mp256_dg2_chunks2", "go_channels_last",
+        "mp128_one_chunk"])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32],
+                         ids=["float16", "bfloat16", "float32"])
+def test_fused_backward_several_chunks(dtype, case):
+    """The fused backward kernel on up to 128 output channels (one 128-row M
+    chunk) and on deformable groups of several 64-channel chunks, whose corner
+    sums each chunk adds to a per-sample buffer that a second launch turns
+    into grad_offset / grad_mask.  f16 and bf16 run the fused and the
+    two-kernel path, fp32 (which the fused kernel does not serve) the
+    two-kernel path whatever the option says; all five gradients against the
+    oracle.  (NCHW grad_output needs Ho*Wo % 8 == 0 for the fused kernel's
+    16-byte row loads.)"""
+    C, G, Cout, H, W, s, p, d, mb, go_cl = case
+    w = CONFIGS[0].with_(B=2, C=C, H=H, W=W, Cout=Cout, k=3, stride=s, pad=p, dil=d, groups=G,
+                         seed=29, offset_dist="uniform:6", mask_dist="uniform", backward=True)
+    t = make_inputs(w, dtype=dtype)
+    if not mb:
+        t["mask"] = None
+        t["bias"] = None
+    geo = w.geometry()
+    go = t["grad_output"].to(DEV)
+    if go_cl:
+        go = go.to(memory_format=torch.channels_last)
+    rg = oracle_backward(t, geo)
+    for fused in (True, False):
+        print(f"{dtype} {case} fused={fused}", flush=True)
+        grads, gradw_launches = _backward_path(t, geo, go, fused)
+        assert (gradw_launches == 0) == (fused and dtype != torch.float32), "fused kernel selection"
+        if not mb:
+            assert grads[2] is None and grads[4] is None
+        for name, g, r in zip(GRADS, grads, rg):
+            if g is not None:
+                check(f"{name} ({'fused' if fused else 'two kernels'})", g, r, TOL[dtype])
+
+
 @pytest.mark.parametrize("scale_exp", [100, -100, 0], ids=["x2^100", "x2^-100", "x1"])
 @pytest.mark.parametrize("path", [(-1, 1), (0, 1), (-1, 0)], ids=["fused_by_cells", "two_kernels_by_cells",
                                                                  "fused_per_pixel"])

@@ -48,25 +48,31 @@ def _budget(x, weight, geo, go_layout=0, in_layout=0, images=2):
     return n
 
 
-def _sliced(fn):
-    """Runs fn() with the pack stage's launches counted; returns (result, slices)."""
+def _sliced(fn, gradw=False):
+    """Runs fn() with the pack stage's launches counted; returns (result,
+    slices), and with gradw also the launches of the separate grad_weight
+    stage (none when the fused kernel ran)."""
     _C.profile_enable(True)
     try:
         _C.profile_read("bwd_pack")
+        _C.profile_read("bwd_gradw")
         out = fn()
         torch.cuda.synchronize()
-        return out, _C.profile_read("bwd_pack")[1]
+        slices = _C.profile_read("bwd_pack")[1]
+        return (out, slices, _C.profile_read("bwd_gradw")[1]) if gradw else (out, slices)
     finally:
         _C.profile_enable(False)
 
 
 @pytest.mark.parametrize("case", [
     # dtype, C, deformable groups, Cout, H, W, option bwd_fused
-    (torch.float16, 64, 1, 256, 17, 18, -1),   # fused column gradient + grad_weight
+    # (Ho*Wo % 8 == 0 where the fused kernel is to run: 16-byte grad_output rows)
+    (torch.float16, 64, 1, 256, 17, 16, -1),   # fused column gradient + grad_weight
     (torch.float16, 64, 1, 256, 17, 18, 0),    # two kernels
-    (torch.bfloat16, 64, 1, 200, 18, 17, -1),  # fused, Cout not a multiple of 32
+    (torch.bfloat16, 64, 1, 200, 18, 16, -1),  # fused, Cout not a multiple of 32
     (torch.float32, 24, 2, 40, 17, 19, -1),    # fp32, two padded groups (two kernels)
-], ids=["f16_fused", "f16_two_kernels", "bf16_fused", "f32_dg2"])
+    (torch.float16, 128, 1, 128, 17, 16, -1),  # fused, two chunks per group: corner sums per slice
+], ids=["f16_fused", "f16_two_kernels", "bf16_fused", "f32_dg2", "f16_fused_two_chunks"])
 @pytest.mark.parametrize("push", [1, 0], ids=["by_cells", "per_pixel"])
 def test_backward_in_slices_vs_oracle(case, push):
     dtype, C, G, Cout, H, W, fused = case
@@ -78,8 +84,9 @@ def test_backward_in_slices_vs_oracle(case, push):
     go = t["grad_output"].to(DEV)
     with _C.option("gi_push", push), _C.option("bwd_fused", fused):
         with _C.option("bwd_slice_bytes", _budget(dev[0], dev[1], geo)):
-            grads, slices = _sliced(lambda: _C.dcn_v2_backward(*dev, go, *_args(geo)))
+            grads, slices, gradw = _sliced(lambda: _C.dcn_v2_backward(*dev, go, *_args(geo)), True)
     assert slices == 3, "5 images in slices of 2 + 2 + 1"
+    assert (gradw == 0) == (fused != 0 and dtype != torch.float32), "fused kernel selection"
     for name, g, r in zip(GRADS, grads, rg):
         check(f"{name} (sliced)", g, r, TOL[dtype])
 
