@@ -163,7 +163,7 @@ def _ws(L, **kw):
 
 def test_backward_workspace_slices_the_batch(L):
     """The backward runs the batch in slices of whole images whose workspace
-    fits the slice budget (default 192 MiB): c2 (188 MB) and c4 (182 MB) fit in
+    fits the slice budget (default 192 MiB): c2 (188 MB) and c4 (187 MB) fit in
     one slice; c3 (B16 C256 64x64 dg4 bf16, 23.6 MB per image, 382 MB in one
     piece) runs as two slices of eight images, within 200 MB.  A smaller budget gives equal
     slices (B = 7 with room for 3 images: 3 + 2 + 2, workspace of 3), and a
