@@ -20,9 +20,11 @@
 //       blended from the same corner gathers; grad_bias from the same gO
 //  otherwise       dcn2_colgrad_kernel (all but grad_weight) and a grad_weight
 //                  kernel that re-samples the columns
-//  gather          grad_input pulled per pixel from the bucket rows of each
-//                  cell tile (no atomics), border rings merged afterwards
-//  finalize        fp32 accumulators -> caller dtype and layout.
+//  grad_input      per cell tile, from the tile's bucket rows (no atomics):
+//                  summed by cells or pulled per pixel, written straight to
+//                  grad_input in the caller's type and layout; then the
+//                  tile-boundary pixels from the tiles' border rings (and
+//                  grad_weight / grad_bias in the same launch).
 #include <algorithm>
 #include <cstddef>
 #include <cstdlib>
@@ -1151,7 +1153,6 @@ __global__ __launch_bounds__(512) void dcn2_gradw_kernel(const BwdParams p) {
     };
 
     // One step for tile t (the it-th of this work item, set S = it % 2).
-    const int t_last = t_end - 1;
     auto step = [&](auto s_c, int t) __attribute__((always_inline)) {
         constexpr int S = decltype(s_c)::value;
         constexpr int O = S ^ 1;
@@ -2136,21 +2137,26 @@ __global__ __launch_bounds__(256) void dcn2_corner_finish_kernel(const BwdParams
 // and 11 of (py-1, px-1), so its value is the sum over the batch's records of
 // those four cells of (bilinear corner weight) x (masked column-gradient
 // row), computed in a register with up to two batches of row loads in
-// flight.  Interior pixels (reachable from this tile's cells only) are added
-// by a plain read-modify-write; the sums of the one-pixel border ring, shared
-// with the neighbouring tiles, are stored per bucket (kRing pixels; the first
-// batch stores, later batches add) and merged by ring_merge_kernel.  Every
-// entry of the ring is written on every call, an empty bucket's included.
-// This replaces the global atomic per (sample, corner, channel) of the
-// reference's col2im scatter (com.cu:553-609) with plain stores.
+// flight.  Interior pixels (reachable from this tile's cells only) are final
+// after the bucket's last batch: they are staged in LDS in the caller's type
+// and written straight to grad_input in its layout (a bucket of several
+// batches keeps their partial sums in gi_acc between batches).  The sums of
+// the one-pixel border ring, shared with the neighbouring tiles, are stored
+// per bucket (kRing pixels; the first batch stores, later batches add), and
+// ring_final_kernel, launched after this kernel, writes every tile-boundary
+// pixel of grad_input from the rings that hold it.  Every entry of the ring
+// is written on every call, an empty bucket's included.  This replaces the
+// global atomic per (sample, corner, channel) of the reference's col2im
+// scatter (com.cu:553-609) with plain stores.
 constexpr int kGatherBatch = 4096;  // records of one batch the LDS sort holds
 // Buffer offset past one batch's rows (the host keeps kGatherBatch * Cgp * esz
 // below it), so a load there reads 0.
 constexpr int kGatherOutOfRange = 0x7ffffff0;
-// static LDS of dcn2_gi_gather_kernel: cell counts and starts, sorted slots and fractions
-// (plus the sorted scale codes of bf16 rows)
+// static LDS of dcn2_gi_gather_kernel: cell counts and starts, sorted slots and fractions,
+// each wave's 8 pixels of grad_input for the NCHW write-out (one channel chunk of 128
+// bytes per pixel), plus the sorted scale codes of bf16 rows
 constexpr int kGatherStaticLds = kCellTile * kCellTile * 4 + (kCellTile * kCellTile + 1) * 4 +
-                                 kGatherBatch * 2 + kGatherBatch * 8;
+                                 kGatherBatch * 2 + kGatherBatch * 8 + 8 * 8 * 128;
 constexpr int gather_static_lds(bool scaled) { return kGatherStaticLds + (scaled ? kGatherBatch * 2 : 4); }
 
 template <typename T>
@@ -2163,9 +2169,13 @@ __global__ __launch_bounds__(512) void dcn2_gi_gather_kernel(const BwdParams p) 
     __shared__ unsigned short sslot[kGatherBatch];    // row in the batch, sorted by cell
     __shared__ float2 sfrac[kGatherBatch];            // (ly, lx), sorted by cell
     __shared__ unsigned short ssc[kRowScaled<T> ? kGatherBatch : 2];  // bf16 rows: the chunk's scale codes
-    static_assert(sizeof(ccnt) + sizeof(cstart) + sizeof(sslot) + sizeof(sfrac) + sizeof(ssc) ==
+    // each wave's 8 pixels of one channel chunk, transposed for the NCHW write-out
+    __shared__ __attribute__((aligned(16))) T stage[8][8 * KC];
+    static_assert(sizeof(ccnt) + sizeof(cstart) + sizeof(sslot) + sizeof(sfrac) + sizeof(ssc) +
+                          sizeof(stage) ==
                       gather_static_lds(kRowScaled<T>),
                   "the launch's occupancy cap assumes this static LDS");
+    static_assert(KC * sizeof(T) == 128, "one channel chunk of a pixel is 128 bytes");
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int nb = p.B * p.G * p.nty * p.ntx;
@@ -2182,7 +2192,7 @@ __global__ __launch_bounds__(512) void dcn2_gi_gather_kernel(const BwdParams p) 
     for (int base = 0; base == 0 || base < count; base += kGatherBatch) {
         const int nrec = min(count - base, kGatherBatch);
         const BucketRec *__restrict__ recs = p.rec + (size_t)row0 + base;
-        const bool first = base == 0;
+        const bool first = base == 0, last = base + kGatherBatch >= count;
         if (!first) __syncthreads();  // the previous batch is done with the LDS arrays
 
         // 1. counting sort by cell (cell = local row * TS + local column)
@@ -2271,11 +2281,19 @@ __global__ __launch_bounds__(512) void dcn2_gi_gather_kernel(const BwdParams p) 
             const __amdgpu_buffer_rsrc_t rrs = __builtin_amdgcn_make_buffer_rsrc(
                 const_cast<R *>(rows), (short)0, nrec * row_bytes, 0x00020000);
             const int slice = co * 16 * NLD;
-            for (int pl0 = wave * PPW; pl0 < TW * TW; pl0 += 8 * PPW) {
-                const int pl = pl0 + ps;
-                const int py = pl / TW, px = pl - py * TW;
+            // Passes of PPW pixels: pass qp < NSEG takes window row qp / 2,
+            // columns 1 + 8 (qp % 2) .. +7 (8 of the tile's own pixels, 8-aligned
+            // in the image); the later passes take the left ring column (px = 0)
+            // PPW rows at a time.
+            constexpr int NSEG = 2 * TW, NPASS = NSEG + (TW + PPW - 1) / PPW;
+            static_assert(PPW == 8 && 1 + 8 * 2 == TW, "two 8-pixel segments per window row");
+            for (int qp = wave; qp < NPASS; qp += 8) {
+                const bool seg = qp < NSEG;  // (uniform over the wave)
+                const int py = seg ? qp >> 1 : (qp - NSEG) * PPW + ps;
+                const int px = seg ? 1 + 8 * (qp & 1) + ps : 0;
+                const bool inwin = py < TW;
                 const int Y = oy + py, X = ox + px;
-                const bool live = pl < TW * TW && Y >= 0 && Y < p.H && X >= 0 && X < p.W;
+                const bool live = inwin && Y >= 0 && Y < p.H && X >= 0 && X < p.W;
                 // record ranges of the four cells whose corner q is this pixel
                 int beg[4], len[4];
 #pragma unroll
@@ -2363,28 +2381,30 @@ __global__ __launch_bounds__(512) void dcn2_gi_gather_kernel(const BwdParams p) 
                     __builtin_amdgcn_sched_barrier(0);
                 }
                 // Interior pixels (reachable from this tile's cells only) are this
-                // block's alone: the first batch writes them (zeros included, so
-                // the accumulator needs no clearing), later batches add.  The
-                // accumulator's padding channels (Cg..Cgp of a group) are never
-                // read back (and receive zeros), so whole 16-byte pieces are
-                // written (a guarded update per channel made every channel a
-                // separate round trip).
-                if (py >= 1 && py <= TS - 1 && px >= 1 && px <= TS - 1) {
-                    if (!live || (!first && tot == 0)) continue;
-                    f32x4 *d4 = reinterpret_cast<f32x4 *>(gi + ((size_t)Y * p.W + X) * cs + cc * KC + co * EPL);
-                    f32x4 acc4[EPL / 4];
+                // block's alone.  With one batch their sums are final; with
+                // several, the batches before the last keep the partial sums in
+                // gi_acc (the first writes them, so it needs no clearing) and the
+                // last adds them back.  The accumulator's padding channels
+                // (Cg..Cgp of a group) are never read back, so whole 16-byte
+                // pieces are written.
+                const bool inner = py >= 1 && py <= TS - 1 && px >= 1 && px <= TS - 1;
+                if (inner) {
+                    if (live && (first || last || tot > 0)) {
+                        f32x4 *d4 =
+                            reinterpret_cast<f32x4 *>(gi + ((size_t)Y * p.W + X) * cs + cc * KC + co * EPL);
 #pragma unroll
-                    for (int i = 0; i < EPL / 4; ++i) acc4[i] = first ? f32x4{0.0f, 0.0f, 0.0f, 0.0f} : d4[i];
+                        for (int i = 0; i < EPL / 4; ++i) {
+                            f32x4 v = f32x4{sum[4 * i], sum[4 * i + 1], sum[4 * i + 2], sum[4 * i + 3]};
+                            if (!first) v += d4[i];
+                            if (!last) d4[i] = v;
 #pragma unroll
-                    for (int i = 0; i < EPL / 4; ++i) {
-#pragma unroll
-                        for (int k = 0; k < 4; ++k) acc4[i][k] += sum[4 * i + k];
-                        d4[i] = acc4[i];
+                            for (int k = 0; k < 4; ++k) sum[4 * i + k] = v[k];
+                        }
                     }
-                } else if (pl < TW * TW) {
-                    // border ring: written in full every call (zeros included) and
-                    // added by ring_merge_kernel, no atomics.  Later batches add to
-                    // it; this lane wrote the same entry in every earlier batch.
+                } else if (inwin) {
+                    // border ring: written in full every call (zeros included),
+                    // summed by ring_final_kernel, no atomics.  Later batches add
+                    // to it; this lane wrote the same entry in every earlier batch.
                     f32x4 *r4 = reinterpret_cast<f32x4 *>(
                         p.ring + ((size_t)bucket * kRing + ring_index(py, px)) * p.Cgp + cc * KC + co * EPL);
 #pragma unroll
@@ -2392,6 +2412,50 @@ __global__ __launch_bounds__(512) void dcn2_gi_gather_kernel(const BwdParams p) 
                         f32x4 v = f32x4{sum[4 * i], sum[4 * i + 1], sum[4 * i + 2], sum[4 * i + 3]};
                         if (!first) v += r4[i];
                         r4[i] = v;
+#pragma unroll
+                        for (int k = 0; k < 4; ++k) sum[4 * i + k] = v[k];
+                    }
+                }
+                // After the last batch, the pass's 8 pixels of the tile's own
+                // 16 x 16 block (window rows and columns 1 .. TS) go straight to
+                // grad_input in the caller's type and layout: the interior ones
+                // final, those on window row or column TS (tile boundary) partial,
+                // to be overwritten by ring_final_kernel.
+                if (last && seg && py >= 1) {
+                    T *const gout = (T *)p.gi_out;
+                    const int C = p.G * p.Cg, c0 = cc * KC + co * EPL;
+                    if (p.gi_nhwc) {
+                        // lane: its EPL channels of its pixel
+                        if (live && c0 < p.Cg) {
+                            T *dst = gout + (((size_t)b * p.H + Y) * p.W + X) * C + g * p.Cg + c0;
+                            if (p.gi_vec && c0 + EPL <= p.Cg) {
+                                *reinterpret_cast<uint4 *>(dst) = pack16<T>(sum);
+                            } else {
+#pragma unroll
+                                for (int e = 0; e < EPL; ++e)
+                                    if (c0 + e < p.Cg) dst[e] = from_f32<T>(sum[e]);
+                            }
+                        }
+                    } else {
+                        // transposed through this wave's LDS: lane l then holds
+                        // KC/8 consecutive pixels (from LPX) of channel l % KC
+                        *reinterpret_cast<uint4 *>(&stage[wave][ps * KC + co * EPL]) = pack16<T>(sum);
+                        constexpr int PPL = KC / 8;  // pixels per lane: 16 bytes
+                        const int cl = lane % KC, lpx = (lane / KC) * PPL;
+                        T v[PPL];
+#pragma unroll
+                        for (int e = 0; e < PPL; ++e) v[e] = stage[wave][(lpx + e) * KC + cl];
+                        const int X0 = ox + 1 + 8 * (qp & 1) + lpx, cgi = cc * KC + cl;
+                        if (Y < p.H && X0 < p.W && cgi < p.Cg) {
+                            T *dst = gout + (((size_t)b * C + g * p.Cg + cgi) * p.H + Y) * p.W + X0;
+                            if (p.gi_vec && X0 + PPL <= p.W) {
+                                *reinterpret_cast<uint4 *>(dst) = __builtin_bit_cast(uint4, v);
+                            } else {
+#pragma unroll
+                                for (int e = 0; e < PPL; ++e)
+                                    if (X0 + e < p.W) dst[e] = v[e];
+                            }
+                        }
                     }
                 }
             }
@@ -2414,11 +2478,12 @@ __global__ __launch_bounds__(512) void dcn2_gi_gather_kernel(const BwdParams p) 
 // at a time, so no two waves touch one window row at once, and within the
 // wave the four corners are added one after another (a wave's LDS operations
 // complete in order, so the neighbouring group's add to a shared pixel is
-// seen).  Then interior pixels (reachable from this tile's cells only) are
-// written to gi_acc and the one-pixel border ring, shared with the
-// neighbouring tiles, to the bucket's ring, once each, every entry every call
-// (zeros included), for ring_merge_kernel.  The reference scatters one global
-// atomic per (sample, corner, channel) (com.cu:553-609).
+// seen).  Then the one-pixel border ring, shared with the neighbouring tiles,
+// goes to the bucket's ring, every entry every call (zeros included), and the
+// tile's 16 x 16 pixels straight to grad_input in the caller's type and layout;
+// ring_final_kernel completes the tile-boundary pixels from the rings.  The
+// reference scatters one global atomic per (sample, corner, channel)
+// (com.cu:553-609).
 // Mean samples per bucket from which the host takes dcn2_gi_push_kernel.
 constexpr int kPushMinPerBucket = 1024;
 
@@ -2452,7 +2517,7 @@ __global__ __launch_bounds__(512) void dcn2_gi_push_kernel(const BwdParams p) {
     const int bg = bucket / (p.ntx * p.nty), b = bg / p.G, g = bg - b * p.G;
     const int row0 = p.bstart[bucket], count = p.bstart[bucket + 1] - row0;
     const int oy = ty * TS - 1, ox = tx * TS - 1;  // pixel of local (0, 0)
-    const int cs = p.G * p.Cgp, cpg = p.Cgp / KC;
+    const int cpg = p.Cgp / KC;
     const int co = lane % LPR, gq = lane / LPR;
     const int row_bytes = p.Cgp * (int)sizeof(R);
     const int slice = co * 16 * NLD;
@@ -2707,14 +2772,13 @@ __global__ __launch_bounds__(512) void dcn2_gi_push_kernel(const BwdParams p) {
         __syncthreads();
 
         // 3. the window: the border ring to the bucket's ring (for
-        //    ring_final_kernel / ring_merge_kernel); then either the interior
-        //    pixels to gi_acc (lane: pixel slot gq, channel slice co) or, with
-        //    gi_out, the tile's pixels (16ty .. +15, 16tx .. +15) = window
-        //    (1 .. TS, 1 .. TS) straight to grad_input in the caller's type
-        //    and layout.  Of those, the pixels on row or column TS are
-        //    partial sums here; ring_final_kernel, launched after this kernel,
-        //    overwrites every such (tile-boundary) pixel with the full sum.
-        if (p.gi_out) {
+        //    ring_final_kernel); then the tile's pixels (16ty .. +15, 16tx ..
+        //    +15) = window (1 .. TS, 1 .. TS) straight to grad_input in the
+        //    caller's type and layout.  Of those, the pixels on row or column TS
+        //    are partial sums here; ring_final_kernel, launched after this
+        //    kernel, overwrites every such (tile-boundary) pixel with the full
+        //    sum.
+        {
             for (int pl = 8 * wave + gq; pl < TW * TW; pl += 64) {
                 const int py = pl / TW, px = pl - py * TW;
                 if (py >= 1 && py <= TS - 1 && px >= 1 && px <= TS - 1) continue;
@@ -2774,79 +2838,15 @@ __global__ __launch_bounds__(512) void dcn2_gi_push_kernel(const BwdParams p) {
                     }
                 }
             }
-            continue;  // (the chunk loop's barrier orders these reads before the next clear)
-        }
-        float *__restrict__ gi = p.gi_acc + (size_t)b * p.H * p.W * cs + g * p.Cgp + cc * KC + co * EPL;
-        for (int pl = 8 * wave + gq; pl < TW * TW; pl += 64) {
-            const int py = pl / TW, px = pl - py * TW;
-            const int Y = oy + py, X = ox + px;
-            f32x4 *d4;
-            if (py >= 1 && py <= TS - 1 && px >= 1 && px <= TS - 1) {
-                if (Y >= p.H || X >= p.W) continue;  // (Y, X >= 0 here)
-                d4 = reinterpret_cast<f32x4 *>(gi + ((size_t)Y * p.W + X) * cs);
-            } else {
-                d4 = reinterpret_cast<f32x4 *>(p.ring + ((size_t)bucket * kRing + ring_index(py, px)) * p.Cgp +
-                                               cc * KC + co * EPL);
-            }
-#pragma unroll
-            for (int h = 0; h < NPC; ++h) d4[h] = *piece(pl, h);
+            // (the chunk loop's barrier orders these reads before the next clear)
         }
     }  // channel chunks
 }
 
-// ---------------------------------------------------------------------------
-// Writes the sums of the gather's border-ring partials into gi_acc (the
-// gather writes every other pixel, so gi_acc is never cleared).  The tile-boundary
-// pixels are those with (Y+1) % TS == 0 or (X+1) % TS == 0: the whole rows
-// Y = TS*k + TS-1 (nrow of them) first, then the columns X = TS*k + TS-1
-// (ncol) without those rows.  Pixel (Y, X) is (py, px) = ((Y+1) % TS,
-// (X+1) % TS) of the window of tile ((Y+1) / TS, (X+1) / TS), and also row TS
-// of the tile above when py == 0 and column TS of the tile to the left when
-// px == 0; it is on the ring of each of those windows.  One thread per pixel
-// and 4 padded channels; every pixel has exactly one thread, so the update is
-// a plain write.
-__global__ __launch_bounds__(256) void ring_merge_kernel(float *__restrict__ gi_acc,
-                                                         const float *__restrict__ ring, int H,
-                                                         int W, int cs, int Cgp, int G, int nty,
-                                                         int ntx, int nrow, int ncol) {
-    constexpr int TS = kCellTile;
-    const int q4 = cs / 4, b = blockIdx.y;
-    const long npix = (long)nrow * W + (long)(H - nrow) * ncol;
-    const long item = (long)blockIdx.x * 256 + threadIdx.x;
-    if (item >= npix * q4) return;
-    const long k = item / q4;
-    const int cp = (int)(item - k * q4) * 4;
-    int Y, X;
-    if (k < (long)nrow * W) {
-        Y = TS * (int)(k / W) + TS - 1;
-        X = (int)(k % W);
-    } else {
-        const long k2 = k - (long)nrow * W;
-        const int c = (int)(k2 / (H - nrow)), j = (int)(k2 % (H - nrow));
-        Y = j + j / (TS - 1);  // the j-th row that is not a boundary row
-        X = TS * c + TS - 1;
-    }
-    const int g = cp / Cgp, ci = cp - g * Cgp;
-    const int py = (Y + 1) % TS, ty = (Y + 1) / TS, px = (X + 1) % TS, tx = (X + 1) / TS;
-    f32x4 *dst = reinterpret_cast<f32x4 *>(gi_acc + (((size_t)b * H + Y) * W + X) * cs + cp);
-    f32x4 v = f32x4{0.0f, 0.0f, 0.0f, 0.0f};  // the gather never writes these pixels
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        if (i == 1 && (py != 0 || ty == 0)) continue;
-#pragma unroll
-        for (int jj = 0; jj < 2; ++jj) {
-            if (jj == 1 && (px != 0 || tx == 0)) continue;
-            const long bucket = (((long)b * G + g) * nty + (ty - i)) * ntx + (tx - jj);
-            v += *reinterpret_cast<const f32x4 *>(
-                ring + (bucket * kRing + ring_index(i ? TS : py, jj ? TS : px)) * Cgp + ci);
-        }
-    }
-    *dst = v;
-}
-
 // gw_acc [Mp][Kp] (K order tap, group, channel) -> grad_weight [Cout][C][kh][kw];
-// gb_acc -> grad_bias.  nblk workgroups of 256 threads; the grad_input
-// finalisation kernels run them as extra workgroups of their own launch.
+// gb_acc -> grad_bias.  nblk workgroups of 256 threads; ring_final_kernel runs
+// them as extra workgroups of its own launch (finalize_gw_kernel alone for an
+// empty batch).
 template <typename T> struct GwFinal {
     const float *gwa, *gba;
     T *gw, *gb;
@@ -3001,100 +3001,6 @@ __global__ __launch_bounds__(256) void ring_final_kernel(const BwdParams p, cons
     if (gb < f.nblk) finalize_gw_block(f, gb);
 }
 
-// gi_acc [B][HW][cs] fp32 -> grad_input [B][C][HW] T; 64 pixels x 32 padded
-// channels per block, transposed through LDS.  Loads: 8 lanes per pixel, 16
-// bytes (4 channels) each.  Stores: 8 lanes per channel row, 8 consecutive
-// pixels each (one 16-byte store for 2-byte T) when vec (HW % 8 == 0 and a
-// 16-byte aligned grad_input); otherwise one element per store.
-template <typename T>
-__global__ __launch_bounds__(256) void finalize_gi_kernel(const float *__restrict__ acc,
-                                                          T *__restrict__ gi, int C, int HW,
-                                                          int Cg, int Cgp, int cs, int vec, int B,
-                                                          const GwFinal<T> f) {
-    __shared__ float tile[64][33];
-    if ((int)blockIdx.z >= B) {  // z slices past the batch: grad_weight / grad_bias
-        const long blk = blockIdx.x + (long)gridDim.x * (blockIdx.y + (long)gridDim.y * (blockIdx.z - B));
-        if (blk < f.nblk) finalize_gw_block(f, blk);
-        return;
-    }
-    const int px0 = blockIdx.x * 64, cp0 = blockIdx.y * 32, b = blockIdx.z;
-    const int tid = threadIdx.x;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int pl = (tid >> 3) + 32 * i, c4 = (tid & 7) * 4;
-        const int px = px0 + pl;
-        f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
-        if (px < HW)  // cs % 32 == 0 and cp0 % 32 == 0: the 16-byte load stays in the pixel
-            v = *reinterpret_cast<const f32x4 *>(acc + ((size_t)b * HW + px) * cs + cp0 + c4);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) tile[pl][c4 + e] = v[e];
-    }
-    __syncthreads();
-    const int cl = tid >> 3, p8 = (tid & 7) * 8;
-    const int cp = cp0 + cl, g = cp / Cgp, ci = cp - g * Cgp;
-    if (ci >= Cg) return;
-    T *row = gi + ((size_t)b * C + g * Cg + ci) * HW + px0 + p8;
-    T v[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = (T)tile[p8 + e][cl];
-    if (vec && px0 + p8 + 8 <= HW) {
-        if constexpr (sizeof(T) == 2) {
-            *reinterpret_cast<uint4 *>(row) = __builtin_bit_cast(uint4, v);
-        } else {
-            reinterpret_cast<uint4 *>(row)[0] = make_uint4(__builtin_bit_cast(unsigned, v[0]),
-                __builtin_bit_cast(unsigned, v[1]), __builtin_bit_cast(unsigned, v[2]),
-                __builtin_bit_cast(unsigned, v[3]));
-            reinterpret_cast<uint4 *>(row)[1] = make_uint4(__builtin_bit_cast(unsigned, v[4]),
-                __builtin_bit_cast(unsigned, v[5]), __builtin_bit_cast(unsigned, v[6]),
-                __builtin_bit_cast(unsigned, v[7]));
-        }
-    } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-            if (px0 + p8 + e < HW) row[e] = v[e];
-    }
-}
-
-// gi_acc [B][HW][cs] fp32 -> channels-last grad_input [B][HW][C] T, contiguous
-// on both sides.  With vec4 (C and C/G multiples of 4, grad_input aligned to 4
-// elements) each thread moves 4 channels: one 16-byte load and one 8- or
-// 16-byte store; otherwise one element per thread.
-template <typename T>
-__global__ __launch_bounds__(256) void finalize_gi_nhwc_kernel(const float *__restrict__ acc,
-                                                               T *__restrict__ gi, long total,
-                                                               int C, int Cg, int Cgp, int cs,
-                                                               int vec4, int nmain,
-                                                               const GwFinal<T> f) {
-    if ((int)blockIdx.x >= nmain) {  // workgroups past nmain: grad_weight / grad_bias
-        finalize_gw_block(f, blockIdx.x - nmain);
-        return;
-    }
-    const long stride = (long)nmain * 256;
-    if (vec4) {
-        for (long i4 = (long)blockIdx.x * 256 + threadIdx.x; i4 < total / 4; i4 += stride) {
-            const long idx = i4 * 4;
-            const long px = idx / C;
-            const int c = (int)(idx - px * C);
-            const int g = c / Cg, ci = c - g * Cg;  // c..c+3 lie in one group
-            const f32x4 v = *reinterpret_cast<const f32x4 *>(acc + px * cs + g * Cgp + ci);
-            T o[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) o[e] = (T)v[e];
-            if constexpr (sizeof(T) == 2)
-                *reinterpret_cast<uint2 *>(gi + idx) = __builtin_bit_cast(uint2, o);
-            else
-                *reinterpret_cast<uint4 *>(gi + idx) = __builtin_bit_cast(uint4, o);
-        }
-        return;
-    }
-    for (long idx = (long)blockIdx.x * 256 + threadIdx.x; idx < total; idx += stride) {
-        const long px = idx / C;
-        const int c = (int)(idx - px * C);
-        const int g = c / Cg, ci = c - g * Cg;
-        gi[idx] = (T)acc[px * cs + g * Cgp + ci];
-    }
-}
-
 // ---------------------------------------------------------------------------
 // The fused kernel (column gradient and grad_weight in one pass) serves
 // 2-byte types with Mp of 128 or 256 (one M chunk), and images of gO and xt
@@ -3114,8 +3020,9 @@ static hipError_t backward_t(const Geo &g, const BwdParams &p0, void *grad_input
     BwdParams p = p0;
     hipError_t e;
     // (the fp32 grad_weight / grad_bias accumulators and the bucket counts
-    // were zeroed by the pack launch; gi_acc needs no clearing: the gather
-    // writes every interior pixel and ring_merge_kernel every boundary pixel)
+    // were zeroed by the pack launch; gi_acc, the per-pixel gather's partial
+    // sums between the batches of a bucket, needs no clearing: the first batch
+    // writes them)
     int dev = 0, ncu = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
@@ -3264,82 +3171,50 @@ static hipError_t backward_t(const Geo &g, const BwdParams &p0, void *grad_input
         const GatherGeo gg = gather_geometry(g);
         const int nbk = (int)gg.nbuckets;
         const int nrow = g.H / kCellTile, ncol = g.W / kCellTile;
-        const long ring_items = ((long)nrow * g.W + (long)(g.H - nrow) * ncol) * (g.cs / 4);
+        // grad_weight first (when not fused), so that its finalisation can
+        // ride in the last launch, ring_final_kernel, and before the border
+        // rings overwrite xt (they may share its bytes, see bwd_workspace)
+        if (!fused && (e = run_gradw()) != hipSuccess) return e;
+        prof_begin(DCN2_STAGE_BWD_GATHER, s);
+        // both grad_input kernels write the caller's grad_input directly (the
+        // tile-boundary pixels partially; ring_final_kernel completes them)
+        p.gi_out = grad_input;
+        p.gi_nhwc = g.nhwc;
+        const int align16 = ((uintptr_t)grad_input & 15) == 0;
+        p.gi_vec = align16 && (g.nhwc ? g.C % 8 == 0 && g.Cg % 8 == 0 : g.W % 8 == 0);
         if (gg.by_cells) {
-            // grad_weight first (when not fused), so that its finalisation can
-            // ride in the last launch, ring_final_kernel, and before the border
-            // rings overwrite xt (they may share its bytes, see bwd_workspace)
-            if (!fused && (e = run_gradw()) != hipSuccess) return e;
-            prof_begin(DCN2_STAGE_BWD_GATHER, s);
-            p.gi_out = grad_input;
-            p.gi_nhwc = g.nhwc;
-            const int align16 = ((uintptr_t)grad_input & 15) == 0;
-            p.gi_vec = align16 && (g.nhwc ? g.C % 8 == 0 && g.Cg % 8 == 0 : g.W % 8 == 0);
             dcn2_gi_push_kernel<T><<<nbk, 512, 0, s>>>(p);
-            if ((e = hipGetLastError()) != hipSuccess) return e;
-            // the tile-boundary pixels from the border rings, and grad_weight /
-            // grad_bias (see ring_final_kernel)
-            RingFinal rf;
-            rf.nrow = nrow;
-            rf.ncol = ncol;
-            rf.xblk = ceil_div(g.W, 64);
-            rf.cblk = g.cs / 32;
-            rf.nb_rows = g.nhwc ? 0 : (long)g.B * nrow * rf.xblk * rf.cblk;
-            rf.items = (long)g.B * ((g.nhwc ? (long)nrow * g.W : 0) + (long)(g.H - nrow) * ncol) *
-                       (g.cs / 4);
-            rf.nb_items = (rf.items + 255) / 256;
-            // (none in a slice before the last when the images have no
-            // tile-boundary pixels)
-            const long rblocks = rf.nb_rows + rf.nb_items + gwf.nblk;
-            if (rblocks > 0) ring_final_kernel<T><<<(unsigned)rblocks, 256, 0, s>>>(p, rf, gwf);
-            if ((e = hipGetLastError()) != hipSuccess) return e;
-            prof_end(DCN2_STAGE_BWD_GATHER, s);
         } else {
-            // grad_weight first (when not fused): it reads xt, whose bytes the
-            // border rings may share (see bwd_workspace)
-            if (!fused && (e = run_gradw()) != hipSuccess) return e;
-            prof_begin(DCN2_STAGE_BWD_GATHER, s);
-            // At most two workgroups per CU (extra LDS reserved at launch): each
-            // bucket's rows are read once per corner, and with three buckets per
-            // CU the rows in use no longer fit an XCD's L2 (measured at c2:
-            // 138 us at three per CU, 113 us at two, 119 us at one).
+            // At most two workgroups per CU (extra LDS reserved at launch when
+            // the static LDS leaves room for three): each bucket's rows are read
+            // once per corner, and with three buckets per CU the rows in use no
+            // longer fit an XCD's L2 (measured at c2: 138 us at three per CU,
+            // 113 us at two, 119 us at one).
             int lds_cu = 0;
             if (hipDeviceGetAttribute(&lds_cu, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor,
                                       dev) != hipSuccess)
                 lds_cu = 0;
             const int pad = std::max(0, lds_cu / 3 + 256 - gather_static_lds(kRowScaled<T>));
             dcn2_gi_gather_kernel<T><<<nbk, 512, pad, s>>>(p);
-            if ((e = hipGetLastError()) != hipSuccess) return e;
-            // the windows' border rings into gi_acc (tile-boundary pixels only)
-            if (ring_items > 0) {
-                dim3 rgrid((unsigned)((ring_items + 255) / 256), g.B);
-                ring_merge_kernel<<<rgrid, 256, 0, s>>>(p.gi_acc, p.ring, g.H, g.W, g.cs, g.Cgp, g.G,
-                                                        p.nty, p.ntx, nrow, ncol);
-            }
-            if ((e = hipGetLastError()) != hipSuccess) return e;
-            prof_end(DCN2_STAGE_BWD_GATHER, s);
-            // 4. grad_input to the caller's layout (and grad_weight / grad_bias)
-            prof_begin(DCN2_STAGE_BWD_FINAL, s);
-            const int HW = g.H * g.W;
-            if (g.nhwc) {
-                const long total = (long)g.B * HW * g.C;
-                const int vec4 = g.C % 4 == 0 && g.Cg % 4 == 0 &&
-                                 ((uintptr_t)grad_input % (4 * sizeof(T))) == 0;
-                const long work = vec4 ? total / 4 : total;
-                const int nmain = (int)std::min<long>((work + 255) / 256, 16384);
-                finalize_gi_nhwc_kernel<T><<<(unsigned)(nmain + gwf.nblk), 256, 0, s>>>(
-                    p.gi_acc, (T *)grad_input, total, g.C, g.Cg, g.Cgp, g.cs, vec4, nmain, gwf);
-            } else {
-                // grad_weight's workgroups in extra z slices of the same grid
-                const unsigned gx = ceil_div(HW, 64), gy = g.cs / 32;
-                const unsigned zw = (unsigned)((gwf.nblk + (long)gx * gy - 1) / ((long)gx * gy));
-                const int vec = HW % 8 == 0 && ((uintptr_t)grad_input & 15) == 0;
-                finalize_gi_kernel<T><<<dim3(gx, gy, g.B + zw), 256, 0, s>>>(
-                    p.gi_acc, (T *)grad_input, g.C, HW, g.Cg, g.Cgp, g.cs, vec, g.B, gwf);
-            }
-            if ((e = hipGetLastError()) != hipSuccess) return e;
-            prof_end(DCN2_STAGE_BWD_FINAL, s);
         }
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+        // the tile-boundary pixels from the border rings, and grad_weight /
+        // grad_bias (see ring_final_kernel)
+        RingFinal rf;
+        rf.nrow = nrow;
+        rf.ncol = ncol;
+        rf.xblk = ceil_div(g.W, 64);
+        rf.cblk = g.cs / 32;
+        rf.nb_rows = g.nhwc ? 0 : (long)g.B * nrow * rf.xblk * rf.cblk;
+        rf.items = (long)g.B * ((g.nhwc ? (long)nrow * g.W : 0) + (long)(g.H - nrow) * ncol) *
+                   (g.cs / 4);
+        rf.nb_items = (rf.items + 255) / 256;
+        // (none in a slice before the last when the images have no
+        // tile-boundary pixels)
+        const long rblocks = rf.nb_rows + rf.nb_items + gwf.nblk;
+        if (rblocks > 0) ring_final_kernel<T><<<(unsigned)rblocks, 256, 0, s>>>(p, rf, gwf);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+        prof_end(DCN2_STAGE_BWD_GATHER, s);
     } else {
         // 5. (empty batch) grad_weight / grad_bias alone
         prof_begin(DCN2_STAGE_BWD_FINAL, s);

@@ -82,9 +82,10 @@ struct GatherGeo {
     int row_scaled;  // bf16 rows carry one scale byte per 32 channels
     long nbuckets, rows;
     long batch_bytes, max_batch_bytes;
-    // grad_input by cells (dcn2_gi_push_kernel, written straight into the
-    // caller's grad_input; no fp32 accumulator in the workspace) or by pixels
-    // (dcn2_gi_gather_kernel into gi_acc, then a finalisation pass)
+    // grad_input by cells (dcn2_gi_push_kernel) or by pixels
+    // (dcn2_gi_gather_kernel, which keeps the partial sums of a bucket of
+    // several record batches in an fp32 accumulator, gi_acc); both write the
+    // caller's grad_input directly
     bool by_cells;
 };
 GatherGeo gather_geometry(const Geo &g);
