@@ -188,8 +188,8 @@ BwdWorkspace bwd_workspace(const Geo &g0) {
     w.tab = o;
     o += align256((size_t)(g.Kp / g.KC) * 16);
     const GatherGeo gg = gather_geometry(g);
-    w.gi_acc = o;  // (the by-cells grad_input writes the caller's buffer directly)
-    if (!gg.by_cells) o += align256((size_t)g.B * g.H * g.W * g.cs * sizeof(float));
+    w.gi_acc = o;  // (by pixels only: partial sums of buckets of several record batches)
+    if (!gg.by_cells) o += align256((size_t)gg.acc_bytes);
     w.gw_acc = o;
     o += align256((size_t)g.Mp * g.Kp * sizeof(float));
     w.gb_acc = o;

@@ -2184,8 +2184,14 @@ __global__ __launch_bounds__(512) void dcn2_gi_gather_kernel(const BwdParams p) 
     const int bg = bucket / (p.ntx * p.nty), b = bg / p.G, g = bg - b * p.G;
     const int row0 = p.bstart[bucket], count = p.bstart[bucket + 1] - row0;
     const int oy = ty * TS - 1, ox = tx * TS - 1;  // pixel of local (0, 0)
-    const int cs = p.G * p.Cgp, cpg = p.Cgp / KC;
-    float *__restrict__ gi = p.gi_acc + (size_t)b * p.H * p.W * cs + g * p.Cgp;
+    const int cpg = p.Cgp / KC;
+    // A bucket of several batches (count > kGatherBatch) keeps its interior
+    // pixels' partial sums between batches in its gi_acc slot
+    // [(TS-1)^2 pixels][Cgp], slot row0 / (kGatherBatch + 1): the row ranges of
+    // two such buckets start at least kGatherBatch + 1 rows apart, so no two
+    // share a slot.
+    float *__restrict__ gi =
+        p.gi_acc + (size_t)(row0 / (kGatherBatch + 1)) * (TS - 1) * (TS - 1) * p.Cgp;
 
     // one pass per batch of records; an empty bucket still takes one (with no
     // records) to write its ring
@@ -2383,15 +2389,15 @@ __global__ __launch_bounds__(512) void dcn2_gi_gather_kernel(const BwdParams p) 
                 // Interior pixels (reachable from this tile's cells only) are this
                 // block's alone.  With one batch their sums are final; with
                 // several, the batches before the last keep the partial sums in
-                // gi_acc (the first writes them, so it needs no clearing) and the
-                // last adds them back.  The accumulator's padding channels
+                // the bucket's gi_acc slot (the first writes them, so it needs
+                // no clearing) and the last adds them back.  The accumulator's padding channels
                 // (Cg..Cgp of a group) are never read back, so whole 16-byte
                 // pieces are written.
                 const bool inner = py >= 1 && py <= TS - 1 && px >= 1 && px <= TS - 1;
                 if (inner) {
                     if (live && (first || last || tot > 0)) {
                         f32x4 *d4 =
-                            reinterpret_cast<f32x4 *>(gi + ((size_t)Y * p.W + X) * cs + cc * KC + co * EPL);
+                            reinterpret_cast<f32x4 *>(gi + ((py - 1) * (TS - 1) + px - 1) * p.Cgp + cc * KC + co * EPL);
 #pragma unroll
                         for (int i = 0; i < EPL / 4; ++i) {
                             f32x4 v = f32x4{sum[4 * i], sum[4 * i + 1], sum[4 * i + 2], sum[4 * i + 3]};
@@ -3243,6 +3249,8 @@ GatherGeo gather_geometry(const Geo &g) {
     // (576 per bucket) ~118 against 73 us.
     gg.by_cells = g.opt_push >= 0 ? g.opt_push != 0
                                   : gg.rows >= (long)kPushMinPerBucket * gg.nbuckets;
+    gg.acc_bytes = gg.rows / (kGatherBatch + 1) * (long)(kCellTile - 1) * (kCellTile - 1) * g.Cgp *
+                   (long)sizeof(float);
     return gg;
 }
 

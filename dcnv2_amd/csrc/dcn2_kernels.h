@@ -87,6 +87,9 @@ struct GatherGeo {
     // several record batches in an fp32 accumulator, gi_acc); both write the
     // caller's grad_input directly
     bool by_cells;
+    // bytes of gi_acc (by pixels): one slot of interior pixels per bucket of
+    // several record batches, at most rows / (batch + 1) of them
+    long acc_bytes;
 };
 GatherGeo gather_geometry(const Geo &g);
 
