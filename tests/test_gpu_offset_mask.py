@@ -63,6 +63,9 @@ GEOMS = {
     "b2_c16_dg2_3x3": (2, 16, 12, 10, 24, 3, 1, 1, 1, 2),
     "b1_c64_s2_d2": (1, 64, 20, 18, 40, 3, 2, 2, 2, 1),
     "b2_c80_cout300": (2, 80, 9, 11, 300, 3, 1, 1, 1, 1),
+    # fused backward with two 64-channel chunks per group (the chunks' corner
+    # sums finished in a second launch, through the sigmoid of the logits)
+    "b2_c128_cout96": (2, 128, 14, 16, 96, 3, 1, 1, 1, 1),
 }
 
 
