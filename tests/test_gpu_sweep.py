@@ -113,3 +113,54 @@ def test_random_geometry_vs_oracle(c):
             assert r is None or name in ("grad_mask", "grad_bias")
             continue
         check(name, g, r, tol)
+
+
+@pytest.mark.parametrize("c", CASES[:48], ids=[_id(c) for c in CASES[:48]])
+def test_random_geometry_om_vs_oracle(c):
+    """The offset/mask entry points (the predictor's [B, 3*G*kh*kw, Ho, Wo]
+    output read directly, mask logits through the sigmoid) on the same random
+    geometries: output, grad_input, both parts of grad_om, grad_weight and
+    grad_bias against the oracle."""
+    print(_id(c), flush=True)
+    dtype = DT[c["dt"]]
+    w = CONFIGS[0].with_(B=c["B"], C=c["C"], H=c["H"], W=c["W"], Cout=c["Cout"], k=c["k"],
+                         stride=c["s"], pad=c["p"], dil=c["d"], groups=c["G"], seed=101,
+                         offset_dist=f"normal:{c['osc']}", backward=True)
+    t = make_inputs(w, dtype=dtype)
+    if c["WG"] > 1:
+        t["weight"] = t["weight"][:, : c["C"] // c["WG"]].contiguous()
+    if not c["bias"]:
+        t["bias"] = None
+    n_off = t["offset"].shape[1]
+    g = torch.Generator().manual_seed(103)
+    logits = (torch.randn(t["mask"].shape, generator=g) * 1.5).to(dtype)
+    om = torch.cat([t["offset"], logits], dim=1)
+    geo = w.geometry()
+    args = (c["s"], c["s"], c["p"], c["p"], c["d"], c["d"], c["G"])
+    x = t["input"].to(DEV)
+    if c["in_cl"]:
+        x = x.to(memory_format=torch.channels_last)
+    wt, omd = t["weight"].to(DEV), om.to(DEV)
+    b = None if t["bias"] is None else t["bias"].to(DEV)
+    go = t["grad_output"].to(DEV)
+    if c["go_cl"]:
+        go = go.to(memory_format=torch.channels_last)
+    with _C.option("bwd_fused", c["fused"]), _C.option("gi_push", c["push"]):
+        y = _C.dcn_v2_forward_om(x, wt, omd, b, *args)
+        gi, gom, gw, gb = _C.dcn_v2_backward_om(x, wt, omd, b, go, *args)
+        torch.cuda.synchronize()
+    tol = TOL[dtype]
+    o64 = om.double()
+    offset, mask = o64[:, :n_off], torch.sigmoid(o64[:, n_off:])
+    x64 = {k: None if t[k] is None else t[k].double() for k in ("input", "weight", "bias", "grad_output")}
+    check("output", y, oracle.dcn_forward(x64["input"], x64["weight"], mask, offset, x64["bias"],
+                                          pos_f32=True, **geo), tol)
+    r_gi, r_goff, r_gmask, r_gw, r_gb = oracle.dcn_backward(
+        x64["input"], x64["weight"], mask, offset, x64["bias"], x64["grad_output"], pos_f32=True, **geo)
+    m = mask.numpy()
+    check("grad_input", gi, r_gi, tol)
+    check("grad_om[offsets]", gom[:, :n_off], r_goff, tol)
+    check("grad_om[logits]", gom[:, n_off:], r_gmask * m * (1.0 - m), tol)
+    check("grad_weight", gw, r_gw, tol)
+    if gb is not None:
+        check("grad_bias", gb, r_gb, tol)
