@@ -1891,7 +1891,7 @@ void dcn2_bwd_fused_kernel(const BwdParams p) {
         if (cpg > 1) {
             // a group of several chunks: this chunk's part of the corner sums
             // goes to p.csum, summed over the group's chunks there, and
-            // dcn2_corner_finish_kernel turns the totals into grad_offset /
+            // ring_final_kernel (corner_finish) turns the totals into grad_offset /
             // grad_mask
             float *cs4 = p.csum + (((size_t)b * p.G * KK + plane) * N + (nr < N ? nr : 0)) * 4;
             if (nr < N) {
@@ -2095,13 +2095,11 @@ void dcn2_bwd_fused_kernel(const BwdParams p) {
 // csum by the fused kernel's workgroups, become the coordinate and mask
 // gradients (com.cu:431-501), with the sample position, corner validity and
 // mask value recomputed from the offsets exactly as the fused kernel's
-// sampler does.  One thread per sample (pixel n, plane g*KK + tap, image b).
+// sampler does.  One thread per sample (pixel n, plane g*KK + tap, image b),
+// run as a block range of ring_final_kernel.
 template <typename T>
-__global__ __launch_bounds__(256) void dcn2_corner_finish_kernel(const BwdParams p) {
-    const int n = blockIdx.x * 256 + threadIdx.x;
-    const int plane = blockIdx.y, b = blockIdx.z;
+__device__ __forceinline__ void corner_finish(const BwdParams &p, int n, int plane, int b) {
     const int N = p.Ho * p.Wo, KK = p.kh * p.kw;
-    if (n >= N) return;
     const int tap = plane % KK, ki = tap / p.kw, kj = tap - ki * p.kw;
     const int oy = n / p.Wo, ox = n - oy * p.Wo;
     const T *offs = (const T *)p.offset + (size_t)b * p.off_bs + (size_t)plane * 2 * N;
@@ -2890,13 +2888,15 @@ __global__ __launch_bounds__(256) void finalize_gw_kernel(const GwFinal<T> f) {
 // column); it is (py, px) = ((Y+1) % TS, (X+1) % TS) of the window of tile
 // ((Y+1) / TS, (X+1) / TS), and also row TS of the tile above when py == 0
 // and column TS of the tile to the left when px == 0.  One launch, 256
-// threads per block, three block ranges:
+// threads per block, four block ranges:
 //   [0, nb_rows)  NCHW boundary rows: 64 pixels x 32 padded channels per
 //                 block, ring sums -> LDS -> 16-byte stores of 8 pixels of
 //                 one channel (stores along pixels, as the rows are
 //                 contiguous in NCHW);
 //   then          the other boundary pixels (all of them for channels-last),
 //                 one thread per pixel and 4 padded channels;
+//   then          grad_offset / grad_mask of the fused kernel's groups of
+//                 several chunks (corner_finish), one thread per sample;
 //   then          grad_weight / grad_bias (their accumulators are complete
 //                 when this kernel runs).
 struct RingFinal {
@@ -2905,6 +2905,7 @@ struct RingFinal {
     long nb_rows;         // blocks of the NCHW row part
     long items;           // items of the per-thread part
     long nb_items;        // its blocks
+    long nb_corner;       // blocks of the fused kernel's corner-sum finish (0: none)
 };
 __device__ __forceinline__ f32x4 ring_sum(const BwdParams &p, int b, int g, int ci, int Y, int X) {
     constexpr int TS = kCellTile;
@@ -3003,7 +3004,20 @@ __global__ __launch_bounds__(256) void ring_final_kernel(const BwdParams p, cons
         }
         return;
     }
-    const long gb = blk - r.nb_rows - r.nb_items;
+    const long cb = blk - r.nb_rows - r.nb_items;
+    if (cb < r.nb_corner) {
+        // grad_offset / grad_mask of groups of several chunks (csum is complete:
+        // the fused kernel ran before the grad_input kernels)
+        const int N = p.Ho * p.Wo, planes = p.G * p.kh * p.kw;
+        const long sidx = cb * 256 + threadIdx.x;
+        if (sidx < (long)p.B * planes * N) {
+            const int n = (int)(sidx % N);
+            const long bp = sidx / N;
+            corner_finish<T>(p, n, (int)(bp % planes), (int)(bp / planes));
+        }
+        return;
+    }
+    const long gb = cb - r.nb_corner;
     if (gb < f.nblk) finalize_gw_block(f, gb);
 }
 
@@ -3052,6 +3066,7 @@ static hipError_t backward_t(const Geo &g, const BwdParams &p0, void *grad_input
     gwf.Kp = g.Kp;
     gwf.nblk = last ? (std::max<long>((long)g.Cout * g.Cw * g.KK, g.Cout) + 255) / 256 : 0;
     const bool fused = fused_bwd_shape(g) && p.go_vec;
+    long corner_blocks = 0;  // ring_final_kernel's corner-sum finish blocks
     if (g.B > 0) {
         // 2. column gradient: grad_offset, grad_mask, grad_input accumulation
         //    (and grad_weight / grad_bias when fused)
@@ -3099,12 +3114,9 @@ static hipError_t backward_t(const Geo &g, const BwdParams &p0, void *grad_input
 #undef DCN2_FUSED
                     if ((e = hipGetLastError()) != hipSuccess) return e;
                     // groups of several chunks: grad_offset / grad_mask from
-                    // the corner sums the chunks added up in csum
-                    if (cpg > 1) {
-                        dcn2_corner_finish_kernel<T>
-                            <<<dim3(ceil_div(g.N, 256), g.G * g.KK, g.B), 256, 0, s>>>(pf);
-                        if ((e = hipGetLastError()) != hipSuccess) return e;
-                    }
+                    // the corner sums the chunks added up in csum, finished by
+                    // ring_final_kernel
+                    corner_blocks = cpg > 1 ? ((long)g.B * g.G * g.KK * g.N + 255) / 256 : 0;
                 }
             }
         }
@@ -3215,9 +3227,10 @@ static hipError_t backward_t(const Geo &g, const BwdParams &p0, void *grad_input
         rf.items = (long)g.B * ((g.nhwc ? (long)nrow * g.W : 0) + (long)(g.H - nrow) * ncol) *
                    (g.cs / 4);
         rf.nb_items = (rf.items + 255) / 256;
+        rf.nb_corner = corner_blocks;
         // (none in a slice before the last when the images have no
-        // tile-boundary pixels)
-        const long rblocks = rf.nb_rows + rf.nb_items + gwf.nblk;
+        // tile-boundary pixels and no corner sums to finish)
+        const long rblocks = rf.nb_rows + rf.nb_items + rf.nb_corner + gwf.nblk;
         if (rblocks > 0) ring_final_kernel<T><<<(unsigned)rblocks, 256, 0, s>>>(p, rf, gwf);
         if ((e = hipGetLastError()) != hipSuccess) return e;
         prof_end(DCN2_STAGE_BWD_GATHER, s);
