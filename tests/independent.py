@@ -8,7 +8,8 @@ contraction is a matmul, and every gradient comes from torch autograd.  At
 samples exactly on an integer coordinate the one-sided floor derivative of
 grid_sample equals torchvision's ``get_coordinate_weight``; the normalisation
 round trip can move such points by one ulp, so comparisons against this module
-use continuous random offsets.
+use continuous random offsets, except on images whose H - 1 and W - 1 are
+powers of two, where the round trip is exact.
 """
 from __future__ import annotations
 

@@ -353,6 +353,43 @@ def test_weight_groups_match_independent_formulation(geom):
         assert rel_err(a, r) < 1e-10, name
 
 
+@pytest.mark.parametrize("geom", [
+    # B, C, H, W, Co, kh, kw, s, p, d, G: H - 1 and W - 1 powers of two
+    (2, 6, 17, 17, 5, 3, 3, 1, 1, 1, 2),
+    (1, 4, 9, 17, 3, 3, 2, 2, 1, 2, 1),
+    (1, 3, 5, 9, 2, 5, 5, 1, 2, 1, 1),
+])
+def test_integer_coordinates_match_grid_sample(geom):
+    """Samples exactly on integer coordinates, the tie points of the bilinear
+    weights where the coordinate gradient is one-sided: the oracle against the
+    grid_sample formulation on images whose H - 1 and W - 1 are powers of two,
+    so that grid_sample's align_corners normalisation maps every integer
+    position to itself exactly.  grid_sample takes the floor-side difference
+    there, as torchvision's get_coordinate_weight does, at y = -1 and x = -1
+    too; there the reference's early exit (com.cu:392-396, ref_boundary=True)
+    gives 0 instead, which this comparison tells apart.  A left-side rule (the
+    positions nudged below the integers) misses by O(1)."""
+    from independent import forward_backward_gs, sample_positions
+    B, C, H, W, Co, kh, kw, s, p, d, G = geom
+    t, geo = rand_case(*geom, seed=11)
+    g = torch.Generator().manual_seed(12)
+    t["offset"] = torch.randint(-4, 5, t["offset"].shape, generator=g).to(f64)
+    out, *ref = forward_backward_gs(t["input"], t["weight"], t["offset"], t["mask"], t["bias"],
+                                    t["grad_output"], **geo)
+    Ho, Wo = out.shape[-2:]
+    y, x = sample_positions(t["offset"], kh, kw, Ho, Wo, s, p, d, G)
+    assert bool(((y == y.round()) & (x == x.round())).all())
+    assert bool(((y == -1) | (x == -1)).any())  # boundary ties occur
+    assert rel_err(fwd(t, geo), out) < 1e-13
+    for name, a, r in zip(GRADS, bwd(t, geo), ref):
+        assert rel_err(a, r) < 1e-12, name
+    goff_ref_rule = bwd(t, geo, ref_boundary=True)[1]
+    assert rel_err(goff_ref_rule, ref[1]) > 1e-3
+    left = forward_backward_gs(t["input"], t["weight"], t["offset"] - 1e-9, t["mask"], t["bias"],
+                               t["grad_output"], **geo)[2]
+    assert rel_err(bwd(t, geo)[1], left) > 1e-2
+
+
 def test_weight_groups_are_block_diagonal():
     """A grouped weight equals the full weight that is zero outside each output
     channel's group (forward and grad_input), and its grad_weight is that full
