@@ -104,10 +104,82 @@ def _stage_avgs(_C, names):
     return out
 
 
+COPY_MIB = 512  # calibration copy of the PMC passes
+
+
+def _pmc_pass(counter, workdir, timeout_s):
+    """One ``rocprofv3 --pmc <counter>`` run of ``bench.py --mode fwd`` (c1
+    forward loops after one plain device copy of COPY_MIB MiB) as a child
+    process.  Returns {kernel name: [counter value per dispatch, KiB]}, or a
+    string saying why there is none."""
+    import csv
+    import glob
+    import shutil
+    import subprocess
+    prof = shutil.which("rocprofv3")
+    if not prof:
+        return "rocprofv3 not found"
+    d = os.path.join(workdir, counter)
+    cmd = [prof, "--pmc", counter, "--output-format", "csv", "-d", d, "-o", "p", "--",
+           sys.executable, os.path.join(ROOT, "bench.py"), "--mode", "fwd", "--steps", "3",
+           "--warmup", "2", "--settle-ms", "0", "--copy-mib", str(COPY_MIB), "--no-cpu"]
+    try:
+        # (the profiler may exit non-zero after the program ends with its
+        # results complete; the csv decides)
+        subprocess.run(cmd, cwd=ROOT, env=dict(os.environ, TMPDIR="/tmp"), stdout=subprocess.DEVNULL,
+                       stderr=subprocess.DEVNULL, timeout=timeout_s)
+    except subprocess.TimeoutExpired:
+        return f"the {counter} pass did not finish in {timeout_s} s"
+    except OSError as e:
+        return f"the {counter} pass did not start: {e}"
+    paths = glob.glob(os.path.join(d, "**", "p_counter_collection.csv"), recursive=True)
+    if not paths:
+        return f"the {counter} pass wrote no counter file"
+    per = {}
+    with open(paths[0]) as f:
+        for r in csv.DictReader(f):
+            if r.get("Counter_Name") != counter:
+                continue
+            key = (r["Kernel_Name"], int(r["Dispatch_Id"]))
+            per[key] = per.get(key, 0.0) + float(r["Counter_Value"])
+    out = {}
+    for (name, _), v in per.items():
+        out.setdefault(name, []).append(v)
+    return out
+
+
+def _live_traffic(timeout_s=180):
+    """HBM bytes per launch of the c1 forward kernel, measured by this run: a
+    FETCH_SIZE and a WRITE_SIZE pass (rocprofv3 --pmc, each its own child
+    process, run before this process touches the GPU), each reading scaled by
+    what the same counter reads for a plain device copy of known size in the
+    same pass.  Returns (bytes or None, detail dict)."""
+    import statistics
+    import tempfile
+    detail = {}
+    total = 0.0
+    with tempfile.TemporaryDirectory(prefix="dcn2_pmc_", dir="/tmp") as tmp:
+        for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+            per = _pmc_pass(counter, tmp, timeout_s)
+            if isinstance(per, str):
+                return None, {"error": per}
+            copy = [v for n, vs in per.items() if "copyBuffer" in n for v in vs]
+            kern = [v for n, vs in per.items() if "dcn2_fwd_rw_kernel" in n for v in vs]
+            if not copy or not kern or max(copy) <= 0:
+                return None, {"error": f"the {counter} pass holds no copy or no forward kernel dispatch"}
+            factor = COPY_MIB * 1024.0 / max(copy)  # KiB the copy moves / KiB the counter reads
+            kib = statistics.median(kern)
+            detail[counter] = {"kib_per_launch": round(kib, 1), "copy_factor": round(factor, 4),
+                               "dispatches": len(kern)}
+            total += kib * factor * 1024.0
+    return int(total), detail
+
+
 def _traffic():
     """HBM bytes per launch of the forward kernel, from the two rocprofv3 PMC
     passes (FETCH_SIZE, WRITE_SIZE) summarised in
-    profiles/fwd_kernel_traffic_c1.md (its ``hbm_bytes_per_launch:`` line)."""
+    profiles/fwd_kernel_traffic_c1.md (its ``hbm_bytes_per_launch:`` line);
+    the fallback when the bench cannot run the passes itself."""
     path = os.path.join(ROOT, "profiles", "fwd_kernel_traffic_c1.md")
     try:
         with open(path) as f:
@@ -229,11 +301,19 @@ def main():
     ap.add_argument("--copy-mib", type=int, default=0)
     ap.add_argument("--bwd-slice-mib", type=int, default=0,
                     help="backward workspace budget per slice of images (0: library default)")
+    ap.add_argument("--no-live-traffic", action="store_true",
+                    help="take roofline.traffic from the committed profile instead of measuring it")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU; the batch-sharded multi-GPU path is "
               "a design only and is not benchmarked (run with --gpus 1)", file=sys.stderr)
         sys.exit(2)
+
+    # HBM traffic of the forward kernel: the PMC passes run as child processes
+    # first, while this process has not touched the GPU yet
+    live_traffic, traffic_detail = (None, {"error": "not measured (--no-live-traffic)"})
+    if args.mode == "full" and not args.no_live_traffic:
+        live_traffic, traffic_detail = _live_traffic()
 
     import torch
 
@@ -336,9 +416,15 @@ def main():
             "peak": PEAK_FP16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_FP16_TFLOPS, 4),
-            "traffic": _traffic(),
-            "traffic_source": "profiles/fwd_kernel_traffic_c1.md: rocprofv3 FETCH_SIZE + WRITE_SIZE "
-                              "passes of this kernel, calibrated against a copy of known size",
+            "traffic": live_traffic if live_traffic is not None else _traffic(),
+            "traffic_source": (
+                "measured by this run: rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE, each over "
+                "bench.py --mode fwd in a child process, median per dispatch of this kernel scaled "
+                f"by the counter's reading for a {COPY_MIB} MiB device copy in the same pass"
+                if live_traffic is not None else
+                "profiles/fwd_kernel_traffic_c1.md: rocprofv3 FETCH_SIZE + WRITE_SIZE passes of this "
+                "kernel, calibrated against a copy of known size (" + traffic_detail["error"] + ")"),
+            "traffic_detail": traffic_detail,
             "algorithmic_flops_per_launch": c1.gemm_flops(),
             "kernel_ms": round(kern_ms, 5),
         },
