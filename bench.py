@@ -312,7 +312,11 @@ def main():
     # HBM traffic of the forward kernel: the PMC passes run as child processes
     # first, while this process has not touched the GPU yet
     live_traffic, traffic_detail = (None, {"error": "not measured (--no-live-traffic)"})
-    if args.mode == "full" and not args.no_live_traffic:
+    under_profiler = any(k.startswith("ROCPROF_") for k in os.environ) or \
+        "rocprofiler" in os.environ.get("LD_PRELOAD", "")
+    if under_profiler:
+        traffic_detail = {"error": "not measured: this run is itself under a profiler"}
+    elif args.mode == "full" and not args.no_live_traffic:
         live_traffic, traffic_detail = _live_traffic()
 
     import torch
