@@ -56,6 +56,8 @@ def _draw(rng):
             break
         if H <= 5 and W <= 5:
             B, Cout = 1, max(8, Cout // 2)
+            if Ho < 1 or Wo < 1:  # the dilated kernel overhangs the smallest image
+                p += 1
         H, W = max(5, H * 3 // 4), max(5, W * 3 // 4)
     return dict(dt=dt, B=B, C=C, G=G, WG=WG, Cout=Cout, H=H, W=W, k=k, s=s, p=p, d=d,
                 osc=rng.choice([0.5, 2.0, 5.0]), mask=rng.random() < 0.8, bias=rng.random() < 0.8,
