@@ -148,7 +148,7 @@ def _pmc_pass(counter, workdir, timeout_s):
     return out
 
 
-def _live_traffic(timeout_s=180):
+def _live_traffic(timeout_s=100):
     """HBM bytes per launch of the c1 forward kernel, measured by this run: a
     FETCH_SIZE and a WRITE_SIZE pass (rocprofv3 --pmc, each its own child
     process, run before this process touches the GPU), each reading scaled by
@@ -160,6 +160,8 @@ def _live_traffic(timeout_s=180):
     total = 0.0
     with tempfile.TemporaryDirectory(prefix="dcn2_pmc_", dir="/tmp") as tmp:
         for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+            print(f"bench.py: rocprofv3 --pmc {counter} pass over the c1 forward (traffic of its kernel)",
+                  file=sys.stderr, flush=True)
             per = _pmc_pass(counter, tmp, timeout_s)
             if isinstance(per, str):
                 return None, {"error": per}
